@@ -1,0 +1,160 @@
+// extern "C" entry points of libmq.so (declared in include/mq.h): argument validation, error
+// reporting and dispatch to the kernel launchers. Nothing here allocates device memory.
+#include "../../include/mq.h"
+
+#include <cstdarg>
+#include <cstring>
+
+#include "mq_internal.h"
+
+namespace mq {
+
+namespace {
+thread_local char g_err[512] = "";
+
+bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+}  // namespace
+
+void set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+void clear_error() { g_err[0] = '\0'; }
+
+int launch_status(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("%s: kernel launch failed: %s", what, hipGetErrorString(e));
+        return MQ_ELAUNCH;
+    }
+    return MQ_OK;
+}
+
+namespace {
+
+#define MQ_REQUIRE(cond, ...)        \
+    do {                             \
+        if (!(cond)) {               \
+            set_error(__VA_ARGS__);  \
+            return MQ_EINVAL;        \
+        }                            \
+    } while (0)
+
+int check_gemm_common(const int8_t* qa, int64_t lda, const void* qw, int64_t ldw, int64_t M, int64_t N,
+                      int64_t K, int64_t wbytes_per_row) {
+    MQ_REQUIRE(M >= 0 && N >= 0 && K > 0, "gemm: bad shape M=%lld N=%lld K=%lld", (long long)M,
+               (long long)N, (long long)K);
+    MQ_REQUIRE(K % 64 == 0, "gemm: K=%lld must be a multiple of 64", (long long)K);
+    MQ_REQUIRE(M <= (int64_t(1) << 31) - 256 && N <= (int64_t(1) << 31) - 256, "gemm: M or N too large");
+    MQ_REQUIRE(qa && qw, "gemm: null operand");
+    MQ_REQUIRE(lda >= K && lda % 16 == 0 && aligned(qa, 16), "gemm: qa needs lda >= K, lda %% 16 == 0 and a 16-byte aligned base");
+    MQ_REQUIRE(ldw >= wbytes_per_row && ldw % 16 == 0 && aligned(qw, 16),
+               "gemm: qw needs ldw >= %lld bytes, ldw %% 16 == 0 and a 16-byte aligned base", (long long)wbytes_per_row);
+    return MQ_OK;
+}
+
+}  // namespace
+}  // namespace mq
+
+using namespace mq;
+
+extern "C" {
+
+int mq_abi_version(void) { return MQ_ABI_VERSION; }
+
+const char* mq_last_error(void) { return g_err; }
+
+int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits, int packed, void* q,
+                int64_t ldq, float* scale, void* stream) {
+    clear_error();
+    MQ_REQUIRE(M >= 0 && K > 0, "rotquant: bad shape M=%lld K=%lld", (long long)M, (long long)K);
+    MQ_REQUIRE(M < (int64_t(1) << 31), "rotquant: M too large");
+    MQ_REQUIRE(bits == 8 || bits == 4, "rotquant: bits must be 8 or 4 (got %d)", bits);
+    MQ_REQUIRE(packed == 0 || bits == 4, "rotquant: packed output needs bits = 4");
+    MQ_REQUIRE(hblock == 0 || hblock == 16 || hblock == 64 || hblock == 256,
+               "rotquant: convrot group size must be 16, 64 or 256 (got %d)", hblock);
+    MQ_REQUIRE(K % 16 == 0, "rotquant: K=%lld must be a multiple of 16", (long long)K);
+    MQ_REQUIRE(hblock == 0 || K % hblock == 0, "rotquant: K=%lld is not a multiple of the group size %d",
+               (long long)K, hblock);
+    if (K > 16384) {
+        set_error("rotquant: K=%lld exceeds 16384", (long long)K);
+        return MQ_EUNSUPPORTED;
+    }
+    if (M == 0) return MQ_OK;
+    MQ_REQUIRE(x && q && scale, "rotquant: null pointer");
+    MQ_REQUIRE(ldx >= K && ldx % 8 == 0 && aligned(x, 16), "rotquant: x needs ldx >= K, ldx %% 8 == 0, 16-byte aligned base");
+    const int64_t row_bytes = packed ? K / 2 : K;
+    const int64_t qalign = packed ? 8 : 16;
+    MQ_REQUIRE(ldq >= row_bytes && ldq % qalign == 0 && aligned(q, qalign),
+               "rotquant: q needs ldq >= %lld bytes, ldq %% %lld == 0 and an aligned base", (long long)row_bytes,
+               (long long)qalign);
+    MQ_REQUIRE(aligned(scale, 4), "rotquant: scale must be 4-byte aligned");
+    return launch_rotquant(static_cast<const uint16_t*>(x), M, K, ldx, hblock, bits, packed, q, ldq, scale,
+                           static_cast<hipStream_t>(stream));
+}
+
+int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
+                     const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group,
+                     const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                     void* stream) {
+    clear_error();
+    MQ_REQUIRE(group == 64, "gemm_w4_group: quant group size must be 64 (got %d)", group);
+    int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, K / 2);
+    if (rc) return rc;
+    MQ_REQUIRE(sa && ws && y, "gemm_w4_group: null pointer");
+    MQ_REQUIRE(ldws >= K / group, "gemm_w4_group: ldws < K/group");
+    MQ_REQUIRE(!wz || ldwz >= (K / group + 1) / 2, "gemm_w4_group: ldwz < ceil(K/group/2)");
+    MQ_REQUIRE(ldy >= N, "gemm_w4_group: ldy < N");
+    GemmArgs a{};
+    a.qa = qa; a.lda = lda; a.sa = sa; a.qw = qw; a.ldw = ldw; a.ws16 = ws; a.ldws = ldws;
+    a.wz = wz; a.ldwz = ldwz; a.bias = bias; a.y = y; a.ldy = ldy; a.M = M; a.N = N; a.K = K;
+    return launch_gemm(a, wz ? WKind::U4Asym : WKind::I4Sym, Epi::GroupScale, static_cast<hipStream_t>(stream));
+}
+
+int mq_gemm_w4_group_partials(const int8_t* qa, int64_t lda, const uint8_t* qw, int64_t ldw, const uint8_t* wz,
+                              int64_t ldwz, int group, int32_t* part, int64_t M, int64_t N, int64_t K,
+                              void* stream) {
+    clear_error();
+    MQ_REQUIRE(group == 64, "gemm_w4_group_partials: quant group size must be 64 (got %d)", group);
+    int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, K / 2);
+    if (rc) return rc;
+    MQ_REQUIRE(part, "gemm_w4_group_partials: null pointer");
+    MQ_REQUIRE(!wz || ldwz >= (K / group + 1) / 2, "gemm_w4_group_partials: ldwz < ceil(K/group/2)");
+    GemmArgs a{};
+    a.qa = qa; a.lda = lda; a.qw = qw; a.ldw = ldw; a.wz = wz; a.ldwz = ldwz; a.part = part;
+    a.M = M; a.N = N; a.K = K;
+    return launch_gemm(a, wz ? WKind::U4Asym : WKind::I4Sym, Epi::GroupPartials, static_cast<hipStream_t>(stream));
+}
+
+int mq_gemm_rowscale(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw, int wbits,
+                     const float* ws, const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N,
+                     int64_t K, void* stream) {
+    clear_error();
+    MQ_REQUIRE(wbits == 4 || wbits == 8, "gemm_rowscale: wbits must be 4 or 8 (got %d)", wbits);
+    int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, wbits == 4 ? K / 2 : K);
+    if (rc) return rc;
+    MQ_REQUIRE(sa && ws && y, "gemm_rowscale: null pointer");
+    MQ_REQUIRE(ldy >= N, "gemm_rowscale: ldy < N");
+    GemmArgs a{};
+    a.qa = qa; a.lda = lda; a.sa = sa; a.qw = static_cast<const uint8_t*>(qw); a.ldw = ldw; a.ws32 = ws;
+    a.bias = bias; a.y = y; a.ldy = ldy; a.M = M; a.N = N; a.K = K;
+    return launch_gemm(a, wbits == 4 ? WKind::I4Sym : WKind::I8, Epi::RowScale, static_cast<hipStream_t>(stream));
+}
+
+int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t ldw, int wbits, int32_t* acc,
+                         int64_t M, int64_t N, int64_t K, void* stream) {
+    clear_error();
+    MQ_REQUIRE(wbits == 4 || wbits == 8, "gemm_rowscale_acc: wbits must be 4 or 8 (got %d)", wbits);
+    int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, wbits == 4 ? K / 2 : K);
+    if (rc) return rc;
+    MQ_REQUIRE(acc, "gemm_rowscale_acc: null pointer");
+    GemmArgs a{};
+    a.qa = qa; a.lda = lda; a.qw = static_cast<const uint8_t*>(qw); a.ldw = ldw; a.part = acc;
+    a.M = M; a.N = N; a.K = K;
+    return launch_gemm(a, wbits == 4 ? WKind::I4Sym : WKind::I8, Epi::RowAcc, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,51 @@
+// Device helpers for gfx950 (CDNA4): bf16 bit conversions, DPP lane exchanges, magic rounding.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace mq {
+
+// 1.5 * 2^23: fma(v, r, kMagic) rounds v*r to the nearest integer n (ties to even) and leaves
+// n in the low mantissa bits, for |v*r| < 2^22. bits(kMagic + n) = 0x4B400000 + n.
+constexpr float kMagic = 12582912.0f;
+
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// float -> bf16 bits, round to nearest even (finite values).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// v_mov_b32 with a DPP source: every lane reads `src` from the lane the control selects.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float src) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(src), CTRL, 0xf, 0xf, true));
+}
+
+// DPP move restricted to the banks in BANK_MASK (4-lane groups of each 16-lane row); lanes in
+// other banks keep `old`.
+template <int CTRL, int BANK_MASK>
+__device__ __forceinline__ float dpp_upd(float old, float src) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(src), CTRL, 0xf, BANK_MASK, false));
+}
+
+// DPP controls (GFX9 encoding).
+constexpr int kQuadPerm0022 = 0xA0;   // lane <- lane & ~1 within the quad
+constexpr int kQuadPerm1133 = 0xF5;   // lane <- lane | 1
+constexpr int kQuadPerm0101 = 0x44;   // lane <- lane & ~2
+constexpr int kQuadPerm2323 = 0xEE;   // lane <- lane | 2
+constexpr int kRowShl4 = 0x104;       // lane <- lane + 4 (within a row of 16)
+constexpr int kRowShl8 = 0x108;
+constexpr int kRowShr4 = 0x114;       // lane <- lane - 4
+constexpr int kRowShr8 = 0x118;
+
+}  // namespace mq

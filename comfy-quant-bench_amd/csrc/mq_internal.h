@@ -1,0 +1,47 @@
+// Internal declarations shared by the libmq translation units (not part of the C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+namespace mq {
+
+// Thread-local error message behind mq_last_error().
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+// Translates the HIP launch status into the ABI status and message.
+int launch_status(const char* what);
+
+// --- rotate + quantize (mq_rotquant.hip)
+int launch_rotquant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits,
+                    int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
+
+// --- GEMMs (mq_gemm.hip)
+enum class WKind : int { U4Asym = 0, I4Sym = 1, I8 = 2 };
+enum class Epi : int { GroupScale = 0, GroupPartials = 1, RowScale = 2, RowAcc = 3 };
+
+struct GemmArgs {
+    const int8_t* qa;
+    int64_t lda;
+    const float* sa;
+    const uint8_t* qw;
+    int64_t ldw;
+    const uint16_t* ws16;   // per-group fp16 scales [N, ldws]
+    int64_t ldws;
+    const float* ws32;      // per-row fp32 scales [N]
+    const uint8_t* wz;      // packed u4 zero-points [N, ldwz]
+    int64_t ldwz;
+    const uint16_t* bias;   // bf16 [N] or null
+    uint16_t* y;            // bf16 [M, ldy]
+    int64_t ldy;
+    int32_t* part;          // int32 partials / accumulators
+    int64_t M, N, K;
+};
+
+int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream);
+
+}  // namespace mq

@@ -1,0 +1,79 @@
+"""ctypes binding of libmq.so (C ABI in include/mq.h).
+
+The library is loaded after `import torch`, so its `libamdhip64.so.7` dependency resolves to the
+HIP runtime torch already mapped: device pointers, streams and the kernels share one runtime.
+There is no fallback: if the library is missing, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must be imported before the library is loaded)
+
+ABI_VERSION = 1
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmq.so")
+
+_lib = None
+
+c_i64 = ctypes.c_int64
+c_int = ctypes.c_int
+c_vp = ctypes.c_void_p
+
+_SIGNATURES = {
+    "mq_abi_version": ([], c_int),
+    "mq_last_error": ([], ctypes.c_char_p),
+    "mq_rotquant": ([c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_vp], c_int),
+    "mq_gemm_w4_group": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_vp, c_i64,
+                          c_i64, c_i64, c_i64, c_vp], c_int),
+    "mq_gemm_w4_group_partials": ([c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_vp],
+                                  c_int),
+    "mq_gemm_rowscale": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp],
+                         c_int),
+    "mq_gemm_rowscale_acc": ([c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_vp], c_int),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+
+class MQError(RuntimeError):
+    """A libmq entry point returned a failure status."""
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built: run `python comfy-quant-bench_amd/build.py` "
+                           "(or __graft_entry__.build()) first; there is no CPU fallback")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (argtypes, restype) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
+    ver = lib.mq_abi_version()
+    if ver != ABI_VERSION:
+        raise RuntimeError(f"libmq ABI version {ver}, expected {ABI_VERSION}: rebuild the library")
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.mq_last_error().decode(errors="replace")
+        if rc == -1:
+            raise ValueError(f"{name}: {msg}")
+        raise MQError(f"{name} failed ({rc}): {msg}")
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None for a missing optional operand)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream

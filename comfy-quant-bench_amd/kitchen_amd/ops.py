@@ -1,0 +1,221 @@
+"""Online ops with comfy-kitchen's call surface, executed by libmq.so on the current HIP stream.
+
+Names, keyword arguments and error messages follow the reference's contract:
+  convrot_w4a4_linear(x, qweight, wscales, bias=None, convrot_groupsize=256, quant_group_size=64,
+                      linear_dtype="int4", input_act=None)
+      compile_support.py:84-113; patches/comfy_kitchen_swiglu_w4a4_fused.patch:41-67
+  w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook, correction, bias, group_size,
+                   convrot_groupsize, out_dtype)
+      kwargs pinned at tools/test_verify_formats.py:375-383
+  int8_linear(x, weight, weight_scale, bias, out_dtype, convrot, convrot_groupsize, input_act)
+      tools/verify_w4a4.py:342-370
+  quantize_int4_rowwise_convrot64(x, convrot_groupsize) -> (qact int8 [M, K/2], x_scale f32 [M])
+      patches/comfy_kitchen_swiglu_w4a4_fused.patch:37
+Every op is a thin host wrapper: the caller's tensors are validated, outputs are allocated with
+torch on the input's device, and the HIP kernels run asynchronously on the current stream.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+INT4_GROUP_SIZE = 64
+CONVROT_GROUPSIZES = (16, 64, 256)
+
+
+def _as_bf16_2d(x: torch.Tensor, k: int) -> torch.Tensor:
+    if not x.is_cuda:
+        raise ValueError("kitchen_amd ops run on the GPU: x must be a device tensor")
+    x2 = x.reshape(-1, k)
+    if x2.dtype != torch.bfloat16:
+        x2 = x2.to(torch.bfloat16)
+    return x2.contiguous()
+
+
+def _bias_bf16(bias, n: int, device):
+    if bias is None:
+        return None
+    if bias.numel() != n:
+        raise ValueError(f"bias has {bias.numel()} elements, expected {n}")
+    return bias.to(device=device, dtype=torch.bfloat16).contiguous()
+
+
+def _finish(y: torch.Tensor, x: torch.Tensor, n: int, out_dtype) -> torch.Tensor:
+    y = y.reshape(*x.shape[:-1], n)
+    if out_dtype is not None and out_dtype != torch.bfloat16:
+        y = y.to(out_dtype)
+    return y
+
+
+# --------------------------------------------------------------------------- activation quantizers
+
+def rotate_quantize(x: torch.Tensor, convrot_groupsize: int | None, bits: int, packed: bool = False):
+    """Rotate x [.., K] by H_cg per block and quantize per token to int8 (bits 8) or int4 (bits 4).
+
+    Returns (q, scale): q int8 [M, K] (one code per byte) or int8 [M, K/2] (packed int4),
+    scale float32 [M]."""
+    k = x.shape[-1]
+    x2 = _as_bf16_2d(x, k)
+    m = x2.shape[0]
+    q = torch.empty((m, k // 2 if packed else k), dtype=torch.int8, device=x2.device)
+    s = torch.empty((m,), dtype=torch.float32, device=x2.device)
+    _lib.call("mq_rotquant", x2.data_ptr(), m, k, k, int(convrot_groupsize or 0), int(bits), int(packed),
+              q.data_ptr(), q.stride(0), s.data_ptr(), _lib.stream_of(x2))
+    return q, s
+
+
+def quantize_int4_rowwise_convrot64(x: torch.Tensor, convrot_groupsize: int = 256):
+    """comfy-kitchen's activation quantizer: (qact int8 [M, K/2] packed int4, x_scale f32 [M])."""
+    return rotate_quantize(x, convrot_groupsize, 4, packed=True)
+
+
+def quantize_int8_rowwise_convrot(x: torch.Tensor, convrot_groupsize: int | None = 256):
+    """int8 sibling used inside w4a8_int8_linear / int8_linear: (q int8 [M, K], scale f32 [M])."""
+    return rotate_quantize(x, convrot_groupsize, 8)
+
+
+# --------------------------------------------------------------------------- GEMMs
+
+def _check_w4_group(qa, qweight, wscales, wzeros, n, group_size):
+    """Buffer-size checks the C ABI cannot do (it sees raw pointers)."""
+    m, k = qa.shape
+    if qa.dtype != torch.int8 or qweight.shape != (n, k // 2) or qweight.element_size() != 1:
+        raise ValueError(f"qa must be int8 [M, K] and qweight 8-bit [{n}, {k // 2}]")
+    groups = k // group_size
+    if wscales is not None and (wscales.dtype != torch.float16 or wscales.shape[0] != n
+                                or wscales.shape[1] < groups or wscales.stride(1) != 1):
+        raise ValueError(f"wscales must be float16 [{n}, {groups}] with unit column stride")
+    if wzeros is not None and (wzeros.element_size() != 1 or wzeros.shape[0] != n
+                               or wzeros.shape[1] < (groups + 1) // 2 or wzeros.stride(1) != 1):
+        raise ValueError(f"zero-points must be packed uint4 [{n}, {(groups + 1) // 2}]")
+
+
+def gemm_w4_group(qa, sa, qweight, wscales, wzeros, bias, n: int, group_size: int = INT4_GROUP_SIZE):
+    """y bf16 [M, N] = sa * sum_g wscales[:, g] * P_g + bias with P_g exact int32 group partials."""
+    m, k = qa.shape
+    _check_w4_group(qa, qweight, wscales, wzeros, n, group_size)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=qa.device)
+    ldwz = wzeros.stride(0) if wzeros is not None else 0
+    _lib.call("mq_gemm_w4_group", qa.data_ptr(), qa.stride(0), sa.data_ptr(), qweight.data_ptr(),
+              qweight.stride(0), wscales.data_ptr(), wscales.stride(0), _lib.ptr(wzeros), ldwz, int(group_size),
+              _lib.ptr(bias), y.data_ptr(), y.stride(0), m, n, k, _lib.stream_of(qa))
+    return y
+
+
+def gemm_w4_group_partials(qa, qweight, wzeros, n: int, group_size: int = INT4_GROUP_SIZE):
+    """Parity entry: exact int32 partials P [K/G, M, N] of gemm_w4_group."""
+    m, k = qa.shape
+    _check_w4_group(qa, qweight, None, wzeros, n, group_size)
+    part = torch.empty((k // group_size, m, n), dtype=torch.int32, device=qa.device)
+    ldwz = wzeros.stride(0) if wzeros is not None else 0
+    _lib.call("mq_gemm_w4_group_partials", qa.data_ptr(), qa.stride(0), qweight.data_ptr(), qweight.stride(0),
+              _lib.ptr(wzeros), ldwz, int(group_size), part.data_ptr(), m, n, k, _lib.stream_of(qa))
+    return part
+
+
+def gemm_rowscale(qa, sa, qweight, wscales, bias, n: int, wbits: int):
+    """y bf16 [M, N] = (qa . w^T) * sa[m] * wscales[n] + bias, full-K int32 accumulator."""
+    m, k = qa.shape
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=qa.device)
+    _lib.call("mq_gemm_rowscale", qa.data_ptr(), qa.stride(0), sa.data_ptr(), qweight.data_ptr(),
+              qweight.stride(0), int(wbits), wscales.data_ptr(), _lib.ptr(bias), y.data_ptr(), y.stride(0),
+              m, n, k, _lib.stream_of(qa))
+    return y
+
+
+def gemm_rowscale_acc(qa, qweight, n: int, wbits: int):
+    """Parity entry: the full-K int32 accumulator [M, N] of gemm_rowscale."""
+    m, k = qa.shape
+    acc = torch.empty((m, n), dtype=torch.int32, device=qa.device)
+    _lib.call("mq_gemm_rowscale_acc", qa.data_ptr(), qa.stride(0), qweight.data_ptr(), qweight.stride(0),
+              int(wbits), acc.data_ptr(), m, n, k, _lib.stream_of(qa))
+    return acc
+
+
+# --------------------------------------------------------------------------- linears
+
+def convrot_w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.Tensor, bias=None,
+                        convrot_groupsize: int = 256, quant_group_size: int = INT4_GROUP_SIZE,
+                        linear_dtype: str = "int4", input_act: str | None = None) -> torch.Tensor:
+    """``act(x) @ W.T + bias`` with ConvRot W4A4 weights.
+
+    qweight int8 [N, K/2] holds signed int4 (low nibble = even k). wscales is either the shipped
+    per-row F32 [N] scale (full-K int32 accumulation) or the configs' per-group fp16 [N, K/64]
+    scale. linear_dtype "int4" quantizes activations to int4, "int8" to int8."""
+    if linear_dtype not in {"int4", "int8"}:
+        raise ValueError(f"ConvRot W4A4 linear_dtype must be 'int4' or 'int8', got {linear_dtype!r}")
+    if quant_group_size != INT4_GROUP_SIZE:
+        raise ValueError(f"int4 MMA kernel requires quant_group_size {INT4_GROUP_SIZE}")
+    if input_act is not None:
+        raise NotImplementedError(f"input_act={input_act!r} is not fused in this build")
+    if x.shape[-1] != qweight.shape[-1] * 2:
+        raise ValueError(f"Input K={x.shape[-1]} does not match qweight K={qweight.shape[-1] * 2}")
+    if x.shape[-1] % convrot_groupsize != 0:
+        raise ValueError(f"Input K={x.shape[-1]} is not divisible by convrot_groupsize={convrot_groupsize}")
+    n, k = qweight.shape[0], x.shape[-1]
+    qa, sa = rotate_quantize(x, convrot_groupsize, 4 if linear_dtype == "int4" else 8)
+    b = _bias_bf16(bias, n, qa.device)
+    if wscales.dim() == 2 and wscales.shape[1] > 1:
+        if wscales.shape != (n, k // quant_group_size):
+            raise ValueError(f"per-group wscales must be [{n}, {k // quant_group_size}], got {list(wscales.shape)}")
+        ws = wscales.to(torch.float16).contiguous()
+        y = gemm_w4_group(qa, sa, qweight.contiguous(), ws, None, b, n, quant_group_size)
+    else:
+        ws = wscales.reshape(-1).to(torch.float32).contiguous()
+        if ws.numel() != n:
+            raise ValueError(f"per-row wscales must have {n} elements, got {ws.numel()}")
+        y = gemm_rowscale(qa, sa, qweight.contiguous(), ws, b, n, 4)
+    return _finish(y, x, n, x.dtype if x.dtype in (torch.float16, torch.float32) else None)
+
+
+def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, s_channel=None, codebook=None,
+                     correction=None, bias=None, group_size: int = INT4_GROUP_SIZE, convrot_groupsize: int = 256,
+                     out_dtype=torch.bfloat16) -> torch.Tensor:
+    """W4A8 linear: H_cg rotation + int8 per-token activations + 4-bit weights.
+
+    Configs' scheme (uint4 asymmetric per group): qdata uint8 [N, K/2] packed codes, s_rel fp16
+    [N, K/group] per-group scales, correction uint8 [N, ceil(K/group/2)] packed uint4 zero-points
+    (None = signed int4 weights), s_channel and codebook None. The comfy-kitchen codebook layout
+    (fp8 s_rel + F32 s_channel + F32 codebook[16]) is not implemented in this build."""
+    if codebook is not None or s_channel is not None or s_rel.dtype != torch.float16:
+        raise NotImplementedError("comfy-kitchen codebook W4A8 layout (fp8 s_rel, s_channel, codebook) "
+                                  "is not implemented; pass fp16 per-group s_rel and packed uint4 zero-points")
+    if group_size != INT4_GROUP_SIZE:
+        raise ValueError(f"W4A8 kernel requires group_size {INT4_GROUP_SIZE}, got {group_size}")
+    k = x.shape[-1]
+    if k != qdata.shape[-1] * 2:
+        raise ValueError(f"Input K={k} does not match qdata K={qdata.shape[-1] * 2}")
+    if convrot_groupsize and k % convrot_groupsize:
+        raise ValueError(f"Input K={k} is not divisible by convrot_groupsize={convrot_groupsize}")
+    n = qdata.shape[0]
+    if s_rel.shape != (n, k // group_size):
+        raise ValueError(f"s_rel must be [{n}, {k // group_size}], got {list(s_rel.shape)}")
+    if correction is not None and correction.shape != (n, (k // group_size + 1) // 2):
+        raise ValueError(f"correction (zero-points) must be [{n}, {(k // group_size + 1) // 2}]")
+    qa, sa = rotate_quantize(x, convrot_groupsize, 8)
+    b = _bias_bf16(bias, n, qa.device)
+    qw = qdata.view(torch.uint8).contiguous()
+    zz = correction.view(torch.uint8).contiguous() if correction is not None else None
+    y = gemm_w4_group(qa, sa, qw, s_rel.contiguous(), zz, b, n, group_size)
+    return _finish(y, x, n, out_dtype)
+
+
+def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, bias=None,
+                out_dtype=torch.bfloat16, convrot: bool = False, convrot_groupsize: int = 256,
+                input_act: str | None = None) -> torch.Tensor:
+    """int8_tensorwise linear: int8 per-row weights [N, K] + F32 scale [N, 1], int8 per-token
+    activations (after H_cg when convrot), full-K int32 accumulation."""
+    if input_act is not None:
+        raise NotImplementedError(f"input_act={input_act!r} is not fused in this build")
+    k = x.shape[-1]
+    n = weight.shape[0]
+    if weight.shape[1] != k:
+        raise ValueError(f"Input K={k} does not match weight K={weight.shape[1]}")
+    if convrot and k % convrot_groupsize:
+        raise ValueError(f"Input K={k} is not divisible by convrot_groupsize={convrot_groupsize}")
+    qa, sa = rotate_quantize(x, convrot_groupsize if convrot else None, 8)
+    b = _bias_bf16(bias, n, qa.device)
+    ws = weight_scale.reshape(-1).to(torch.float32).contiguous()
+    y = gemm_rowscale(qa, sa, weight.contiguous(), ws, b, n, 8)
+    return _finish(y, x, n, out_dtype)

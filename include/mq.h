@@ -1,0 +1,122 @@
+/*
+ * mq.h - C ABI of libmq.so, the MI355X (gfx950) quantized-linear library.
+ *
+ * Every entry point takes raw device pointers, sizes and a hipStream_t (passed as void*),
+ * enqueues its kernels on that stream and returns immediately. The caller allocates every
+ * buffer; the library allocates nothing and keeps no mutable global state, so concurrent calls
+ * from several threads are safe. Return value: MQ_OK (0) or a negative MQ_E* code; the message
+ * of the last failure on the calling thread is returned by mq_last_error().
+ *
+ * Layout conventions (all row-major, strides in elements of the stated type):
+ *   bf16 / fp16 values are passed as uint16_t bit patterns.
+ *   int4 packing: byte j of a row holds k = 2j in bits 0-3 and k = 2j + 1 in bits 4-7
+ *   (experiments/qwen21-kernel/node/__init__.py:82-86; custom_nodes/comfy-lowbit-loader/
+ *   kernel.py:75-81 for the unsigned form). Signed nibbles decode as v >= 8 -> v - 16.
+ *   Hadamard blocks: 0 (no rotation), 16, 64 or 256; H_b = (H4/2)^(x log4 b) applied to each
+ *   block of b consecutive columns with the fp32 radix-4 FWHT of
+ *   experiments/qwen21-kernel/kernels/g64_quant.cu:68-86 (strides 1, 4, 16, 64 in that order).
+ */
+#ifndef MQ_H
+#define MQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MQ_ABI_VERSION 1
+
+enum {
+    MQ_OK = 0,
+    MQ_EINVAL = -1,       /* bad shape, stride, alignment or argument */
+    MQ_EUNSUPPORTED = -2, /* valid request outside what this build implements */
+    MQ_ELAUNCH = -3,      /* the HIP runtime refused a launch */
+};
+
+/* ABI version this library was built with (MQ_ABI_VERSION). */
+int mq_abi_version(void);
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* mq_last_error(void);
+
+/*
+ * Rotate + per-token dynamic quantize the activations of one linear.
+ *
+ * Replaces comfy-kitchen's quantize_int4_rowwise_convrot64(x, cg) as called at
+ * patches/comfy_kitchen_swiglu_w4a4_fused.patch:37 and its int8 sibling inside
+ * w4a8_int8_linear (tools/quant_mixed.py:315-317); arithmetic per tools/activation_balance.py:65-71:
+ *   xr = x rotated by H_hblock per block of hblock columns (fp32, pinned FWHT order),
+ *   s[m] = max(max_k |xr[m,k]| / L, 1e-10f), q[m,k] = clamp(rne(xr[m,k] / s[m]), -L, L),
+ * with L = 127 for bits = 8 and L = 7 for bits = 4. The division is IEEE fp32.
+ *
+ *   x      bf16 [M, K], row stride ldx elements (ldx % 8 == 0, 16-byte aligned base)
+ *   bits   8 or 4
+ *   packed 0: q is int8 [M, K] (one code per byte, stride ldq bytes)
+ *          1: q is int8 [M, K/2] packed int4 (bits must be 4, stride ldq bytes)
+ *   scale  fp32 [M]
+ * Requires K % 16 == 0, K <= 16384, K % hblock == 0.
+ */
+int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits, int packed,
+                void* q, int64_t ldq, float* scale, void* stream);
+
+/*
+ * Quantized GEMM with per-group weight scales (W4A8 asym / W4A4 sym, configs' scheme):
+ *   P[g,m,n] = sum_{k in group g} qa[m,k] * (w[n,k] - z[n,g])            (exact int32)
+ *   y[m,n]   = bf16( sa[m] * sum_g ws[n,g] * P[g,m,n] + bias[n] )
+ *
+ * Replaces the GEMM half of w4a8_int8_linear / convrot_w4a4_linear (the int4_linear call at
+ * patches/comfy_kitchen_swiglu_w4a4_fused.patch:37-38) for per-group fp16 weight scales; the
+ * reference's own per-group policy kernel is experiments/qwen21-kernel/kernels/g64_gemm6.cu:93-343
+ * with its torch reference g64_bench6.py:50-68.
+ *
+ *   qa    int8 activation codes [M, K], stride lda bytes (lda % 16 == 0)
+ *   sa    fp32 [M]
+ *   qw    packed 4-bit weights [N, K/2], stride ldw bytes (ldw % 16 == 0)
+ *   ws    fp16 [N, K/group], stride ldws elements
+ *   wz    packed uint4 zero-points [N, ceil(K/group/2)], stride ldwz bytes; NULL = signed
+ *         symmetric int4 weights (no zero-point)
+ *   group 64
+ *   bias  bf16 [N] or NULL
+ *   y     bf16 [M, N], stride ldy elements
+ * Requires K % 128 == 0.
+ */
+int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
+                     const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group,
+                     const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                     void* stream);
+
+/*
+ * Debug / parity entry: the exact per-group int32 partials P[g,m,n] of mq_gemm_w4_group
+ * (same tile loaders, unpack and MFMA code), written to part int32 [K/group, M, N] (dense).
+ */
+int mq_gemm_w4_group_partials(const int8_t* qa, int64_t lda, const uint8_t* qw, int64_t ldw,
+                              const uint8_t* wz, int64_t ldwz, int group, int32_t* part,
+                              int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * Quantized GEMM with per-row weight scales and a full-K int32 accumulator (policy 0 of
+ * experiments/qwen21-kernel/kernels/g64_gemm6.cu:5):
+ *   y[m,n] = bf16( (sum_k qa[m,k] * w[n,k]) * sa[m] * ws[n] + bias[n] )
+ * Replaces int4_linear(qact, qweight, x_scale, wscales, bias, out_dtype) of the shipped ConvRot
+ * W4A4 format (patches/comfy_kitchen_swiglu_w4a4_fused.patch:37-38) when wbits = 4, and the
+ * int8 x int8 GEMM of int8_linear (tools/verify_w4a4.py:342-370) when wbits = 8.
+ *
+ *   qa    int8 activation codes [M, K], stride lda bytes
+ *   qw    wbits 4: signed int4 packed [N, K/2]; wbits 8: int8 [N, K]; stride ldw bytes
+ *   ws    fp32 [N]
+ * Requires K % 64 == 0.
+ */
+int mq_gemm_rowscale(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw,
+                     int wbits, const float* ws, const uint16_t* bias, uint16_t* y, int64_t ldy,
+                     int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Debug / parity entry: the full-K int32 accumulator of mq_gemm_rowscale, acc int32 [M, N]. */
+int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t ldw, int wbits,
+                         int32_t* acc, int64_t M, int64_t N, int64_t K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MQ_H */

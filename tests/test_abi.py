@@ -1,0 +1,74 @@
+"""The C ABI: libmq.so loads, exports every symbol include/mq.h declares, and rejects bad
+arguments with MQ_EINVAL before touching the GPU (CPU only: no kernel is launched)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import REPO
+
+HEADER = os.path.join(REPO, "include", "mq.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(mq_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from kitchen_amd import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("libmq.so is not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_header_declares_expected_entry_points():
+    syms = declared_symbols()
+    assert "mq_rotquant" in syms and "mq_gemm_w4_group" in syms and "mq_last_error" in syms
+    from kitchen_amd import _lib
+
+    assert sorted(_lib.EXPORTED) == syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    assert lib.mq_abi_version() == 1
+
+
+def _err(lib):
+    return lib.mq_last_error().decode()
+
+
+def test_rotquant_validation_rejects_before_launch(lib):
+    # null device pointers are never dereferenced: every case fails validation first
+    assert lib.mq_rotquant(None, 4, 256, 256, 256, 5, 0, None, 256, None, None) == -1
+    assert "bits" in _err(lib)
+    assert lib.mq_rotquant(None, 4, 256, 256, 32, 8, 0, None, 256, None, None) == -1
+    assert "group size" in _err(lib)
+    assert lib.mq_rotquant(None, 4, 200, 200, 0, 8, 0, None, 256, None, None) == -1
+    assert "multiple of 16" in _err(lib)
+    assert lib.mq_rotquant(None, 4, 320, 320, 256, 8, 0, None, 320, None, None) == -1
+    assert "not a multiple of the group size" in _err(lib)
+    assert lib.mq_rotquant(None, 4, 32768, 32768, 256, 8, 0, None, 32768, None, None) == -2
+    assert lib.mq_rotquant(None, 4, 256, 256, 256, 8, 1, None, 256, None, None) == -1
+    assert "packed" in _err(lib)
+    # M == 0 is a valid no-op
+    assert lib.mq_rotquant(None, 0, 256, 256, 256, 8, 0, None, 256, None, None) == 0
+
+
+def test_gemm_validation_rejects_before_launch(lib):
+    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 128, None, None, 8, 8, 8, 64, None) == -1
+    assert "group size must be 64" in _err(lib)
+    assert lib.mq_gemm_w4_group(None, 96, None, None, 48, None, 1, None, 1, 64, None, None, 8, 8, 8, 96, None) == -1
+    assert "multiple of 64" in _err(lib)
+    assert lib.mq_gemm_rowscale(None, 64, None, None, 64, 3, None, None, None, 8, 8, 8, 64, None) == -1
+    assert "wbits" in _err(lib)
+    assert lib.mq_gemm_rowscale_acc(None, 64, None, 64, 8, None, 8, 8, 64, None) == -1
+    assert "null" in _err(lib)
