@@ -73,7 +73,8 @@ int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, in
     MQ_REQUIRE(M >= 0 && K > 0, "rotquant: bad shape M=%lld K=%lld", (long long)M, (long long)K);
     MQ_REQUIRE(M < (int64_t(1) << 31), "rotquant: M too large");
     MQ_REQUIRE(bits == 8 || bits == 4, "rotquant: bits must be 8 or 4 (got %d)", bits);
-    MQ_REQUIRE(packed == 0 || bits == 4, "rotquant: packed output needs bits = 4");
+    MQ_REQUIRE(packed >= MQ_Q_BYTES && packed <= MQ_Q_X16ALT, "rotquant: unknown code layout %d", packed);
+    MQ_REQUIRE(packed == MQ_Q_BYTES || bits == 4, "rotquant: packed output needs bits = 4");
     MQ_REQUIRE(hblock == 0 || hblock == 16 || hblock == 64 || hblock == 256,
                "rotquant: convrot group size must be 16, 64 or 256 (got %d)", hblock);
     MQ_REQUIRE(K % 16 == 0, "rotquant: K=%lld must be a multiple of 16", (long long)K);
@@ -86,8 +87,8 @@ int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, in
     if (M == 0) return MQ_OK;
     MQ_REQUIRE(x && q && scale, "rotquant: null pointer");
     MQ_REQUIRE(ldx >= K && ldx % 8 == 0 && aligned(x, 16), "rotquant: x needs ldx >= K, ldx %% 8 == 0, 16-byte aligned base");
-    const int64_t row_bytes = packed ? K / 2 : K;
-    const int64_t qalign = packed ? 8 : 16;
+    const int64_t row_bytes = packed == MQ_Q_PACKED ? K / 2 : K;
+    const int64_t qalign = packed == MQ_Q_PACKED ? 8 : 16;
     MQ_REQUIRE(ldq >= row_bytes && ldq % qalign == 0 && aligned(q, qalign),
                "rotquant: q needs ldq >= %lld bytes, ldq %% %lld == 0 and an aligned base", (long long)row_bytes,
                (long long)qalign);
@@ -97,11 +98,12 @@ int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, in
 }
 
 int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
-                     const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group,
+                     const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
                      const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                      void* stream) {
     clear_error();
     MQ_REQUIRE(group == 64, "gemm_w4_group: quant group size must be 64 (got %d)", group);
+    MQ_REQUIRE(act_mode >= MQ_ACT_I8 && act_mode <= MQ_ACT_X16ALT, "gemm_w4_group: unknown act_mode %d", act_mode);
     int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, K / 2);
     if (rc) return rc;
     MQ_REQUIRE(sa && ws && y, "gemm_w4_group: null pointer");
@@ -111,21 +113,24 @@ int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8
     GemmArgs a{};
     a.qa = qa; a.lda = lda; a.sa = sa; a.qw = qw; a.ldw = ldw; a.ws16 = ws; a.ldws = ldws;
     a.wz = wz; a.ldwz = ldwz; a.bias = bias; a.y = y; a.ldy = ldy; a.M = M; a.N = N; a.K = K;
+    a.act_mode = act_mode;
     return launch_gemm(a, wz ? WKind::U4Asym : WKind::I4Sym, Epi::GroupScale, static_cast<hipStream_t>(stream));
 }
 
 int mq_gemm_w4_group_partials(const int8_t* qa, int64_t lda, const uint8_t* qw, int64_t ldw, const uint8_t* wz,
-                              int64_t ldwz, int group, int32_t* part, int64_t M, int64_t N, int64_t K,
+                              int64_t ldwz, int group, int act_mode, int32_t* part, int64_t M, int64_t N, int64_t K,
                               void* stream) {
     clear_error();
     MQ_REQUIRE(group == 64, "gemm_w4_group_partials: quant group size must be 64 (got %d)", group);
+    MQ_REQUIRE(act_mode >= MQ_ACT_I8 && act_mode <= MQ_ACT_X16ALT, "gemm_w4_group_partials: unknown act_mode %d",
+               act_mode);
     int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, K / 2);
     if (rc) return rc;
     MQ_REQUIRE(part, "gemm_w4_group_partials: null pointer");
     MQ_REQUIRE(!wz || ldwz >= (K / group + 1) / 2, "gemm_w4_group_partials: ldwz < ceil(K/group/2)");
     GemmArgs a{};
     a.qa = qa; a.lda = lda; a.qw = qw; a.ldw = ldw; a.wz = wz; a.ldwz = ldwz; a.part = part;
-    a.M = M; a.N = N; a.K = K;
+    a.M = M; a.N = N; a.K = K; a.act_mode = act_mode;
     return launch_gemm(a, wz ? WKind::U4Asym : WKind::I4Sym, Epi::GroupPartials, static_cast<hipStream_t>(stream));
 }
 

@@ -13,7 +13,8 @@
 //
 // Epilogues:
 //   GroupScale    acc[m,n] += float(P_g[m,n]) * ws[n,g] after every group; at the end
-//                 y = bf16(acc * sa[m] + bias[n])      (g64_bench6.py:50-68 order of scales)
+//                 y = bf16(acc * sa[m] + bias[n])      (g64_bench6.py:50-68 order of scales).
+//                 Activation layout 2 (16 * q, negated in odd groups) is undone through the scale.
 //   GroupPartials writes P_g[m,n] (int32) for every group (parity entry)
 //   RowScale      one int32 accumulator over all of K; y = bf16(P * sa[m] * ws[n] + bias[n])
 //                 (policy 0 of experiments/qwen21-kernel/kernels/g64_gemm6.cu:5)
@@ -90,6 +91,8 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
         if constexpr (EPI == Epi::GroupScale) {
             const int64_t n = n0 + (tid & (BN - 1));
             rs = n < N ? f16_bits_to_f32(a.ws16[n * a.ldws + kt]) : 0.0f;
+            // layout 2 activations are 16 * q, negated in odd groups (exact power-of-two rescale)
+            if (a.act_mode == 2) rs *= (kt & 1) ? -0.0625f : 0.0625f;
         }
     };
     auto fix_edges = [&]() {
@@ -189,7 +192,9 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        if (row < M && col < N) part[row * N + col] = p[i][j][r];
+                        int32_t v = p[i][j][r];
+                        if (a.act_mode == 2) v = (kt & 1) ? -(v >> 4) : (v >> 4);   // exact: a multiple of 16
+                        if (row < M && col < N) part[row * N + col] = v;
                     }
                 }
         }
@@ -254,6 +259,11 @@ int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
 
 int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     if (a.M == 0 || a.N == 0) return 0;
+    // The 256 x 256-tile kernel addresses each operand with 32-bit buffer offsets.
+    const int64_t wbytes = wk == WKind::I8 ? a.K : a.K / 2;
+    const bool fits32 = a.M * a.lda < (int64_t(1) << 31) && a.N * a.ldw < (int64_t(1) << 31) &&
+                        (a.N * a.ldws + a.K / 64) * 2 < (int64_t(1) << 31) && wbytes <= a.ldw;
+    if (a.M > 128 && fits32) return launch_gemm_wide(a, wk, epi, stream);
     switch (wk) {
         case WKind::U4Asym:
             if (epi == Epi::RowScale || epi == Epi::RowAcc) break;

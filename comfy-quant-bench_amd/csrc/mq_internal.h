@@ -40,8 +40,20 @@ struct GemmArgs {
     int64_t ldy;
     int32_t* part;          // int32 partials / accumulators
     int64_t M, N, K;
+    int act_mode;           // group-scale GEMMs: MQ_ACT_* layout of qa (include/mq.h)
 };
 
+// Power-of-two factor by which a group GEMM's MFMA result exceeds the true partial, per
+// activation layout and weight kind (see mq_gemm_wide.hip).
+__host__ __device__ inline int group_shift(int act_mode, WKind wk) {
+    if (act_mode == 1) return 4;
+    if (act_mode == 2) return wk == WKind::I4Sym ? 8 : 4;
+    return 0;
+}
+
 int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream);
+
+// 256 x 256-tile kernel for large M (mq_gemm_wide.hip).
+int launch_gemm_wide(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream);
 
 }  // namespace mq

@@ -121,7 +121,9 @@ __device__ __forceinline__ float quant_magic(float v, float r, float s) {
     return m;
 }
 
-// OUT: 0 = int8 codes, 1 = int4 codes one per byte, 2 = int4 codes packed two per byte.
+// OUT: 0 = int8 codes, 1 = int4 codes one per byte, 2 = int4 codes packed two per byte,
+//      3 = int4 codes one per byte as 16 * q, negated in odd 64-column groups (the operand layout
+//          the group-scale GEMM takes for int4 activations: exact, and 16x finer in its fp32 step).
 template <int BLK, int OUT, int NCH>
 __global__ void __launch_bounds__(64 * kWaves)
 rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
@@ -172,10 +174,20 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
         uint32_t word[4];
 #pragma unroll
         for (int hi = 0; hi < 4; ++hi) {
-            const uint32_t m0 = __float_as_uint(quant_magic<LIMIT>(v[c][4 * hi + 0], r, s));
-            const uint32_t m1 = __float_as_uint(quant_magic<LIMIT>(v[c][4 * hi + 1], r, s));
-            const uint32_t m2 = __float_as_uint(quant_magic<LIMIT>(v[c][4 * hi + 2], r, s));
-            const uint32_t m3 = __float_as_uint(quant_magic<LIMIT>(v[c][4 * hi + 3], r, s));
+            // quantization is odd-symmetric (rint and the clamp are), so negating the input of an
+            // odd 64-column group negates its codes exactly
+            float sg = 1.0f;
+            if constexpr (OUT == 3) {
+                const int col = c * 1024 + (BLK < 64 ? 16 * lane + 4 * hi : group_col<BLK>(lane, hi));
+                sg = (col >> 6) & 1 ? -1.0f : 1.0f;
+            }
+            uint32_t m0 = __float_as_uint(quant_magic<LIMIT>(sg * v[c][4 * hi + 0], r, s));
+            uint32_t m1 = __float_as_uint(quant_magic<LIMIT>(sg * v[c][4 * hi + 1], r, s));
+            uint32_t m2 = __float_as_uint(quant_magic<LIMIT>(sg * v[c][4 * hi + 2], r, s));
+            uint32_t m3 = __float_as_uint(quant_magic<LIMIT>(sg * v[c][4 * hi + 3], r, s));
+            if constexpr (OUT == 3) {
+                m0 <<= 4; m1 <<= 4; m2 <<= 4; m3 <<= 4;
+            }
             if constexpr (OUT == 2) {
                 word[hi] = (m0 & 0xfu) | ((m1 & 0xfu) << 4) | ((m2 & 0xfu) << 8) | ((m3 & 0xfu) << 12);
             } else {
@@ -239,7 +251,8 @@ template <int BLK>
 int dispatch_out(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int bits, int packed, void* q,
                  int64_t ldq, float* scale, hipStream_t stream) {
     if (bits == 8) return dispatch_nch<BLK, 0>(x, M, K, ldx, q, ldq, scale, stream);
-    if (packed) return dispatch_nch<BLK, 2>(x, M, K, ldx, q, ldq, scale, stream);
+    if (packed == 1) return dispatch_nch<BLK, 2>(x, M, K, ldx, q, ldq, scale, stream);
+    if (packed == 2) return dispatch_nch<BLK, 3>(x, M, K, ldx, q, ldq, scale, stream);
     return dispatch_nch<BLK, 1>(x, M, K, ldx, q, ldq, scale, stream);
 }
 

@@ -50,17 +50,19 @@ def _finish(y: torch.Tensor, x: torch.Tensor, n: int, out_dtype) -> torch.Tensor
 
 # --------------------------------------------------------------------------- activation quantizers
 
-def rotate_quantize(x: torch.Tensor, convrot_groupsize: int | None, bits: int, packed: bool = False):
+def rotate_quantize(x: torch.Tensor, convrot_groupsize: int | None, bits: int, packed: bool | int = False):
     """Rotate x [.., K] by H_cg per block and quantize per token to int8 (bits 8) or int4 (bits 4).
 
-    Returns (q, scale): q int8 [M, K] (one code per byte) or int8 [M, K/2] (packed int4),
-    scale float32 [M]."""
+    packed: False / Q_BYTES one code per byte, True / Q_PACKED packed int4 [M, K/2], Q_X16ALT the
+    group GEMM's int4 operand layout (16 * q, negated in odd 64-column groups).
+    Returns (q, scale): q int8 [M, K] or [M, K/2], scale float32 [M]."""
+    layout = int(packed)
     k = x.shape[-1]
     x2 = _as_bf16_2d(x, k)
     m = x2.shape[0]
-    q = torch.empty((m, k // 2 if packed else k), dtype=torch.int8, device=x2.device)
+    q = torch.empty((m, k // 2 if layout == _lib.Q_PACKED else k), dtype=torch.int8, device=x2.device)
     s = torch.empty((m,), dtype=torch.float32, device=x2.device)
-    _lib.call("mq_rotquant", x2.data_ptr(), m, k, k, int(convrot_groupsize or 0), int(bits), int(packed),
+    _lib.call("mq_rotquant", x2.data_ptr(), m, k, k, int(convrot_groupsize or 0), int(bits), layout,
               q.data_ptr(), q.stride(0), s.data_ptr(), _lib.stream_of(x2))
     return q, s
 
@@ -91,26 +93,32 @@ def _check_w4_group(qa, qweight, wscales, wzeros, n, group_size):
         raise ValueError(f"zero-points must be packed uint4 [{n}, {(groups + 1) // 2}]")
 
 
-def gemm_w4_group(qa, sa, qweight, wscales, wzeros, bias, n: int, group_size: int = INT4_GROUP_SIZE):
-    """y bf16 [M, N] = sa * sum_g wscales[:, g] * P_g + bias with P_g exact int32 group partials."""
+def gemm_w4_group(qa, sa, qweight, wscales, wzeros, bias, n: int, group_size: int = INT4_GROUP_SIZE,
+                  act_mode: int = _lib.ACT_I8):
+    """y bf16 [M, N] = sa * sum_g wscales[:, g] * P_g + bias with P_g exact int32 group partials.
+
+    act_mode: ACT_I8 int8 codes, ACT_I4 int4 codes one per byte, ACT_X16ALT the layout written by
+    rotate_quantize(..., packed=Q_X16ALT)."""
     m, k = qa.shape
     _check_w4_group(qa, qweight, wscales, wzeros, n, group_size)
     y = torch.empty((m, n), dtype=torch.bfloat16, device=qa.device)
     ldwz = wzeros.stride(0) if wzeros is not None else 0
     _lib.call("mq_gemm_w4_group", qa.data_ptr(), qa.stride(0), sa.data_ptr(), qweight.data_ptr(),
               qweight.stride(0), wscales.data_ptr(), wscales.stride(0), _lib.ptr(wzeros), ldwz, int(group_size),
-              _lib.ptr(bias), y.data_ptr(), y.stride(0), m, n, k, _lib.stream_of(qa))
+              int(act_mode), _lib.ptr(bias), y.data_ptr(), y.stride(0), m, n, k, _lib.stream_of(qa))
     return y
 
 
-def gemm_w4_group_partials(qa, qweight, wzeros, n: int, group_size: int = INT4_GROUP_SIZE):
-    """Parity entry: exact int32 partials P [K/G, M, N] of gemm_w4_group."""
+def gemm_w4_group_partials(qa, qweight, wzeros, n: int, group_size: int = INT4_GROUP_SIZE,
+                           act_mode: int = _lib.ACT_I8):
+    """Parity entry: exact int32 partials P [K/G, M, N] of gemm_w4_group (of the codes themselves,
+    whatever act_mode's scaling)."""
     m, k = qa.shape
     _check_w4_group(qa, qweight, None, wzeros, n, group_size)
     part = torch.empty((k // group_size, m, n), dtype=torch.int32, device=qa.device)
     ldwz = wzeros.stride(0) if wzeros is not None else 0
     _lib.call("mq_gemm_w4_group_partials", qa.data_ptr(), qa.stride(0), qweight.data_ptr(), qweight.stride(0),
-              _lib.ptr(wzeros), ldwz, int(group_size), part.data_ptr(), m, n, k, _lib.stream_of(qa))
+              _lib.ptr(wzeros), ldwz, int(group_size), int(act_mode), part.data_ptr(), m, n, k, _lib.stream_of(qa))
     return part
 
 
@@ -154,17 +162,23 @@ def convrot_w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.T
     if x.shape[-1] % convrot_groupsize != 0:
         raise ValueError(f"Input K={x.shape[-1]} is not divisible by convrot_groupsize={convrot_groupsize}")
     n, k = qweight.shape[0], x.shape[-1]
-    qa, sa = rotate_quantize(x, convrot_groupsize, 4 if linear_dtype == "int4" else 8)
-    b = _bias_bf16(bias, n, qa.device)
+    bits = 4 if linear_dtype == "int4" else 8
     if wscales.dim() == 2 and wscales.shape[1] > 1:
         if wscales.shape != (n, k // quant_group_size):
             raise ValueError(f"per-group wscales must be [{n}, {k // quant_group_size}], got {list(wscales.shape)}")
+        # int4 activations go to the group GEMM in its x16 operand layout
+        layout = _lib.Q_X16ALT if bits == 4 else _lib.Q_BYTES
+        qa, sa = rotate_quantize(x, convrot_groupsize, bits, layout)
+        b = _bias_bf16(bias, n, qa.device)
         ws = wscales.to(torch.float16).contiguous()
-        y = gemm_w4_group(qa, sa, qweight.contiguous(), ws, None, b, n, quant_group_size)
+        act = _lib.ACT_X16ALT if bits == 4 else _lib.ACT_I8
+        y = gemm_w4_group(qa, sa, qweight.contiguous(), ws, None, b, n, quant_group_size, act)
     else:
         ws = wscales.reshape(-1).to(torch.float32).contiguous()
         if ws.numel() != n:
             raise ValueError(f"per-row wscales must have {n} elements, got {ws.numel()}")
+        qa, sa = rotate_quantize(x, convrot_groupsize, bits)
+        b = _bias_bf16(bias, n, qa.device)
         y = gemm_rowscale(qa, sa, qweight.contiguous(), ws, b, n, 4)
     return _finish(y, x, n, x.dtype if x.dtype in (torch.float16, torch.float32) else None)
 

@@ -25,13 +25,28 @@
 extern "C" {
 #endif
 
-#define MQ_ABI_VERSION 1
+#define MQ_ABI_VERSION 2
 
 enum {
     MQ_OK = 0,
     MQ_EINVAL = -1,       /* bad shape, stride, alignment or argument */
     MQ_EUNSUPPORTED = -2, /* valid request outside what this build implements */
     MQ_ELAUNCH = -3,      /* the HIP runtime refused a launch */
+};
+
+/* Layouts of the activation codes written by mq_rotquant (its `packed` argument). */
+enum {
+    MQ_Q_BYTES = 0,    /* one code per byte: int8 codes (bits 8) or int4 codes in [-7, 7] (bits 4) */
+    MQ_Q_PACKED = 1,   /* int4 codes packed two per byte, low nibble = even k (bits 4) */
+    MQ_Q_X16ALT = 2,   /* int4 codes one per byte as 16 * q, negated in odd 64-column groups (bits 4):
+                          the operand layout of the group GEMMs for int4 activations (MQ_ACT_X16ALT) */
+};
+
+/* Layouts of the activation codes qa taken by the group-scale GEMMs (their `act_mode`). */
+enum {
+    MQ_ACT_I8 = 0,       /* int8 per-token codes (int8 range) */
+    MQ_ACT_I4 = 1,       /* int4 codes in [-8, 7], one per byte (scaled by 16 inside the kernel) */
+    MQ_ACT_X16ALT = 2,   /* layout MQ_Q_X16ALT of mq_rotquant */
 };
 
 /* ABI version this library was built with (MQ_ABI_VERSION). */
@@ -52,8 +67,9 @@ const char* mq_last_error(void);
  *
  *   x      bf16 [M, K], row stride ldx elements (ldx % 8 == 0, 16-byte aligned base)
  *   bits   8 or 4
- *   packed 0: q is int8 [M, K] (one code per byte, stride ldq bytes)
- *          1: q is int8 [M, K/2] packed int4 (bits must be 4, stride ldq bytes)
+ *   packed MQ_Q_BYTES: q is int8 [M, K] (one code per byte, stride ldq bytes)
+ *          MQ_Q_PACKED: q is int8 [M, K/2] packed int4 (bits must be 4, stride ldq bytes)
+ *          MQ_Q_X16ALT: q is int8 [M, K], 16 * code, negated where (k / 64) is odd (bits 4)
  *   scale  fp32 [M]
  * Requires K % 16 == 0, K <= 16384, K % hblock == 0.
  */
@@ -70,7 +86,7 @@ int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, in
  * reference's own per-group policy kernel is experiments/qwen21-kernel/kernels/g64_gemm6.cu:93-343
  * with its torch reference g64_bench6.py:50-68.
  *
- *   qa    int8 activation codes [M, K], stride lda bytes (lda % 16 == 0)
+ *   qa    activation codes [M, K] in layout act_mode (MQ_ACT_*), stride lda bytes (lda % 16 == 0)
  *   sa    fp32 [M]
  *   qw    packed 4-bit weights [N, K/2], stride ldw bytes (ldw % 16 == 0)
  *   ws    fp16 [N, K/group], stride ldws elements
@@ -79,19 +95,20 @@ int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, in
  *   group 64
  *   bias  bf16 [N] or NULL
  *   y     bf16 [M, N], stride ldy elements
- * Requires K % 128 == 0.
+ * Requires K % 64 == 0. The partials are exact; the sum over groups is accumulated in fp32.
  */
 int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
-                     const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group,
+                     const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
                      const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                      void* stream);
 
 /*
  * Debug / parity entry: the exact per-group int32 partials P[g,m,n] of mq_gemm_w4_group
  * (same tile loaders, unpack and MFMA code), written to part int32 [K/group, M, N] (dense).
+ * P is the partial of the codes themselves: the x16 / sign of layout MQ_ACT_X16ALT is undone.
  */
 int mq_gemm_w4_group_partials(const int8_t* qa, int64_t lda, const uint8_t* qw, int64_t ldw,
-                              const uint8_t* wz, int64_t ldwz, int group, int32_t* part,
+                              const uint8_t* wz, int64_t ldwz, int group, int act_mode, int32_t* part,
                               int64_t M, int64_t N, int64_t K, void* stream);
 
 /*

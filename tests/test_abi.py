@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mq_abi_version() == 1
+    assert lib.mq_abi_version() == 2
 
 
 def _err(lib):
@@ -59,15 +59,23 @@ def test_rotquant_validation_rejects_before_launch(lib):
     assert lib.mq_rotquant(None, 4, 32768, 32768, 256, 8, 0, None, 32768, None, None) == -2
     assert lib.mq_rotquant(None, 4, 256, 256, 256, 8, 1, None, 256, None, None) == -1
     assert "packed" in _err(lib)
+    assert lib.mq_rotquant(None, 4, 256, 256, 256, 8, 2, None, 256, None, None) == -1
+    assert "packed" in _err(lib)
+    assert lib.mq_rotquant(None, 4, 256, 256, 256, 4, 3, None, 256, None, None) == -1
+    assert "layout" in _err(lib)
     # M == 0 is a valid no-op
     assert lib.mq_rotquant(None, 0, 256, 256, 256, 8, 0, None, 256, None, None) == 0
 
 
 def test_gemm_validation_rejects_before_launch(lib):
-    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 128, None, None, 8, 8, 8, 64, None) == -1
+    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 128, 0, None, None, 8, 8, 8, 64, None) == -1
     assert "group size must be 64" in _err(lib)
-    assert lib.mq_gemm_w4_group(None, 96, None, None, 48, None, 1, None, 1, 64, None, None, 8, 8, 8, 96, None) == -1
+    assert lib.mq_gemm_w4_group(None, 96, None, None, 48, None, 1, None, 1, 64, 0, None, None, 8, 8, 8, 96, None) == -1
     assert "multiple of 64" in _err(lib)
+    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 64, 3, None, None, 8, 8, 8, 64, None) == -1
+    assert "act_mode" in _err(lib)
+    assert lib.mq_gemm_w4_group_partials(None, 64, None, 32, None, 1, 64, 7, None, 8, 8, 64, None) == -1
+    assert "act_mode" in _err(lib)
     assert lib.mq_gemm_rowscale(None, 64, None, None, 64, 3, None, None, None, 8, 8, 8, 64, None) == -1
     assert "wbits" in _err(lib)
     assert lib.mq_gemm_rowscale_acc(None, 64, None, 64, 8, None, 8, 8, 64, None) == -1

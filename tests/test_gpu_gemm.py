@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from kitchen_amd import ops
+from kitchen_amd import _lib, ops
 from oracle import gemm, quant
 
 pytestmark = pytest.mark.gpu
@@ -112,4 +112,77 @@ def test_rowscale_acc_and_output(gpu_device, wbits, m, n, k):
                           torch.from_numpy(bias).to(gpu_device, torch.bfloat16), n, wbits)
     torch.cuda.synchronize()
     err = gemm.rel_l2(gemm.epilogue_row(p0, sa, sw, bias), y.float().cpu().numpy())
+    assert err < TIGHT, err
+
+
+# ---------------------------------------------------------------- activation layouts and tile paths
+# M <= 128 runs the 128 x 128-tile kernel, larger M the 256 x 256-tile kernel: both are covered.
+
+def _x16alt(qa):
+    """The group GEMM's int4 operand layout (mq_rotquant MQ_Q_X16ALT): 16 * q, odd groups negated."""
+    sign = np.where((np.arange(qa.shape[1]) // 64) % 2 == 1, -1, 1).astype(np.int16)
+    return (16 * qa.astype(np.int16) * sign[None, :]).astype(np.int8)
+
+
+@pytest.mark.parametrize("act_mode", [_lib.ACT_I4, _lib.ACT_X16ALT])
+@pytest.mark.parametrize("wkind", ["u4", "i4"])
+@pytest.mark.parametrize("m,n,k", [(96, 128, 256), (300, 384, 1024), (513, 256, 3072)])
+def test_int4_activation_layouts_partials_bitexact(gpu_device, act_mode, wkind, m, n, k):
+    print(f"[gemm] int4 act mode={act_mode} w={wkind} M={m} N={n} K={k}", flush=True)
+    rng = np.random.default_rng(m + n + act_mode)
+    qa = rng.integers(-7, 8, (m, k)).astype(np.int8)
+    qa_dev = _x16alt(qa) if act_mode == _lib.ACT_X16ALT else qa
+    if wkind == "u4":
+        q = rng.integers(0, 16, (n, k)).astype(np.uint8)
+        z = rng.integers(0, 16, (n, k // 64)).astype(np.uint8)
+        wpk, zpk, wq = quant.pack_u4(q), quant.pack_u4(z), gemm.zero_adjusted(q, z, 64)
+    else:
+        wq = rng.integers(-8, 8, (n, k)).astype(np.int8)
+        wpk, zpk = quant.pack_i4(wq), None
+    part = ops.gemm_w4_group_partials(_t(qa_dev, gpu_device), _t(wpk, gpu_device),
+                                      None if zpk is None else _t(zpk, gpu_device), n, 64, act_mode)
+    torch.cuda.synchronize()
+    assert np.array_equal(part.cpu().numpy().astype(np.int64), gemm.partials(qa, wq, 64))
+
+
+@pytest.mark.parametrize("act_mode", [_lib.ACT_I4, _lib.ACT_X16ALT])
+@pytest.mark.parametrize("m", [64, 1024])
+def test_int4_activation_layouts_output(gpu_device, act_mode, m):
+    """W4A4 group scheme (int4 per-token activations, int4 sym g64 fp16 weights): the fp32 group
+    accumulation stays at the bf16 rounding floor with int4-sized partials."""
+    n, k = 768, 3072
+    print(f"[gemm] int4 act output mode={act_mode} M={m}", flush=True)
+    rng = np.random.default_rng(11 * m + act_mode)
+    qa = rng.integers(-7, 8, (m, k)).astype(np.int8)
+    sa = rng.uniform(0.05, 0.2, m).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    qw, s16 = quant.quant_weight_i4_sym_group(w, 64)
+    bias = _bf16_round(rng.standard_normal(n) * 0.5)
+    qa_dev = _x16alt(qa) if act_mode == _lib.ACT_X16ALT else qa
+    y = ops.gemm_w4_group(_t(qa_dev, gpu_device), _t(sa, gpu_device), _t(quant.pack_i4(qw), gpu_device),
+                          _t(s16, gpu_device), None, torch.from_numpy(bias).to(gpu_device, torch.bfloat16), n, 64,
+                          act_mode)
+    torch.cuda.synchronize()
+    y0 = gemm.epilogue_group(gemm.partials(qa, qw, 64), sa, s16, bias)
+    err = gemm.rel_l2(y0, y.float().cpu().numpy())
+    assert err < TIGHT, err
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 1000, 640), (257, 200, 128), (1000, 520, 3072)])
+def test_wide_tile_ragged_edges(gpu_device, m, n, k):
+    """Ragged M and N (N % 8 != 0 takes the element-wise store path) on the 256 x 256-tile kernel,
+    int8 activations with full-range signed int4 weights (nibble -8 included)."""
+    print(f"[gemm] ragged M={m} N={n} K={k}", flush=True)
+    rng = np.random.default_rng(m * 7 + n)
+    qa = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    qw = rng.integers(-8, 8, (n, k)).astype(np.int8)
+    part = ops.gemm_w4_group_partials(_t(qa, gpu_device), _t(quant.pack_i4(qw), gpu_device), None, n)
+    torch.cuda.synchronize()
+    assert np.array_equal(part.cpu().numpy().astype(np.int64), gemm.partials(qa, qw, 64))
+    sa = rng.uniform(0.005, 0.015, m).astype(np.float32)
+    s16 = rng.uniform(0.001, 0.01, (n, k // 64)).astype(np.float16)
+    y = ops.gemm_w4_group(_t(qa, gpu_device), _t(sa, gpu_device), _t(quant.pack_i4(qw), gpu_device),
+                          _t(s16, gpu_device), None, None, n)
+    torch.cuda.synchronize()
+    err = gemm.rel_l2(gemm.epilogue_group(gemm.partials(qa, qw, 64), sa, s16), y.float().cpu().numpy())
     assert err < TIGHT, err

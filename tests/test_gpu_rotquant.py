@@ -31,14 +31,18 @@ def _check(xbits, hblock, bits, packed, dev, label):
     q, s = _run(xbits, hblock, bits, packed, dev)
     q0, s0 = _oracle(xbits, hblock, bits)
     assert np.array_equal(s.view(np.uint32), s0.view(np.uint32)), "scales differ"
-    if packed:
+    if packed == _lib.Q_X16ALT:
+        # the group GEMM's int4 operand layout: 16 * q, negated in odd 64-column groups
+        sign = np.where((np.arange(q0.shape[1]) // 64) % 2 == 1, -1, 1).astype(np.int16)
+        assert np.array_equal(q.astype(np.int16), 16 * q0.astype(np.int16) * sign[None, :]), "x16alt codes differ"
+    elif packed:
         assert np.array_equal(q, quant.pack_i4(q0)), "packed codes differ"
     else:
         diff = np.nonzero(q != q0)
         assert diff[0].size == 0, f"{diff[0].size} codes differ, first at {diff[0][0]},{diff[1][0]}"
 
 
-MODES = [(8, False), (4, False), (4, True)]
+MODES = [(8, False), (4, False), (4, True), (4, _lib.Q_X16ALT)]
 
 
 @pytest.mark.parametrize("hblock", [0, 16, 64, 256])
@@ -62,6 +66,7 @@ def test_k_range_bitexact(gpu_device, k):
     for hb in (64, 256):
         _check(xb, hb, 8, False, gpu_device, f"K{k}")
     _check(xb, 256, 4, True, gpu_device, f"K{k}")
+    _check(xb, 64, 4, _lib.Q_X16ALT, gpu_device, f"K{k}")
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 5, 63, 65])
@@ -74,6 +79,7 @@ def test_small_k_no_rotation_and_block16(gpu_device):
     xb = synth.activations(9, 16, seed=3)
     _check(xb, 0, 8, False, gpu_device, "K16")
     _check(xb, 16, 4, True, gpu_device, "K16")
+    _check(xb, 16, 4, _lib.Q_X16ALT, gpu_device, "K16")
 
 
 def test_zero_rows_and_exact_ties(gpu_device):
