@@ -4,9 +4,12 @@
 //
 // Layout. Waves form a 4 (M) x 2 (N) grid; each owns a 64 x 128 output tile made of 4 x 8 MFMA
 // 16x16 tiles. In the 16x16 output layout lane l holds column l % 16 and rows 4 * (l / 16) + r,
-// r = 0..3, so every lane needs one weight scale per column tile. A (int8 activation codes) and B (weights, unpacked to int8 on their way into LDS)
-// are double-buffered in LDS with an 80-byte row pitch (conflict-free ds_read_b128); global loads
-// of group g+2 are in flight while group g is multiplied.
+// r = 0..3, so every lane needs one weight scale per column tile. A (int8 activation codes) and
+// B (weights, unpacked to int8 on their way into LDS) are double-buffered in LDS as 64-byte rows
+// whose four 16-byte chunks are XOR-swizzled by (row >> 1) & 3: the fragment reads (lane l reads
+// chunk l / 16 of row l % 16) are then free of bank conflicts on gfx950, which a padded pitch of 80
+// bytes is not (measured). Global loads run two K groups ahead of the group being multiplied, in
+// two register sets.
 //
 // Per-group scale epilogue without an int->float conversion. The MFMA accumulator of group g
 // is seeded with the bit pattern of 1.5 * 2^23, so the int32 result D = seed + X reads as the
@@ -41,14 +44,15 @@ typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 
 constexpr int TM = 256, TN = 256, TK = 64;
 constexpr int NT = 512;                   // threads per workgroup
-constexpr int LROW = 80;                  // LDS pitch of A / B tile rows (bytes)
+constexpr int LROW = 64;                  // LDS pitch of A / B tile rows (bytes)
 constexpr int OROW = 136;                 // bf16 pitch of the output staging rows (128 + 8)
 constexpr int kSeed = 0x4B400000;         // bits of 1.5 * 2^23
 
+constexpr int NSTAGE = 3;                 // LDS ring of K groups
 struct alignas(16) Pipe {
-    alignas(16) int8_t a[2][TM * LROW];
-    alignas(16) int8_t b[2][TN * LROW];
-    alignas(16) float s[2][TN];
+    alignas(16) int8_t a[NSTAGE][TM * LROW];
+    alignas(16) int8_t b[NSTAGE][TN * LROW];
+    alignas(16) float s[NSTAGE][TN];
 };
 struct alignas(16) Smem {
     union alignas(16) {
@@ -200,10 +204,10 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     const int z_off = has_z && b_ok ? static_cast<int>(brow * a.ldwz) : kOob;
     const int s_off = has_s && b_ok ? static_cast<int>(brow * a.ldws * 2) : kOob;
 
+    // one register set carries a K group from its global load to its LDS store
     uint4 ra[2], rb[2];
     uint32_t rz = 0, rs = 0;
-#define MQ_GLOAD(g)                                                                                   \
-    gload_group<WK, EPI>(g, ra_rs, rb_rs, rz_rs, rs_rs, a_off, b8_off, b_off, z_off, s_off, ra, rb, rz, rs)
+#define MQ_GLOAD(g) gload_group<WK, EPI>(g, ra_rs, rb_rs, rz_rs, rs_rs, a_off, b8_off, b_off, z_off, s_off, ra, rb, rz, rs)
     // Activation layouts (group GEMMs): 0 = int8 codes; 1 = int4 codes, scaled by 16 here on their
     // way into LDS; 2 = int4 codes already stored as 16 * q and negated in odd groups (so the
     // weights are not negated). Signed int4 weights meet layout 2 as 16 * v (high-nibble form).
@@ -211,7 +215,9 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     const int gshift = kGroup ? group_shift(act_mode, WK) : 0;
     const float sfac = 1.0f / static_cast<float>(1 << gshift);
     float cs = 0.0f;   // sum_g (-1)^g s[n, g] for this thread's weight row (GroupScale)
-    auto lstore = [&](int buf, int g) {
+    // byte offset of 16-byte chunk c of tile row r in the swizzled LDS layout
+    auto lds_off = [](int r, int c) { return r * LROW + ((c ^ ((r >> 1) & 3)) << 4); };
+    auto lstore = [&](int stage, int g) {
         const bool neg = kGroup && (g & 1);
         const bool neg_w = neg && act_mode != 2;
 #pragma unroll
@@ -219,29 +225,34 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             uint4 v = ra[c];
             if (act_mode == 1) v = make_uint4((v.x << 4) & 0xf0f0f0f0u, (v.y << 4) & 0xf0f0f0f0u,
                                               (v.z << 4) & 0xf0f0f0f0u, (v.w << 4) & 0xf0f0f0f0u);
-            *reinterpret_cast<uint4*>(&sm.u.pipe.a[buf][(lrow + 128 * c) * LROW + lpart * 16]) = v;
+            *reinterpret_cast<uint4*>(&sm.u.pipe.a[stage][lds_off(lrow + 128 * c, lpart)]) = v;
         }
         if constexpr (kPacked) {
             uint4 u0, u1;
             unpack_weights<WK>(rb[0], rz, g, neg_w, act_mode == 2, u0, u1);
-            *reinterpret_cast<uint4*>(&sm.u.pipe.b[buf][brow * LROW + bhalf * 32]) = u0;
-            *reinterpret_cast<uint4*>(&sm.u.pipe.b[buf][brow * LROW + bhalf * 32 + 16]) = u1;
+            *reinterpret_cast<uint4*>(&sm.u.pipe.b[stage][lds_off(brow, 2 * bhalf)]) = u0;
+            *reinterpret_cast<uint4*>(&sm.u.pipe.b[stage][lds_off(brow, 2 * bhalf + 1)]) = u1;
         } else {
 #pragma unroll
             for (int c = 0; c < 2; ++c)
-                *reinterpret_cast<uint4*>(&sm.u.pipe.b[buf][(lrow + 128 * c) * LROW + lpart * 16]) = rb[c];
+                *reinterpret_cast<uint4*>(&sm.u.pipe.b[stage][lds_off(lrow + 128 * c, lpart)]) = rb[c];
         }
         if constexpr (EPI == Epi::GroupScale) {
             if (bhalf == 0) {
                 float sv = f16_bits_to_f32(static_cast<uint16_t>(rs)) * sfac;   // exact: power of two
                 sv = neg ? -sv : sv;
-                sm.u.pipe.s[buf][brow] = sv;
+                sm.u.pipe.s[stage][brow] = sv;
                 cs += sv;
             }
         }
     };
 
-    const int fr = lane & 15, fk = (lane >> 4) * 16;
+    // fragment reads: lane l reads chunk l / 16 of row l % 16 of a 16-row block (swizzle depends
+    // only on the row within the block, so one per-lane offset serves every block)
+    const int fr = lane & 15, fk = ((lane >> 4) ^ ((fr >> 1) & 3)) << 4;
+    const int a_frag = (wm * 64 + fr) * LROW + fk;    // + i * 16 * LROW
+    const int b_frag = (wn * 128 + fr) * LROW + fk;   // + j * 16 * LROW
+    const int s_frag = wn * 128 + fr;                 // + j * 16
     const v4i seed = {kSeed, kSeed, kSeed, kSeed};
 
     float acc[4][8][4];
@@ -257,77 +268,95 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             }
         }
 
+    // Fragment registers: A of the current K group (fragment i is refilled with group g + 1's right
+    // after its last MFMA in group g), and a 4-slot ring of B fragments and scales (slot = column
+    // % 4, 8 columns per group) read three columns ahead; the last columns of group g fetch
+    // columns 0-2 of group g + 1.
+    v4i fa[4], fb[4];
+    float fs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto read_a = [&](int stage, int i, v4i& dst) {
+        dst = *reinterpret_cast<const v4i*>(&sm.u.pipe.a[stage][a_frag + i * 16 * LROW]);
+    };
+    auto read_b = [&](int stage, int j, v4i& dst, float& sdst) {
+        dst = *reinterpret_cast<const v4i*>(&sm.u.pipe.b[stage][b_frag + j * 16 * LROW]);
+        if constexpr (EPI == Epi::GroupScale) sdst = sm.u.pipe.s[stage][s_frag + j * 16];
+    };
+
+    // prologue: groups 0 and 1 into LDS stages 0 and 1, group 2 in registers
     MQ_GLOAD(0);
     lstore(0, 0);
-    if (G > 1) MQ_GLOAD(1);
+    if (G > 1) {
+        MQ_GLOAD(1);
+        lstore(1, 1);
+    }
+    if (G > 2) MQ_GLOAD(2);
     __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) read_a(0, i, fa[i]);
+    read_b(0, 0, fb[0], fs[0]);
+    read_b(0, 1, fb[1], fs[1]);
+    read_b(0, 2, fb[2], fs[2]);
 
+    // K group g: 32 MFMA tiles t = 4 j + i, column-major. Tile t's MFMA is
+    // issued, then the fmas of tile t - 2 (its result has landed): MFMA and VALU work overlap and
+    // three tiles of results are live. After column 1 the stage of group g + 2 is filled from the
+    // register set and the global loads of group g + 3 are issued. One barrier per group: stage
+    // (g + 2) % 3 was last read before the previous barrier, group g + 1's stage was completed
+    // before it.
     for (int g = 0; g < G; ++g) {
-        const int buf = g & 1;
-        const int8_t* pa = &sm.u.pipe.a[buf][(wm * 64 + fr) * LROW + fk];
-        const int8_t* pb = &sm.u.pipe.b[buf][(wn * 128 + fr) * LROW + fk];
-        const float* ps = &sm.u.pipe.s[buf][wn * 128 + fr];
-        v4i af[4];
+        const int st = g % NSTAGE, st1 = (g + 1) % NSTAGE;
+        const bool has_next = g + 1 < G;
+        v4i d[3];
+        v4i seedv = seed;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const v4i*>(pa + i * 16 * LROW);
-        if constexpr (EPI == Epi::GroupScale) {
-            // 32 tiles t = 4 j + i in column-major order. Tile t's MFMA is issued, then the fmas of
-            // tile t - 2 (whose result has landed by then): MFMA and VALU work overlap, and only
-            // three tiles of results are live.
-            float sv[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) sv[j] = ps[j * 16];
-            v4i d[3];
-            v4i bf[2];
-            v4i seedv = seed;
-            bf[0] = *reinterpret_cast<const v4i*>(pb);
-#pragma unroll
-            for (int t = 0; t < 34; ++t) {
-                if (t < 32) {
-                    const int j = t >> 2, i = t & 3;
-                    // next column's B fragment, two tiles before it is needed
-                    if (i == 2 && j < 7) bf[(j + 1) & 1] = *reinterpret_cast<const v4i*>(pb + (j + 1) * 16 * LROW);
-                    // empty asm on the seed: the MFMA cannot be hoisted above this step
-                    asm volatile("" : "+v"(seedv));
-                    d[t % 3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j & 1], seedv, 0, 0, 0);
+        for (int t = 0; t < 34; ++t) {
+            if (t < 32) {
+                const int j = t >> 2, i = t & 3;
+                if (i == 2) {
+                    // three columns ahead, into the slot of column j - 1 (its last MFMA and fma
+                    // have been issued)
+                    const int jj = j + 3;
+                    if (jj < 8) read_b(st, jj, fb[jj & 3], fs[jj & 3]);
+                    else if (has_next) read_b(st1, jj - 8, fb[jj & 3], fs[jj & 3]);
                 }
+                if (t == 8) {
+                    if (g + 2 < G) lstore((g + 2) % NSTAGE, g + 2);
+                    if (g + 3 < G) MQ_GLOAD(g + 3);
+                }
+                // empty asm on the seed: the MFMA cannot be hoisted above this step
+                asm volatile("" : "+v"(seedv));
+                if constexpr (kGroup) {
+                    d[t % 3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j & 3], seedv, 0, 0, 0);
+                    if constexpr (EPI == Epi::GroupPartials) {
+                        const int64_t col = n0 + wn * 128 + j * 16 + fr;
+                        int32_t* part = a.part + static_cast<int64_t>(g) * M * N;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int64_t row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
+                            const int32_t pv = (d[t % 3][r] - kSeed) >> gshift;   // exact: a multiple of 2^gshift
+                            if (row < M && col < N) part[row * N + col] = (g & 1) ? -pv : pv;
+                        }
+                    }
+                } else {
+                    acci[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j & 3], acci[i][j], 0, 0, 0);
+                }
+                if (j == 7 && has_next) read_a(st1, i, fa[i]);   // fa[i]'s last use in group g
+            }
+            if constexpr (EPI == Epi::GroupScale) {
                 if (t >= 2) {
                     const int tp = t - 2, jp = tp >> 2, ip = tp & 3;
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        acc[ip][jp][r] = __builtin_fmaf(__int_as_float(d[tp % 3][r]), sv[jp], acc[ip][jp][r]);
+                        acc[ip][jp][r] = __builtin_fmaf(__int_as_float(d[tp % 3][r]), fs[jp & 3], acc[ip][jp][r]);
                     // empty asm on the accumulators: the fmas complete in this step (not sunk)
                     asm volatile("" : "+v"(acc[ip][jp][0]), "+v"(acc[ip][jp][1]), "+v"(acc[ip][jp][2]),
                                  "+v"(acc[ip][jp][3]));
                 }
             }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int bc = wn * 128 + j * 16 + fr;
-                const v4i bf = *reinterpret_cast<const v4i*>(pb + j * 16 * LROW);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if constexpr (kGroup) {
-                        const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf, seed, 0, 0, 0);
-                        const int64_t col = n0 + bc;
-                        int32_t* part = a.part + static_cast<int64_t>(g) * M * N;
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int64_t row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
-                            const int32_t p = (d[r] - kSeed) >> gshift;   // exact: a multiple of 2^gshift
-                            if (row < M && col < N) part[row * N + col] = (g & 1) ? -p : p;
-                        }
-                    } else {
-                        acci[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf, acci[i][j], 0, 0, 0);
-                    }
-                }
-            }
         }
-        if (g + 1 < G) lstore(buf ^ 1, g + 1);
-        if (g + 2 < G) MQ_GLOAD(g + 2);
         __syncthreads();
     }
+#undef MQ_GLOAD
 
     if constexpr (EPI == Epi::GroupPartials) return;
 
