@@ -32,6 +32,8 @@
 // kernel) stores 16 * q negated in odd groups, and signed int4 weights then enter as 16 * v. The
 // MFMA result is 2^gshift times the partial (gshift 4 or 8) and the scales are divided by the same
 // power of two, so every step stays exact.
+#include <type_traits>
+
 #include "mq_device.h"
 #include "mq_internal.h"
 
@@ -79,11 +81,10 @@ __device__ __forceinline__ void unpack_neg(uint32_t w, uint32_t zz80, uint32_t& 
 }
 
 // 32 packed 4-bit weights (16 bytes, one half of a row's K group) -> 32 int8 operands in k order.
-// U4Asym: q - z (or z - q when neg); I4Sym: v (or -v), or 16 * v when x16 (no negation then).
-template <WKind WK>
-__device__ __forceinline__ void unpack_weights(uint4 w, uint32_t rz, int g, bool neg, bool x16, uint4& u0,
-                                               uint4& u1) {
-    if (WK == WKind::I4Sym && x16) {
+// U4Asym: q - z (z - q when NEG); I4Sym: v (-v when NEG), or 16 * v when X16 (never negated).
+template <WKind WK, bool NEG, bool X16>
+__device__ __forceinline__ void unpack_weights(uint4 w, uint32_t zb, uint4& u0, uint4& u1) {
+    if constexpr (WK == WKind::I4Sym && X16) {
         const uint32_t in[4] = {w.x, w.y, w.z, w.w};
         uint32_t o[8];
 #pragma unroll
@@ -95,28 +96,25 @@ __device__ __forceinline__ void unpack_weights(uint4 w, uint32_t rz, int g, bool
         }
         u0 = make_uint4(o[0], o[1], o[2], o[3]);
         u1 = make_uint4(o[4], o[5], o[6], o[7]);
-        return;
-    }
-    uint32_t zb;
-    if constexpr (WK == WKind::U4Asym) {
-        zb = (rz >> ((g & 1) * 4)) & 0xfu;
     } else {
-        // signed nibble v -> v ^ 8 in [0, 15] with zero-point 8 (a zero-filled row stays 0)
-        w.x ^= 0x88888888u; w.y ^= 0x88888888u; w.z ^= 0x88888888u; w.w ^= 0x88888888u;
-        zb = 8u;
-    }
-    const uint32_t zz = zb * 0x01010101u;
-    if (neg) {
-        const uint32_t zz80 = zz | 0x80808080u;
-        unpack_neg(w.x, zz80, u0.x, u0.y);
-        unpack_neg(w.y, zz80, u0.z, u0.w);
-        unpack_neg(w.z, zz80, u1.x, u1.y);
-        unpack_neg(w.w, zz80, u1.z, u1.w);
-    } else {
-        unpack_pos(w.x, zz, u0.x, u0.y);
-        unpack_pos(w.y, zz, u0.z, u0.w);
-        unpack_pos(w.z, zz, u1.x, u1.y);
-        unpack_pos(w.w, zz, u1.z, u1.w);
+        if constexpr (WK == WKind::I4Sym) {
+            // signed nibble v -> v ^ 8 in [0, 15] with zero-point 8 (a zero-filled row stays 0)
+            w.x ^= 0x88888888u; w.y ^= 0x88888888u; w.z ^= 0x88888888u; w.w ^= 0x88888888u;
+            zb = 8u;
+        }
+        const uint32_t zz = zb * 0x01010101u;
+        if constexpr (NEG) {
+            const uint32_t zz80 = zz | 0x80808080u;
+            unpack_neg(w.x, zz80, u0.x, u0.y);
+            unpack_neg(w.y, zz80, u0.z, u0.w);
+            unpack_neg(w.z, zz80, u1.x, u1.y);
+            unpack_neg(w.w, zz80, u1.z, u1.w);
+        } else {
+            unpack_pos(w.x, zz, u0.x, u0.y);
+            unpack_pos(w.y, zz, u0.z, u0.w);
+            unpack_pos(w.z, zz, u1.x, u1.y);
+            unpack_pos(w.w, zz, u1.z, u1.w);
+        }
     }
 }
 
@@ -165,10 +163,14 @@ __device__ __forceinline__ void gload_group(int g, __amdgpu_buffer_rsrc_t ra_rs,
     if constexpr (EPI == Epi::GroupScale) rs = __builtin_amdgcn_raw_buffer_load_b16(rs_rs, s_off, 2 * g, 0);
 }
 
-template <WKind WK, Epi EPI>
+// One workgroup: a 256 x 256 output tile. AM is the activation layout of the group epilogues
+// (0 int8 codes; 1 int4 codes, scaled by 16 on their way into LDS; 2 int4 codes stored as 16 * q
+// and negated in odd groups, signed int4 weights then entering as 16 * v); row epilogues use 0.
+template <WKind WK, Epi EPI, int AM>
 __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, int tiles_n) {
     constexpr bool kGroup = EPI == Epi::GroupScale || EPI == Epi::GroupPartials;
     constexpr bool kPacked = WK != WKind::I8;
+    constexpr int kShift = kGroup ? (AM == 1 ? 4 : AM == 2 ? (WK == WKind::I4Sym ? 8 : 4) : 0) : 0;
     __shared__ Smem sm;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -208,28 +210,28 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     uint4 ra[2], rb[2];
     uint32_t rz = 0, rs = 0;
 #define MQ_GLOAD(g) gload_group<WK, EPI>(g, ra_rs, rb_rs, rz_rs, rs_rs, a_off, b8_off, b_off, z_off, s_off, ra, rb, rz, rs)
-    // Activation layouts (group GEMMs): 0 = int8 codes; 1 = int4 codes, scaled by 16 here on their
-    // way into LDS; 2 = int4 codes already stored as 16 * q and negated in odd groups (so the
-    // weights are not negated). Signed int4 weights meet layout 2 as 16 * v (high-nibble form).
-    const int act_mode = kGroup ? a.act_mode : 0;
-    const int gshift = kGroup ? group_shift(act_mode, WK) : 0;
-    const float sfac = 1.0f / static_cast<float>(1 << gshift);
+    constexpr float kSfac = 1.0f / static_cast<float>(1 << kShift);
     float cs = 0.0f;   // sum_g (-1)^g s[n, g] for this thread's weight row (GroupScale)
     // byte offset of 16-byte chunk c of tile row r in the swizzled LDS layout
     auto lds_off = [](int r, int c) { return r * LROW + ((c ^ ((r >> 1) & 3)) << 4); };
-    auto lstore = [&](int stage, int g) {
-        const bool neg = kGroup && (g & 1);
-        const bool neg_w = neg && act_mode != 2;
+    // Store the register set (group g_data, or a repeat of the last group past the end) into
+    // stage `stage`; NEG is the parity of the group the stage is for. `real` says whether that
+    // group exists (its scale then enters the offset sum).
+    auto lstore = [&](int stage, auto NEGC, bool real) {
+        constexpr bool neg = kGroup && decltype(NEGC)::value;
+        constexpr bool neg_w = neg && AM != 2;
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             uint4 v = ra[c];
-            if (act_mode == 1) v = make_uint4((v.x << 4) & 0xf0f0f0f0u, (v.y << 4) & 0xf0f0f0f0u,
-                                              (v.z << 4) & 0xf0f0f0f0u, (v.w << 4) & 0xf0f0f0f0u);
+            if constexpr (AM == 1 && kGroup)
+                v = make_uint4((v.x << 4) & 0xf0f0f0f0u, (v.y << 4) & 0xf0f0f0f0u, (v.z << 4) & 0xf0f0f0f0u,
+                               (v.w << 4) & 0xf0f0f0f0u);
             *reinterpret_cast<uint4*>(&sm.u.pipe.a[stage][lds_off(lrow + 128 * c, lpart)]) = v;
         }
         if constexpr (kPacked) {
             uint4 u0, u1;
-            unpack_weights<WK>(rb[0], rz, g, neg_w, act_mode == 2, u0, u1);
+            const uint32_t zb = (rz >> (neg ? 4 : 0)) & 0xfu;
+            unpack_weights<WK, neg_w, AM == 2 && kGroup>(rb[0], zb, u0, u1);
             *reinterpret_cast<uint4*>(&sm.u.pipe.b[stage][lds_off(brow, 2 * bhalf)]) = u0;
             *reinterpret_cast<uint4*>(&sm.u.pipe.b[stage][lds_off(brow, 2 * bhalf + 1)]) = u1;
         } else {
@@ -238,12 +240,11 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
                 *reinterpret_cast<uint4*>(&sm.u.pipe.b[stage][lds_off(lrow + 128 * c, lpart)]) = rb[c];
         }
         if constexpr (EPI == Epi::GroupScale) {
-            if (bhalf == 0) {
-                float sv = f16_bits_to_f32(static_cast<uint16_t>(rs)) * sfac;   // exact: power of two
-                sv = neg ? -sv : sv;
-                sm.u.pipe.s[stage][brow] = sv;
-                cs += sv;
-            }
+            // both threads of a row store the same value (no divergent branch)
+            float sv = f16_bits_to_f32(static_cast<uint16_t>(rs)) * kSfac;   // exact: power of two
+            sv = neg ? -sv : sv;
+            sm.u.pipe.s[stage][brow] = sv;
+            cs += real ? sv : 0.0f;
         }
     };
 
@@ -268,10 +269,10 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             }
         }
 
-    // Fragment registers: A of the current K group (fragment i is refilled with group g + 1's right
-    // after its last MFMA in group g), and a 4-slot ring of B fragments and scales (slot = column
-    // % 4, 8 columns per group) read three columns ahead; the last columns of group g fetch
-    // columns 0-2 of group g + 1.
+    // Fragment registers: A of the current K group (fragment i is refilled with group g + 1's
+    // right after its last MFMA in group g), and a 4-slot ring of B fragments and scales (slot =
+    // column % 4, 8 columns per group) read two columns ahead; the last two columns of group g
+    // fetch columns 0 and 1 of group g + 1.
     v4i fa[4], fb[4];
     float fs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     auto read_a = [&](int stage, int i, v4i& dst) {
@@ -281,80 +282,88 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         dst = *reinterpret_cast<const v4i*>(&sm.u.pipe.b[stage][b_frag + j * 16 * LROW]);
         if constexpr (EPI == Epi::GroupScale) sdst = sm.u.pipe.s[stage][s_frag + j * 16];
     };
+    using T0 = std::integral_constant<int, 0>;
+    using T1 = std::integral_constant<int, 1>;
 
-    // prologue: groups 0 and 1 into LDS stages 0 and 1, group 2 in registers
+    // prologue: groups 0 and 1 into LDS stages 0 and 1, group 2 in registers (group indices are
+    // clamped to the last group: the repeats are never read)
+    const int glast = G - 1;
     MQ_GLOAD(0);
-    lstore(0, 0);
-    if (G > 1) {
-        MQ_GLOAD(1);
-        lstore(1, 1);
-    }
-    if (G > 2) MQ_GLOAD(2);
+    lstore(0, T0{}, true);
+    MQ_GLOAD(1 < glast ? 1 : glast);
+    lstore(1, T1{}, G > 1);
+    MQ_GLOAD(2 < glast ? 2 : glast);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i) read_a(0, i, fa[i]);
     read_b(0, 0, fb[0], fs[0]);
     read_b(0, 1, fb[1], fs[1]);
-    read_b(0, 2, fb[2], fs[2]);
 
-    // K group g: 32 MFMA tiles t = 4 j + i, column-major. Tile t's MFMA is
-    // issued, then the fmas of tile t - 2 (its result has landed): MFMA and VALU work overlap and
-    // three tiles of results are live. After column 1 the stage of group g + 2 is filled from the
-    // register set and the global loads of group g + 3 are issued. One barrier per group: stage
+    // K group g: 32 MFMA tiles t = 4 j + i, column-major. Every step issues tile t's MFMA, then the
+    // fmas of tile t - 1 (MFMA and VALU work overlap, two tiles of results are live); a scheduling
+    // fence after each step keeps every LDS read and store where it is written, so the reads really
+    // run two columns ahead. After column 1 the stage of group g + 2 is filled from the register
+    // set and the global loads of group g + 3 are issued. One barrier per group: stage
     // (g + 2) % 3 was last read before the previous barrier, group g + 1's stage was completed
-    // before it.
-    for (int g = 0; g < G; ++g) {
-        const int st = g % NSTAGE, st1 = (g + 1) % NSTAGE;
-        const bool has_next = g + 1 < G;
-        v4i d[3];
+    // before it. The body is branch-free: past the last group, loads and stores repeat the last
+    // group (never read), so each group is one scheduling region.
+    auto step = [&](int g, auto P) {
+        constexpr int par = decltype(P)::value;   // g & 1
+        const int st = g % NSTAGE, st1 = (g + 1) % NSTAGE, st2 = (g + 2) % NSTAGE;
+        constexpr int LAG = 1;   // tile t's fmas run LAG steps after its MFMA
+        v4i d[LAG + 1];
         v4i seedv = seed;
 #pragma unroll
-        for (int t = 0; t < 34; ++t) {
+        for (int t = 0; t < 32 + LAG; ++t) {
             if (t < 32) {
                 const int j = t >> 2, i = t & 3;
-                if (i == 2) {
-                    // three columns ahead, into the slot of column j - 1 (its last MFMA and fma
-                    // have been issued)
-                    const int jj = j + 3;
+                if (i == 0) {
+                    // two columns ahead, into the slot of column j - 2 (its MFMAs and fmas are done)
+                    const int jj = j + 2;
                     if (jj < 8) read_b(st, jj, fb[jj & 3], fs[jj & 3]);
-                    else if (has_next) read_b(st1, jj - 8, fb[jj & 3], fs[jj & 3]);
+                    else read_b(st1, jj - 8, fb[jj & 3], fs[jj & 3]);
                 }
                 if (t == 8) {
-                    if (g + 2 < G) lstore((g + 2) % NSTAGE, g + 2);
-                    if (g + 3 < G) MQ_GLOAD(g + 3);
+                    lstore(st2, std::integral_constant<int, par>{}, g + 2 < G);
+                    MQ_GLOAD(g + 3 < glast ? g + 3 : glast);
                 }
                 // empty asm on the seed: the MFMA cannot be hoisted above this step
                 asm volatile("" : "+v"(seedv));
                 if constexpr (kGroup) {
-                    d[t % 3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j & 3], seedv, 0, 0, 0);
+                    d[t % (LAG + 1)] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j & 3], seedv, 0, 0, 0);
                     if constexpr (EPI == Epi::GroupPartials) {
                         const int64_t col = n0 + wn * 128 + j * 16 + fr;
                         int32_t* part = a.part + static_cast<int64_t>(g) * M * N;
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             const int64_t row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
-                            const int32_t pv = (d[t % 3][r] - kSeed) >> gshift;   // exact: a multiple of 2^gshift
-                            if (row < M && col < N) part[row * N + col] = (g & 1) ? -pv : pv;
+                            const int32_t pv = (d[t % (LAG + 1)][r] - kSeed) >> kShift;   // exact: a multiple of 2^kShift
+                            if (row < M && col < N) part[row * N + col] = par ? -pv : pv;
                         }
                     }
                 } else {
                     acci[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j & 3], acci[i][j], 0, 0, 0);
                 }
-                if (j == 7 && has_next) read_a(st1, i, fa[i]);   // fa[i]'s last use in group g
+                if (j == 7) read_a(st1, i, fa[i]);   // fa[i]'s last use in group g
             }
             if constexpr (EPI == Epi::GroupScale) {
-                if (t >= 2) {
-                    const int tp = t - 2, jp = tp >> 2, ip = tp & 3;
+                if (t >= LAG) {
+                    const int tp = t - LAG, jp = tp >> 2, ip = tp & 3;
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        acc[ip][jp][r] = __builtin_fmaf(__int_as_float(d[tp % 3][r]), fs[jp & 3], acc[ip][jp][r]);
+                        acc[ip][jp][r] = __builtin_fmaf(__int_as_float(d[tp % (LAG + 1)][r]), fs[jp & 3], acc[ip][jp][r]);
                     // empty asm on the accumulators: the fmas complete in this step (not sunk)
                     asm volatile("" : "+v"(acc[ip][jp][0]), "+v"(acc[ip][jp][1]), "+v"(acc[ip][jp][2]),
                                  "+v"(acc[ip][jp][3]));
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
         __syncthreads();
+    };
+    for (int g = 0; g < G; g += 2) {
+        step(g, T0{});
+        if (g + 1 < G) step(g + 1, T1{});
     }
 #undef MQ_GLOAD
 
@@ -444,41 +453,48 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     }
 }
 
-template <WKind WK>
-int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
+template <WKind WK, Epi EPI, int AM>
+int launch_one(const GemmArgs& a, hipStream_t stream) {
     const int tiles_m = static_cast<int>((a.M + TM - 1) / TM);
     const int tiles_n = static_cast<int>((a.N + TN - 1) / TN);
-    const dim3 grid(static_cast<unsigned>(tiles_m * tiles_n));
-    const dim3 block(NT);
-    switch (epi) {
-        case Epi::GroupScale:
-            hipLaunchKernelGGL((gemm_wide_kernel<WK, Epi::GroupScale>), grid, block, 0, stream, a, tiles_m, tiles_n);
-            break;
-        case Epi::GroupPartials:
-            hipLaunchKernelGGL((gemm_wide_kernel<WK, Epi::GroupPartials>), grid, block, 0, stream, a, tiles_m,
-                               tiles_n);
-            break;
-        case Epi::RowScale:
-            hipLaunchKernelGGL((gemm_wide_kernel<WK, Epi::RowScale>), grid, block, 0, stream, a, tiles_m, tiles_n);
-            break;
-        case Epi::RowAcc:
-            hipLaunchKernelGGL((gemm_wide_kernel<WK, Epi::RowAcc>), grid, block, 0, stream, a, tiles_m, tiles_n);
-            break;
-    }
+    hipLaunchKernelGGL((gemm_wide_kernel<WK, EPI, AM>), dim3(static_cast<unsigned>(tiles_m * tiles_n)), dim3(NT), 0,
+                       stream, a, tiles_m, tiles_n);
     return launch_status("gemm_wide");
+}
+
+template <WKind WK, Epi EPI>
+int launch_group(const GemmArgs& a, hipStream_t stream) {
+    switch (a.act_mode) {
+        case 0: return launch_one<WK, EPI, 0>(a, stream);
+        case 1: return launch_one<WK, EPI, 1>(a, stream);
+        case 2: return launch_one<WK, EPI, 2>(a, stream);
+        default: break;
+    }
+    set_error("gemm: unknown activation layout %d", a.act_mode);
+    return -1;
+}
+
+template <WKind WK>
+int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
+    if constexpr (WK != WKind::I8) {   // 4-bit weights: per-group scales
+        if (epi == Epi::GroupScale) return launch_group<WK, Epi::GroupScale>(a, stream);
+        if (epi == Epi::GroupPartials) return launch_group<WK, Epi::GroupPartials>(a, stream);
+    }
+    if constexpr (WK != WKind::U4Asym) {   // full-K accumulators: signed int4 or int8 weights
+        if (epi == Epi::RowScale) return launch_one<WK, Epi::RowScale, 0>(a, stream);
+        if (epi == Epi::RowAcc) return launch_one<WK, Epi::RowAcc, 0>(a, stream);
+    }
+    set_error("gemm: unsupported weight kind / epilogue combination");
+    return -2;
 }
 
 }  // namespace
 
 int launch_gemm_wide(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     switch (wk) {
-        case WKind::U4Asym:
-            if (epi == Epi::RowScale || epi == Epi::RowAcc) break;
-            return launch_wk<WKind::U4Asym>(a, epi, stream);
+        case WKind::U4Asym: return launch_wk<WKind::U4Asym>(a, epi, stream);
         case WKind::I4Sym: return launch_wk<WKind::I4Sym>(a, epi, stream);
-        case WKind::I8:
-            if (epi == Epi::GroupScale || epi == Epi::GroupPartials) break;
-            return launch_wk<WKind::I8>(a, epi, stream);
+        case WKind::I8: return launch_wk<WKind::I8>(a, epi, stream);
     }
     set_error("gemm: unsupported weight kind / epilogue combination");
     return -2;
