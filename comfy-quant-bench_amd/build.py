@@ -9,6 +9,7 @@ multiply-add the kernels want is written explicitly.
 """
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
@@ -45,28 +46,37 @@ def flags() -> list[str]:
     ]
 
 
+def _compile(src: str, build_dir: str, verbose: bool) -> str:
+    obj = os.path.join(build_dir, src.replace(".hip", ".o"))
+    cmd = [hipcc(), *flags(), "-c", os.path.join(CSRC, src), "-o", obj]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
+    noise = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln and ln.strip()]
+    if noise and verbose:
+        print("\n".join(noise), file=sys.stderr)
+    return obj
+
+
 def build(verbose: bool = False) -> str:
-    """Compile every source and link libmq.so; returns its path. Always recompiles."""
-    objs = []
+    """Compile every source (in parallel) and link libmq.so; returns its path. Always recompiles."""
     build_dir = os.path.join(HERE, "_build")
     os.makedirs(build_dir, exist_ok=True)
-    for src in SOURCES:
-        obj = os.path.join(build_dir, src.replace(".hip", ".o"))
-        cmd = [hipcc(), *flags(), "-c", os.path.join(CSRC, src), "-o", obj]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        res = subprocess.run(cmd, capture_output=True, text=True)
-        if res.returncode != 0:
-            raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
-        noise = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln and ln.strip()]
-        if noise and verbose:
-            print("\n".join(noise), file=sys.stderr)
-        objs.append(obj)
+    workers = max(1, min(len(SOURCES), os.cpu_count() or 1))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
+        objs = list(pool.map(lambda src: _compile(src, build_dir, verbose), SOURCES))
     tmp = OUT + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
+    # a kernel whose host-side stub was dropped leaves an undefined mq:: symbol behind
+    undef = subprocess.run(["nm", "-D", "--undefined-only", tmp], capture_output=True, text=True).stdout
+    missing = [ln.split()[-1] for ln in undef.splitlines() if "_ZN2mq" in ln]
+    if missing:
+        raise RuntimeError("libmq.so has undefined library symbols: " + ", ".join(missing[:4]))
     os.replace(tmp, OUT)
     return OUT
 

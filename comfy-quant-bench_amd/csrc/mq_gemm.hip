@@ -263,7 +263,8 @@ int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     const int64_t wbytes = wk == WKind::I8 ? a.K : a.K / 2;
     const bool fits32 = a.M * a.lda < (int64_t(1) << 31) && a.N * a.ldw < (int64_t(1) << 31) &&
                         (a.N * a.ldws + a.K / 64) * 2 < (int64_t(1) << 31) && wbytes <= a.ldw;
-    if (a.M > 128 && fits32) return launch_gemm_wide(a, wk, epi, stream);
+    // (activation layout 1, int4 codes scaled in the kernel, is served by the 128-tile kernel only)
+    if (a.M > 128 && fits32 && a.act_mode != 1) return launch_gemm_wide(a, wk, epi, stream);
     switch (wk) {
         case WKind::U4Asym:
             if (epi == Epi::RowScale || epi == Epi::RowAcc) break;

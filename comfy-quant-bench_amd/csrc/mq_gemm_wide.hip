@@ -5,11 +5,20 @@
 // Layout. Waves form a 4 (M) x 2 (N) grid; each owns a 64 x 128 output tile made of 4 x 8 MFMA
 // 16x16 tiles. In the 16x16 output layout lane l holds column l % 16 and rows 4 * (l / 16) + r,
 // r = 0..3, so every lane needs one weight scale per column tile. A (int8 activation codes) and
-// B (weights, unpacked to int8 on their way into LDS) are double-buffered in LDS as 64-byte rows
+// B (weights, unpacked to int8 on their way into LDS) live in a 3-stage LDS ring of 64-byte rows
 // whose four 16-byte chunks are XOR-swizzled by (row >> 1) & 3: the fragment reads (lane l reads
 // chunk l / 16 of row l % 16) are then free of bank conflicts on gfx950, which a padded pitch of 80
-// bytes is not (measured). Global loads run two K groups ahead of the group being multiplied, in
-// two register sets.
+// bytes is not (measured).
+//
+// Pipeline. The main loop is unrolled over six K groups, so the LDS stage (g % 3) and the sign
+// parity (g % 2) of every group are compile-time constants and every LDS access is a base register
+// plus an immediate offset. Inside a group the 32 MFMA tiles run column by column (t = 4 j + i);
+// step t issues tile t's MFMA and then the fmas of tile t - 3, so a result is read three MFMAs
+// after it was produced (no wait states) while the MFMA and VALU pipes overlap. B fragments and
+// scales sit in a 4-slot register ring read two columns ahead; A fragments of group g + 1 are
+// read right after their last MFMA in group g. Global loads of group g + 3 are issued in group g,
+// stored (B unpacked) into the stage of group g + 2 at steps 8-11, and one barrier per group
+// closes the ring.
 //
 // Per-group scale epilogue without an int->float conversion. The MFMA accumulator of group g
 // is seeded with the bit pattern of 1.5 * 2^23, so the int32 result D = seed + X reads as the
@@ -46,23 +55,24 @@ typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 
 constexpr int TM = 256, TN = 256, TK = 64;
 constexpr int NT = 512;                   // threads per workgroup
-constexpr int LROW = 64;                  // LDS pitch of A / B tile rows (bytes)
-constexpr int OROW = 136;                 // bf16 pitch of the output staging rows (128 + 8)
+constexpr int LAG = 3;                    // tile t's fmas run LAG MFMAs after it
 constexpr int kSeed = 0x4B400000;         // bits of 1.5 * 2^23
 
-constexpr int NSTAGE = 3;                 // LDS ring of K groups
-struct alignas(16) Pipe {
-    alignas(16) int8_t a[NSTAGE][TM * LROW];
-    alignas(16) int8_t b[NSTAGE][TN * LROW];
-    alignas(16) float s[NSTAGE][TN];
-};
-struct alignas(16) Smem {
-    union alignas(16) {
-        Pipe pipe;
-        alignas(16) uint16_t out[8][64 * OROW];
-    } u;
-    alignas(16) float corr[TN];
-};
+// LDS map (bytes): 4-stage rings of A tiles, unpacked B tiles and fp32 scales. The output staging
+// of the epilogue reuses the ring region.
+constexpr int NSTAGE = 4;
+constexpr int TILE_BYTES = TM * TK;                       // one A or B stage: 256 rows x 64 bytes
+constexpr int A_LDS = 0;
+constexpr int B_LDS = A_LDS + NSTAGE * TILE_BYTES;        // 65536
+constexpr int S_LDS = B_LDS + NSTAGE * TILE_BYTES;        // 131072: fp32 scales, 1 KB per stage
+constexpr int PIPE_END = S_LDS + NSTAGE * TN * 4;         // 135168
+constexpr int OROW = 136;                                 // bf16 pitch of the output staging rows
+constexpr int OUT_END = 8 * 64 * OROW * 2;                // 139264
+constexpr int C_LDS = PIPE_END > OUT_END ? PIPE_END : OUT_END;   // per-column offset correction
+constexpr int SMEM_BYTES = C_LDS + TN * 4;
+
+// byte offset of 16-byte chunk c of tile row r in the swizzled layout
+__device__ __forceinline__ int lds_off(int r, int c) { return r * TK + ((c ^ ((r >> 1) & 3)) << 4); }
 
 __device__ __forceinline__ void unpack_pos(uint32_t w, uint32_t zz, uint32_t& o0, uint32_t& o1) {
     uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
@@ -80,41 +90,24 @@ __device__ __forceinline__ void unpack_neg(uint32_t w, uint32_t zz80, uint32_t& 
     o1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
 }
 
-// 32 packed 4-bit weights (16 bytes, one half of a row's K group) -> 32 int8 operands in k order.
+// 8 packed 4-bit weights (one dword) -> 8 int8 operands in k order (two dwords).
 // U4Asym: q - z (z - q when NEG); I4Sym: v (-v when NEG), or 16 * v when X16 (never negated).
 template <WKind WK, bool NEG, bool X16>
-__device__ __forceinline__ void unpack_weights(uint4 w, uint32_t zb, uint4& u0, uint4& u1) {
+__device__ __forceinline__ void unpack_dword(uint32_t w, uint32_t zb, uint32_t& o0, uint32_t& o1) {
     if constexpr (WK == WKind::I4Sym && X16) {
-        const uint32_t in[4] = {w.x, w.y, w.z, w.w};
-        uint32_t o[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            // a nibble moved to the high half of its byte reads as 16 x its signed value
-            const uint32_t lo = (in[e] << 4) & 0xf0f0f0f0u, hi = in[e] & 0xf0f0f0f0u;
-            o[2 * e] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
-            o[2 * e + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
-        }
-        u0 = make_uint4(o[0], o[1], o[2], o[3]);
-        u1 = make_uint4(o[4], o[5], o[6], o[7]);
+        // a nibble moved to the high half of its byte reads as 16 x its signed value
+        const uint32_t lo = (w << 4) & 0xf0f0f0f0u, hi = w & 0xf0f0f0f0u;
+        o0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+        o1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
     } else {
         if constexpr (WK == WKind::I4Sym) {
             // signed nibble v -> v ^ 8 in [0, 15] with zero-point 8 (a zero-filled row stays 0)
-            w.x ^= 0x88888888u; w.y ^= 0x88888888u; w.z ^= 0x88888888u; w.w ^= 0x88888888u;
+            w ^= 0x88888888u;
             zb = 8u;
         }
-        const uint32_t zz = zb * 0x01010101u;
-        if constexpr (NEG) {
-            const uint32_t zz80 = zz | 0x80808080u;
-            unpack_neg(w.x, zz80, u0.x, u0.y);
-            unpack_neg(w.y, zz80, u0.z, u0.w);
-            unpack_neg(w.z, zz80, u1.x, u1.y);
-            unpack_neg(w.w, zz80, u1.z, u1.w);
-        } else {
-            unpack_pos(w.x, zz, u0.x, u0.y);
-            unpack_pos(w.y, zz, u0.z, u0.w);
-            unpack_pos(w.z, zz, u1.x, u1.y);
-            unpack_pos(w.w, zz, u1.z, u1.w);
-        }
+        const uint32_t zz = __builtin_amdgcn_perm(0u, zb, 0u);   // byte 0 of zb in every byte
+        if constexpr (NEG) unpack_neg(w, zz | 0x80808080u, o0, o1);
+        else unpack_pos(w, zz, o0, o1);
     }
 }
 
@@ -144,36 +137,50 @@ __device__ __forceinline__ uint4 ld128(__amdgpu_buffer_rsrc_t r, int voff, int s
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// Global loads of K group g into registers (A: two 16-byte chunks; B: one packed or two int8
-// chunks; the zero-point byte and fp16 scale of this thread's weight row).
-template <WKind WK, Epi EPI>
-__device__ __forceinline__ void gload_group(int g, __amdgpu_buffer_rsrc_t ra_rs, __amdgpu_buffer_rsrc_t rb_rs,
-                                            __amdgpu_buffer_rsrc_t rz_rs, __amdgpu_buffer_rsrc_t rs_rs,
-                                            const int (&a_off)[2], const int (&b8_off)[2], int b_off, int z_off,
-                                            int s_off, uint4 (&ra)[2], uint4 (&rb)[2], uint32_t& rz, uint32_t& rs) {
-#pragma unroll
-    for (int c = 0; c < 2; ++c) ra[c] = ld128(ra_rs, a_off[c], g * TK);
-    if constexpr (WK != WKind::I8) {
-        rb[0] = ld128(rb_rs, b_off, g * (TK / 2));
-    } else {
-#pragma unroll
-        for (int c = 0; c < 2; ++c) rb[c] = ld128(rb_rs, b8_off[c], g * TK);
-    }
-    if constexpr (WK == WKind::U4Asym) rz = __builtin_amdgcn_raw_buffer_load_b8(rz_rs, z_off, g >> 1, 0);
-    if constexpr (EPI == Epi::GroupScale) rs = __builtin_amdgcn_raw_buffer_load_b16(rs_rs, s_off, 2 * g, 0);
+// 16 bytes per lane from buffer r at voff + soff straight into LDS: lane l writes bytes
+// [lds_off + 16 l, lds_off + 16 l + 16) (lds_off is wave-uniform; it becomes M0).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* smem, int lds_off, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(smem + lds_off), 16, voff,
+                                             soff, 0, 0);
+}
+
+// LDS stores written as inline asm. The compiler orders every LDS access after a pending LDS DMA
+// (buffer_load ... lds) by waiting for the DMA to complete; these stores never alias a DMA in
+// flight (different ring region or stage), and their completion is awaited explicitly.
+__device__ __forceinline__ void ds_write16(int base, int imm, uint4 v) {
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    const u4v x = {v.x, v.y, v.z, v.w};
+    if (imm == 0) asm volatile("ds_write_b128 %0, %1" ::"v"(base), "v"(x) : "memory");
+    else if (imm == 1 * TM * TK) asm volatile("ds_write_b128 %0, %1 offset:16384" ::"v"(base), "v"(x) : "memory");
+    else if (imm == 2 * TM * TK) asm volatile("ds_write_b128 %0, %1 offset:32768" ::"v"(base), "v"(x) : "memory");
+    else asm volatile("ds_write_b128 %0, %1 offset:49152" ::"v"(base), "v"(x) : "memory");
+}
+__device__ __forceinline__ void ds_write4(int base, int imm, float v) {
+    if (imm == 0) asm volatile("ds_write_b32 %0, %1" ::"v"(base), "v"(v) : "memory");
+    else if (imm == 1 * TN * 4) asm volatile("ds_write_b32 %0, %1 offset:1024" ::"v"(base), "v"(v) : "memory");
+    else if (imm == 2 * TN * 4) asm volatile("ds_write_b32 %0, %1 offset:2048" ::"v"(base), "v"(v) : "memory");
+    else asm volatile("ds_write_b32 %0, %1 offset:3072" ::"v"(base), "v"(v) : "memory");
+}
+
+template <typename T>
+__device__ __forceinline__ T& lds(uint8_t* smem, int off) {
+    return *reinterpret_cast<T*>(smem + off);
 }
 
 // One workgroup: a 256 x 256 output tile. AM is the activation layout of the group epilogues
-// (0 int8 codes; 1 int4 codes, scaled by 16 on their way into LDS; 2 int4 codes stored as 16 * q
-// and negated in odd groups, signed int4 weights then entering as 16 * v); row epilogues use 0.
+// (0 int8 codes; 2 int4 codes stored as 16 * q and negated in odd groups, signed int4 weights then
+// entering as 16 * v); row epilogues use 0.
 template <WKind WK, Epi EPI, int AM>
 __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, int tiles_n) {
+    static_assert(AM == 0 || AM == 2, "activation layout 1 is served by the 128-tile kernel");
     constexpr bool kGroup = EPI == Epi::GroupScale || EPI == Epi::GroupPartials;
     constexpr bool kPacked = WK != WKind::I8;
-    constexpr int kShift = kGroup ? (AM == 1 ? 4 : AM == 2 ? (WK == WKind::I4Sym ? 8 : 4) : 0) : 0;
-    __shared__ Smem sm;
+    constexpr int kShift = kGroup && AM == 2 ? (WK == WKind::I4Sym ? 8 : 4) : 0;
+    constexpr float kSfac = 1.0f / static_cast<float>(1 << kShift);
+    __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM_BYTES];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     int tm, tn;
     map_tile(static_cast<int>(blockIdx.x), tiles_m, tiles_n, tm, tn);
@@ -183,19 +190,25 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     const int rows_m = M - m0 < TM ? static_cast<int>(M - m0) : TM;   // valid rows of this tile
     const int rows_n = N - n0 < TN ? static_cast<int>(N - n0) : TN;
     const int kbytes_w = kPacked ? static_cast<int>(a.K / 2) : static_cast<int>(a.K);
-
-    // ---- loader roles. A (and I8 B): chunks tid and tid + 512 of 16 bytes, 4 per 64-byte row.
-    const int lrow = tid >> 2, lpart = tid & 3;
-    const int brow = tid >> 1, bhalf = tid & 1;   // packed B: 2 threads per weight row
     const auto ra_rs = rsrc(a.qa + m0 * a.lda, (rows_m - 1) * a.lda + a.K);
     const auto rb_rs = rsrc(a.qw + n0 * a.ldw, (rows_n - 1) * a.ldw + kbytes_w);
-    int a_off[2], b8_off[2];
+
+    // ---- DMA roles (A, and int8 B): wave w copies tile rows [32 w, 32 w + 32) of a K group as two
+    // 1 KB blocks. Lane l of block h writes LDS bytes [16 l, 16 l + 16) of tile rows
+    // 32 w + 16 h + l / 4; that is physical chunk l % 4 of the swizzled row, so it fetches logical
+    // chunk (l % 4) ^ swizzle(row).
+    int dma_a[2], dma_b[2];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        const int r = lrow + 128 * c;
-        a_off[c] = r < rows_m ? static_cast<int>(r * a.lda) + lpart * 16 : kOob;
-        b8_off[c] = r < rows_n ? static_cast<int>(r * a.ldw) + lpart * 16 : kOob;
+    for (int h = 0; h < 2; ++h) {
+        const int r = 32 * wave + 16 * h + (lane >> 2);
+        const int c = (lane & 3) ^ ((r >> 1) & 3);
+        dma_a[h] = r < rows_m ? static_cast<int>(r * a.lda) + c * 16 : kOob;
+        dma_b[h] = r < rows_n ? static_cast<int>(r * a.ldw) + c * 16 : kOob;
     }
+    const int dma_lds = (32 * wave) * TK;   // + 16 * TK for block 1
+
+    // ---- packed B roles: 2 threads per weight row, 16 packed bytes (32 weights) each
+    const int brow = tid >> 1, bhalf = tid & 1;
     const bool b_ok = brow < rows_n;
     const int b_off = b_ok ? static_cast<int>(brow * a.ldw) + bhalf * 16 : kOob;
     // zero-points and scales (null for the kinds that have none: the range is then empty)
@@ -205,56 +218,71 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
                             has_s ? ((rows_n - 1) * a.ldws + G) * 2 : 0);
     const int z_off = has_z && b_ok ? static_cast<int>(brow * a.ldwz) : kOob;
     const int s_off = has_s && b_ok ? static_cast<int>(brow * a.ldws * 2) : kOob;
-
-    // one register set carries a K group from its global load to its LDS store
-    uint4 ra[2], rb[2];
-    uint32_t rz = 0, rs = 0;
-#define MQ_GLOAD(g) gload_group<WK, EPI>(g, ra_rs, rb_rs, rz_rs, rs_rs, a_off, b8_off, b_off, z_off, s_off, ra, rb, rz, rs)
-    constexpr float kSfac = 1.0f / static_cast<float>(1 << kShift);
-    float cs = 0.0f;   // sum_g (-1)^g s[n, g] for this thread's weight row (GroupScale)
-    // byte offset of 16-byte chunk c of tile row r in the swizzled LDS layout
-    auto lds_off = [](int r, int c) { return r * LROW + ((c ^ ((r >> 1) & 3)) << 4); };
-    // Store the register set (group g_data, or a repeat of the last group past the end) into
-    // stage `stage`; NEG is the parity of the group the stage is for. `real` says whether that
-    // group exists (its scale then enters the offset sum).
-    auto lstore = [&](int stage, auto NEGC, bool real) {
-        constexpr bool neg = kGroup && decltype(NEGC)::value;
-        constexpr bool neg_w = neg && AM != 2;
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            uint4 v = ra[c];
-            if constexpr (AM == 1 && kGroup)
-                v = make_uint4((v.x << 4) & 0xf0f0f0f0u, (v.y << 4) & 0xf0f0f0f0u, (v.z << 4) & 0xf0f0f0f0u,
-                               (v.w << 4) & 0xf0f0f0f0u);
-            *reinterpret_cast<uint4*>(&sm.u.pipe.a[stage][lds_off(lrow + 128 * c, lpart)]) = v;
-        }
-        if constexpr (kPacked) {
-            uint4 u0, u1;
-            const uint32_t zb = (rz >> (neg ? 4 : 0)) & 0xfu;
-            unpack_weights<WK, neg_w, AM == 2 && kGroup>(rb[0], zb, u0, u1);
-            *reinterpret_cast<uint4*>(&sm.u.pipe.b[stage][lds_off(brow, 2 * bhalf)]) = u0;
-            *reinterpret_cast<uint4*>(&sm.u.pipe.b[stage][lds_off(brow, 2 * bhalf + 1)]) = u1;
-        } else {
-#pragma unroll
-            for (int c = 0; c < 2; ++c)
-                *reinterpret_cast<uint4*>(&sm.u.pipe.b[stage][lds_off(lrow + 128 * c, lpart)]) = rb[c];
-        }
-        if constexpr (EPI == Epi::GroupScale) {
-            // both threads of a row store the same value (no divergent branch)
-            float sv = f16_bits_to_f32(static_cast<uint16_t>(rs)) * kSfac;   // exact: power of two
-            sv = neg ? -sv : sv;
-            sm.u.pipe.s[stage][brow] = sv;
-            cs += real ? sv : 0.0f;
-        }
-    };
+    const int b_st00 = B_LDS + lds_off(brow, 2 * bhalf);
+    const int b_st10 = B_LDS + lds_off(brow, 2 * bhalf + 1);
+    // scales stored transposed, [wn][column % 16][column tile], so a lane's 8 scales are adjacent
+    const int s_st0 = S_LDS + 4 * ((((brow >> 7) * 16) + (brow & 15)) * 8 + ((brow & 127) >> 4));
 
     // fragment reads: lane l reads chunk l / 16 of row l % 16 of a 16-row block (swizzle depends
     // only on the row within the block, so one per-lane offset serves every block)
     const int fr = lane & 15, fk = ((lane >> 4) ^ ((fr >> 1) & 3)) << 4;
-    const int a_frag = (wm * 64 + fr) * LROW + fk;    // + i * 16 * LROW
-    const int b_frag = (wn * 128 + fr) * LROW + fk;   // + j * 16 * LROW
-    const int s_frag = wn * 128 + fr;                 // + j * 16
-    const v4i seed = {kSeed, kSeed, kSeed, kSeed};
+    const int a_rd0 = A_LDS + (wm * 64 + fr) * TK + fk;   // + i * 16 * TK
+    const int b_rd0 = B_LDS + (wn * 128 + fr) * TK + fk;  // + j * 16 * TK
+    const int s_rd0 = S_LDS + 4 * ((wn * 16 + fr) * 8);    // + 4 * j
+    // opaque LDS base registers: every access below is base + a compile-time offset below 64 KB,
+    // which the ds instructions take as an immediate
+    int a_rd = a_rd0, b_rd = b_rd0, s_rd = s_rd0, b_st0 = b_st00, b_st1 = b_st10, s_st = s_st0;
+    asm volatile("" : "+v"(a_rd), "+v"(b_rd), "+v"(s_rd), "+v"(b_st0), "+v"(b_st1), "+v"(s_st));
+
+    // Groups past the last one ("dead" groups, which pad the loop to a multiple of the unroll) load
+    // with a scalar offset beyond every buffer range: their codes, zero-points and scales are all
+    // zero, so they add nothing to any accumulator.
+    constexpr int kDead = 0x7fffffff;   // voffset + kDead never wraps and is never in range
+    auto soff = [&](int g, int per_group) { return g < G ? g * per_group : kDead; };
+    // DMA of group g's A (and int8 B) tile into stage st
+    auto dma_group = [&](int g, int st) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            dma16(ra_rs, smem, A_LDS + st * TILE_BYTES + dma_lds + h * 16 * TK, dma_a[h], soff(g, TK));
+            if constexpr (!kPacked)
+                dma16(rb_rs, smem, B_LDS + st * TILE_BYTES + dma_lds + h * 16 * TK, dma_b[h], soff(g, TK));
+        }
+    };
+    // Two register sets carry packed B groups from their global load to their LDS store.
+    uint4 rb[2];
+    uint32_t rz[2] = {0u, 0u}, rs[2] = {0u, 0u};
+    auto gload_b = [&](int g, int set) {
+        if constexpr (kPacked) {
+            rb[set] = ld128(rb_rs, b_off, soff(g, TK / 2));
+            if constexpr (WK == WKind::U4Asym)
+                rz[set] = __builtin_amdgcn_raw_buffer_load_b8(rz_rs, z_off, g < G ? g >> 1 : kDead, 0);
+            if constexpr (EPI == Epi::GroupScale) rs[set] = __builtin_amdgcn_raw_buffer_load_b16(rs_rs, s_off, soff(g, 2), 0);
+        }
+    };
+    float cs = 0.0f;   // sum_g (-1)^g s[n, g] for this thread's weight row (GroupScale)
+    // LDS stores of register set `set` (a group of parity PAR) into stage ST, in two halves of the
+    // unpacked row (spread over two steps) and the scale.
+    auto store_b = [&](int st, int set, auto PARc, int h) {
+        if constexpr (kPacked) {
+            constexpr bool neg = kGroup && decltype(PARc)::value == 1;
+            const uint32_t zb = (rz[set] >> (neg ? 4 : 0)) & 0xfu;
+            constexpr bool x16 = AM == 2 && kGroup;
+            uint4 u;
+            const uint32_t w0 = h ? rb[set].z : rb[set].x, w1 = h ? rb[set].w : rb[set].y;
+            unpack_dword<WK, neg && AM != 2, x16>(w0, zb, u.x, u.y);
+            unpack_dword<WK, neg && AM != 2, x16>(w1, zb, u.z, u.w);
+            ds_write16(h ? b_st1 : b_st0, st * TILE_BYTES, u);
+        }
+    };
+    auto store_s = [&](int st, int set, auto PARc) {
+        if constexpr (EPI == Epi::GroupScale) {
+            constexpr bool neg = decltype(PARc)::value == 1;
+            float sv = f16_bits_to_f32(static_cast<uint16_t>(rs[set])) * kSfac;   // exact: power of two
+            sv = neg ? -sv : sv;
+            ds_write4(s_st, st * TN * 4, sv);
+            cs += sv;
+        }
+    };
 
     float acc[4][8][4];
     v4i acci[4][8];
@@ -269,103 +297,143 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             }
         }
 
-    // Fragment registers: A of the current K group (fragment i is refilled with group g + 1's
-    // right after its last MFMA in group g), and a 4-slot ring of B fragments and scales (slot =
-    // column % 4, 8 columns per group) read two columns ahead; the last two columns of group g
-    // fetch columns 0 and 1 of group g + 1.
-    v4i fa[4], fb[4];
+    // Fragment registers: A of the current K group, a 4-slot ring of B fragments and scales
+    // (slot = column % 4) and a 4-slot ring of MFMA results (slot = tile % 4). The ring slots a
+    // tile or column uses are the same in every group, so the pipeline state at a group boundary
+    // does not depend on which unrolled copy ran last. Zeroed results and scales make the first
+    // group's look-back fmas add nothing.
+    v4i fa[4], fb[4], d[4];
     float fs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto read_a = [&](int stage, int i, v4i& dst) {
-        dst = *reinterpret_cast<const v4i*>(&sm.u.pipe.a[stage][a_frag + i * 16 * LROW]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) d[q] = v4i{0, 0, 0, 0};
+    const v4i seed = {kSeed, kSeed, kSeed, kSeed};
+    auto read_a = [&](int st, int i) { fa[i] = lds<v4i>(smem, a_rd + st * TILE_BYTES + i * 16 * TK); };
+    auto read_b = [&](int st, int col) {
+        fb[col & 3] = lds<v4i>(smem, b_rd + st * TILE_BYTES + col * 16 * TK);
+        if constexpr (EPI == Epi::GroupScale) fs[col & 3] = lds<float>(smem, s_rd + st * TN * 4 + 4 * col);
     };
-    auto read_b = [&](int stage, int j, v4i& dst, float& sdst) {
-        dst = *reinterpret_cast<const v4i*>(&sm.u.pipe.b[stage][b_frag + j * 16 * LROW]);
-        if constexpr (EPI == Epi::GroupScale) sdst = sm.u.pipe.s[stage][s_frag + j * 16];
+    // Partials of tile tp (held in d[tp & 3]) of group gp.
+    auto write_partials = [&](int tp, int gp, bool odd) {
+        const int ip = tp & 3, jp = tp >> 2;
+        const int64_t col = n0 + wn * 128 + jp * 16 + fr;
+        int32_t* part = a.part + static_cast<int64_t>(gp) * M * N;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = m0 + wm * 64 + ip * 16 + 4 * (lane >> 4) + r;
+            const int32_t pv = (d[tp & 3][r] - kSeed) >> kShift;   // exact: a multiple of 2^kShift
+            if (row < M && col < N) part[row * N + col] = odd ? -pv : pv;
+        }
     };
-    using T0 = std::integral_constant<int, 0>;
-    using T1 = std::integral_constant<int, 1>;
+    // fmas of tile tp: acc += float(seed + X) * (+-s)
+    auto fma_tile = [&](int tp) {
+        const int ip = tp & 3, jp = tp >> 2;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            acc[ip][jp][r] = __builtin_fmaf(__int_as_float(d[tp & 3][r]), fs[jp & 3], acc[ip][jp][r]);
+        asm volatile("" : "+v"(acc[ip][jp][0]), "+v"(acc[ip][jp][1]), "+v"(acc[ip][jp][2]), "+v"(acc[ip][jp][3]));
+    };
 
-    // prologue: groups 0 and 1 into LDS stages 0 and 1, group 2 in registers (group indices are
-    // clamped to the last group: the repeats are never read)
-    const int glast = G - 1;
-    MQ_GLOAD(0);
-    lstore(0, T0{}, true);
-    MQ_GLOAD(1 < glast ? 1 : glast);
-    lstore(1, T1{}, G > 1);
-    MQ_GLOAD(2 < glast ? 2 : glast);
-    __syncthreads();
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    // Prologue. Steady state at the start of group g: A(g), A(g + 1) (and int8 B) complete in
+    // stages g % 4, (g + 1) % 4 and A(g + 2) in flight; B(g), B(g + 1) unpacked in their stages;
+    // register set g % 2 holds (or is loading) B(g + 2), set (g + 1) % 2 B(g + 3).
+    // The VMEM issue order leaves B(2), A(2), B(3) in flight, as in the steady state; A(0), A(1) are
+    // complete once the compiler has waited for B(1)'s registers.
+    dma_group(0, 0);
+    dma_group(1, 1);
+    gload_b(0, 0);
+    gload_b(1, 1);
+    store_b(0, 0, I0{}, 0);
+    store_b(0, 0, I0{}, 1);
+    store_s(0, 0, I0{});
+    store_b(1, 1, I1{}, 0);
+    store_b(1, 1, I1{}, 1);
+    store_s(1, 1, I1{});
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // A(0), A(1) of every kind (int8 B has no B loads)
+    gload_b(2, 0);
+    dma_group(2, 2);
+    gload_b(3, 1);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 4; ++i) read_a(0, i, fa[i]);
-    read_b(0, 0, fb[0], fs[0]);
-    read_b(0, 1, fb[1], fs[1]);
+    for (int i = 0; i < 4; ++i) read_a(0, i);
+    read_b(0, 0);
+    read_b(0, 1);
 
-    // K group g: 32 MFMA tiles t = 4 j + i, column-major. Every step issues tile t's MFMA, then the
-    // fmas of tile t - 1 (MFMA and VALU work overlap, two tiles of results are live); a scheduling
-    // fence after each step keeps every LDS read and store where it is written, so the reads really
-    // run two columns ahead. After column 1 the stage of group g + 2 is filled from the register
-    // set and the global loads of group g + 3 are issued. One barrier per group: stage
-    // (g + 2) % 3 was last read before the previous barrier, group g + 1's stage was completed
-    // before it. The body is branch-free: past the last group, loads and stores repeat the last
-    // group (never read), so each group is one scheduling region.
-    auto step = [&](int g, auto P) {
-        constexpr int par = decltype(P)::value;   // g & 1
-        const int st = g % NSTAGE, st1 = (g + 1) % NSTAGE, st2 = (g + 2) % NSTAGE;
-        constexpr int LAG = 1;   // tile t's fmas run LAG steps after its MFMA
-        v4i d[LAG + 1];
-        v4i seedv = seed;
+    // VMEM instructions per group and thread, in issue order: the DMA of A(g + 3) (and int8 B) at
+    // step 0, the packed B loads of group g + 4 at step 12. Before the barrier that ends group g,
+    // A(g + 2) (issued at step 0 of group g - 1) must be complete: everything issued after it may
+    // still be in flight.
+    constexpr int kDmaOps = kPacked ? 2 : 4;
+    constexpr int kBOps = kPacked ? 1 + (WK == WKind::U4Asym) + (EPI == Epi::GroupScale) : 0;
+    // (The partials variant also stores to global memory inside the loop; it waits for everything.)
+    constexpr int kVmAfter = EPI == Epi::GroupPartials ? 0 : 2 * kBOps + kDmaOps;
+
+    // K group g with A stage, B stage and register set fixed by U = g % 4 (compile-time). Step t = 4 j + i.
+    auto group = [&](int g, auto Uc) {
+        constexpr int U = decltype(Uc)::value;
+        constexpr int ST = U, ST1 = (U + 1) % 4, ST2 = (U + 2) % 4, ST3 = (U + 3) % 4, SET = U % 2;
+        using PARc = std::integral_constant<int, U % 2>;
+        constexpr int PAR = PARc::value;
 #pragma unroll
-        for (int t = 0; t < 32 + LAG; ++t) {
-            if (t < 32) {
-                const int j = t >> 2, i = t & 3;
-                if (i == 0) {
-                    // two columns ahead, into the slot of column j - 2 (its MFMAs and fmas are done)
-                    const int jj = j + 2;
-                    if (jj < 8) read_b(st, jj, fb[jj & 3], fs[jj & 3]);
-                    else read_b(st1, jj - 8, fb[jj & 3], fs[jj & 3]);
-                }
-                if (t == 8) {
-                    lstore(st2, std::integral_constant<int, par>{}, g + 2 < G);
-                    MQ_GLOAD(g + 3 < glast ? g + 3 : glast);
-                }
-                // empty asm on the seed: the MFMA cannot be hoisted above this step
-                asm volatile("" : "+v"(seedv));
-                if constexpr (kGroup) {
-                    d[t % (LAG + 1)] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j & 3], seedv, 0, 0, 0);
-                    if constexpr (EPI == Epi::GroupPartials) {
-                        const int64_t col = n0 + wn * 128 + j * 16 + fr;
-                        int32_t* part = a.part + static_cast<int64_t>(g) * M * N;
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int64_t row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
-                            const int32_t pv = (d[t % (LAG + 1)][r] - kSeed) >> kShift;   // exact: a multiple of 2^kShift
-                            if (row < M && col < N) part[row * N + col] = par ? -pv : pv;
-                        }
-                    }
-                } else {
-                    acci[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j & 3], acci[i][j], 0, 0, 0);
-                }
-                if (j == 7) read_a(st1, i, fa[i]);   // fa[i]'s last use in group g
-            }
-            if constexpr (EPI == Epi::GroupScale) {
-                if (t >= LAG) {
-                    const int tp = t - LAG, jp = tp >> 2, ip = tp & 3;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        acc[ip][jp][r] = __builtin_fmaf(__int_as_float(d[tp % (LAG + 1)][r]), fs[jp & 3], acc[ip][jp][r]);
-                    // empty asm on the accumulators: the fmas complete in this step (not sunk)
-                    asm volatile("" : "+v"(acc[ip][jp][0]), "+v"(acc[ip][jp][1]), "+v"(acc[ip][jp][2]),
-                                 "+v"(acc[ip][jp][3]));
-                }
+        for (int t = 0; t < 32; ++t) {
+            const int j = t >> 2, i = t & 3;
+            if constexpr (kGroup) {
+                d[t & 3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j & 3], seed, 0, 0, 0);
+            } else {
+                asm volatile("" : "+a"(acci[i][j]));
+                acci[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j & 3], acci[i][j], 0, 0, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
+            // tile t - LAG (for t < LAG: the last tiles of the previous group)
+            const int tp = (t + 32 - LAG) & 31;
+            if constexpr (EPI == Epi::GroupScale) fma_tile(tp);
+            if constexpr (EPI == Epi::GroupPartials) {
+                const int gp = t < LAG ? g - 1 : g;
+                if (gp >= 0 && gp < G) write_partials(tp, gp, t < LAG ? PAR == 0 : PAR == 1);
+            }
+            if (t == 0) dma_group(g + 3, ST3);
+            // every LDS store of this group (steps 8-10) has completed before the barrier that ends it
+            if (t == 12) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            // B fragments and scales two columns ahead (the next group's columns 0, 1 from stage ST1)
+            if (i == 0) {
+                if (j + 2 < 8) read_b(ST, j + 2);
+                else read_b(ST1, j + 2 - 8);
+            }
+            // fa[i]'s last use in this group: read the next group's
+            if (j == 7) read_a(ST1, i);
+            // unpack register set SET (group g + 2, parity PAR) into stage ST2, then reload it with g + 4
+            if (t == 8) store_b(ST2, SET, PARc{}, 0);
+            if (t == 9) store_b(ST2, SET, PARc{}, 1);
+            if (t == 10) store_s(ST2, SET, PARc{});
+            if (t == 12) gload_b(g + 4, SET);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __syncthreads();
+        // A(g + 2) (and this group's B stores, complete since step 12) become visible to every wave;
+        // group g's own stages were last read by MFMAs that have issued. The next group's fragment
+        // reads stay in flight across the barrier.
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kVmAfter) : "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
     };
-    for (int g = 0; g < G; g += 2) {
-        step(g, T0{});
-        if (g + 1 < G) step(g + 1, T1{});
+    const int G4 = (G + 3) / 4 * 4;   // groups run, live and dead
+    for (int g = 0; g < G4; g += 4) {
+        group(g, std::integral_constant<int, 0>{});
+        group(g + 1, std::integral_constant<int, 1>{});
+        group(g + 2, std::integral_constant<int, 2>{});
+        group(g + 3, std::integral_constant<int, 3>{});
     }
-#undef MQ_GLOAD
+    // drain: the last LAG tiles of the last group run (dead unless G is a multiple of four)
+#pragma unroll
+    for (int t = 0; t < LAG; ++t) {
+        const int tp = 32 - LAG + t;
+        if constexpr (EPI == Epi::GroupScale) fma_tile(tp);
+        if constexpr (EPI == Epi::GroupPartials)
+            if (G4 - 1 < G) write_partials(tp, G4 - 1, true);
+    }
 
     if constexpr (EPI == Epi::GroupPartials) return;
 
@@ -386,8 +454,9 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     }
 
     // ---- output epilogue: scale, bias, bf16, staged through LDS for 16-byte row stores
+    __syncthreads();   // every wave is done with the pipeline stages the staging area reuses
     if constexpr (EPI == Epi::GroupScale) {
-        if (bhalf == 0) sm.corr[brow] = cs * kMagic;
+        if (bhalf == 0) lds<float>(smem, C_LDS + 4 * brow) = cs * kMagic;
         __syncthreads();
     }
     float colv[8], biasv[8];
@@ -396,11 +465,11 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         const int lc = wn * 128 + j * 16 + fr;
         const int64_t col = n0 + lc;
         const bool ok = col < N;
-        if constexpr (EPI == Epi::GroupScale) colv[j] = sm.corr[lc];
+        if constexpr (EPI == Epi::GroupScale) colv[j] = lds<float>(smem, C_LDS + 4 * lc);
         else colv[j] = ok ? a.ws32[col] : 0.0f;
         biasv[j] = (ok && a.bias) ? __uint_as_float(static_cast<uint32_t>(a.bias[col]) << 16) : 0.0f;
     }
-    uint16_t* stage = sm.u.out[wave];
+    uint16_t* stage = reinterpret_cast<uint16_t*>(smem) + wave * 64 * OROW;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int lr0 = i * 16 + 4 * (lane >> 4);
@@ -466,7 +535,6 @@ template <WKind WK, Epi EPI>
 int launch_group(const GemmArgs& a, hipStream_t stream) {
     switch (a.act_mode) {
         case 0: return launch_one<WK, EPI, 0>(a, stream);
-        case 1: return launch_one<WK, EPI, 1>(a, stream);
         case 2: return launch_one<WK, EPI, 2>(a, stream);
         default: break;
     }
