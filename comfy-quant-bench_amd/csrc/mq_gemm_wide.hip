@@ -31,8 +31,8 @@
 // final epilogue. The integer partials P_g themselves are exact (GroupPartials writes them).
 //
 // Weight unpack: packed byte j of a row holds k = 2j in bits 0-3 and k = 2j + 1 in bits 4-7. Four
-// bytes at a time: lo/hi nibble masks, ((v | 0x80) - z) ^ 0x80 per byte (no inter-byte borrow) for
-// q - z, ((z | 0x80) - v) ^ 0x80 for z - q, and two byte permutes back to k order. Signed int4
+// bytes at a time: lo/hi nibble masks, (v + (0x80 - z)) ^ 0x80 per byte (no inter-byte carry) for
+// q - z, ((0x80 + z) - v) ^ 0x80 for z - q, and two byte permutes back to k order. Signed int4
 // is the same with v ^ 8 and z = 8.
 //
 // int4 activations. With codes in [-7, 7] the partials are ~100x smaller than with int8 codes and
@@ -51,6 +51,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float f2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 
 constexpr int TM = 256, TN = 256, TK = 64;
@@ -74,40 +75,43 @@ constexpr int SMEM_BYTES = C_LDS + TN * 4;
 // byte offset of 16-byte chunk c of tile row r in the swizzled layout
 __device__ __forceinline__ int lds_off(int r, int c) { return r * TK + ((c ^ ((r >> 1) & 3)) << 4); }
 
-__device__ __forceinline__ void unpack_pos(uint32_t w, uint32_t zz, uint32_t& o0, uint32_t& o1) {
+// 8 packed 4-bit weights (one dword) -> 8 int8 operands in k order (two dwords). Bytes of c are
+// 0x80 - z (u = 0) or 0x80 + z (u = 1): per byte, (lo + c) ^ 0x80 = lo - z and (c - lo) ^ 0x80 =
+// z - lo, without inter-byte carries or borrows since lo is in [0, 15].
+template <bool NEG>
+__device__ __forceinline__ void unpack_nib(uint32_t w, uint32_t c, uint32_t& o0, uint32_t& o1) {
     uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-    lo = ((lo | 0x80808080u) - zz) ^ 0x80808080u;
-    hi = ((hi | 0x80808080u) - zz) ^ 0x80808080u;
+    if constexpr (NEG) {
+        lo = (c - lo) ^ 0x80808080u;
+        hi = (c - hi) ^ 0x80808080u;
+    } else {
+        lo = (lo + c) ^ 0x80808080u;
+        hi = (hi + c) ^ 0x80808080u;
+    }
     o0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
     o1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
 }
 
-__device__ __forceinline__ void unpack_neg(uint32_t w, uint32_t zz80, uint32_t& o0, uint32_t& o1) {
-    uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-    lo = (zz80 - lo) ^ 0x80808080u;
-    hi = (zz80 - hi) ^ 0x80808080u;
-    o0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
-    o1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+// The per-group constant of unpack_nib for zero-point byte zb (U4Asym) or the fixed zero-point 8
+// of signed int4 (whose nibbles are flipped by 8 first, so v ^ 8 = v + 8 is in [0, 15]).
+template <WKind WK, bool NEG>
+__device__ __forceinline__ uint32_t unpack_const(uint32_t zb) {
+    if constexpr (WK == WKind::I4Sym) zb = 8u;
+    const uint32_t zz = __builtin_amdgcn_perm(0u, zb, 0u);   // byte 0 of zb in every byte
+    return NEG ? (0x80808080u | zz) : (0x80808080u - zz);
 }
 
-// 8 packed 4-bit weights (one dword) -> 8 int8 operands in k order (two dwords).
 // U4Asym: q - z (z - q when NEG); I4Sym: v (-v when NEG), or 16 * v when X16 (never negated).
 template <WKind WK, bool NEG, bool X16>
-__device__ __forceinline__ void unpack_dword(uint32_t w, uint32_t zb, uint32_t& o0, uint32_t& o1) {
+__device__ __forceinline__ void unpack_dword(uint32_t w, uint32_t c, uint32_t& o0, uint32_t& o1) {
     if constexpr (WK == WKind::I4Sym && X16) {
         // a nibble moved to the high half of its byte reads as 16 x its signed value
         const uint32_t lo = (w << 4) & 0xf0f0f0f0u, hi = w & 0xf0f0f0f0u;
         o0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
         o1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
     } else {
-        if constexpr (WK == WKind::I4Sym) {
-            // signed nibble v -> v ^ 8 in [0, 15] with zero-point 8 (a zero-filled row stays 0)
-            w ^= 0x88888888u;
-            zb = 8u;
-        }
-        const uint32_t zz = __builtin_amdgcn_perm(0u, zb, 0u);   // byte 0 of zb in every byte
-        if constexpr (NEG) unpack_neg(w, zz | 0x80808080u, o0, o1);
-        else unpack_pos(w, zz, o0, o1);
+        if constexpr (WK == WKind::I4Sym) w ^= 0x88888888u;
+        unpack_nib<NEG>(w, c, o0, o1);
     }
 }
 
@@ -135,6 +139,36 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t
 __device__ __forceinline__ uint4 ld128(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
     return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// Buffer loads written as inline asm, so that the kernel alone decides when to wait for them
+// (s_waitcnt vmcnt with counts that follow the pipeline's fixed issue order; the compiler's own
+// count is conservative at the loop header and would wait for loads issued a group later).
+// The descriptor is the same as make_buffer_rsrc builds: base, stride 0, byte range, format word.
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u4v sdesc(const void* base, int64_t bytes) {
+    const uint64_t p = reinterpret_cast<uint64_t>(base);
+    u4v d;
+    d.x = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
+    d.y = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32) & 0xffffu);
+    d.z = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(bytes));
+    d.w = 0x00020000u;
+    return d;
+}
+__device__ __forceinline__ u4v asm_ld128(u4v d, int voff, int soff) {
+    u4v v;
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
+    return v;
+}
+__device__ __forceinline__ uint32_t asm_ld8(u4v d, int voff, int soff) {
+    uint32_t v;
+    asm volatile("buffer_load_ubyte %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
+    return v;
+}
+__device__ __forceinline__ uint32_t asm_ld16(u4v d, int voff, int soff) {
+    uint32_t v;
+    asm volatile("buffer_load_ushort %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
+    return v;
 }
 
 // 16 bytes per lane from buffer r at voff + soff straight into LDS: lane l writes bytes
@@ -213,9 +247,10 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     const int b_off = b_ok ? static_cast<int>(brow * a.ldw) + bhalf * 16 : kOob;
     // zero-points and scales (null for the kinds that have none: the range is then empty)
     const bool has_z = WK == WKind::U4Asym, has_s = EPI == Epi::GroupScale;
-    const auto rz_rs = rsrc(has_z ? a.wz + n0 * a.ldwz : a.qw, has_z ? (rows_n - 1) * a.ldwz + (G + 1) / 2 : 0);
-    const auto rs_rs = rsrc(has_s ? a.ws16 + n0 * a.ldws : reinterpret_cast<const uint16_t*>(a.qw),
-                            has_s ? ((rows_n - 1) * a.ldws + G) * 2 : 0);
+    const u4v db = sdesc(a.qw + n0 * a.ldw, (rows_n - 1) * a.ldw + kbytes_w);
+    const u4v dz = sdesc(has_z ? a.wz + n0 * a.ldwz : a.qw, has_z ? (rows_n - 1) * a.ldwz + (G + 1) / 2 : 0);
+    const u4v ds = sdesc(has_s ? static_cast<const void*>(a.ws16 + n0 * a.ldws) : a.qw,
+                         has_s ? ((rows_n - 1) * a.ldws + G) * 2 : 0);
     const int z_off = has_z && b_ok ? static_cast<int>(brow * a.ldwz) : kOob;
     const int s_off = has_s && b_ok ? static_cast<int>(brow * a.ldws * 2) : kOob;
     const int b_st00 = B_LDS + lds_off(brow, 2 * bhalf);
@@ -249,28 +284,32 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         }
     };
     // Two register sets carry packed B groups from their global load to their LDS store.
-    uint4 rb[2];
+    u4v rb[2] = {u4v{0u, 0u, 0u, 0u}, u4v{0u, 0u, 0u, 0u}};
     uint32_t rz[2] = {0u, 0u}, rs[2] = {0u, 0u};
     auto gload_b = [&](int g, int set) {
         if constexpr (kPacked) {
-            rb[set] = ld128(rb_rs, b_off, soff(g, TK / 2));
-            if constexpr (WK == WKind::U4Asym)
-                rz[set] = __builtin_amdgcn_raw_buffer_load_b8(rz_rs, z_off, g < G ? g >> 1 : kDead, 0);
-            if constexpr (EPI == Epi::GroupScale) rs[set] = __builtin_amdgcn_raw_buffer_load_b16(rs_rs, s_off, soff(g, 2), 0);
+            rb[set] = asm_ld128(db, b_off, soff(g, TK / 2));
+            if constexpr (WK == WKind::U4Asym) rz[set] = asm_ld8(dz, z_off, g < G ? g >> 1 : kDead);
+            if constexpr (EPI == Epi::GroupScale) rs[set] = asm_ld16(ds, s_off, soff(g, 2));
         }
     };
+    // Wait until at most N VMEM operations are outstanding; register set SET counts as written by
+    // the wait, so no use of it moves above it.
+#define MQ_WAIT_B(N, SET) \
+    asm volatile("s_waitcnt vmcnt(%3)" : "+v"(rb[SET]), "+v"(rz[SET]), "+v"(rs[SET]) : "n"(N) : "memory")
     float cs = 0.0f;   // sum_g (-1)^g s[n, g] for this thread's weight row (GroupScale)
     // LDS stores of register set `set` (a group of parity PAR) into stage ST, in two halves of the
     // unpacked row (spread over two steps) and the scale.
     auto store_b = [&](int st, int set, auto PARc, int h) {
         if constexpr (kPacked) {
             constexpr bool neg = kGroup && decltype(PARc)::value == 1;
-            const uint32_t zb = (rz[set] >> (neg ? 4 : 0)) & 0xfu;
             constexpr bool x16 = AM == 2 && kGroup;
+            constexpr bool nw = neg && AM != 2;
+            const uint32_t c = unpack_const<WK, nw>((rz[set] >> (neg ? 4 : 0)) & 0xfu);
             uint4 u;
             const uint32_t w0 = h ? rb[set].z : rb[set].x, w1 = h ? rb[set].w : rb[set].y;
-            unpack_dword<WK, neg && AM != 2, x16>(w0, zb, u.x, u.y);
-            unpack_dword<WK, neg && AM != 2, x16>(w1, zb, u.z, u.w);
+            unpack_dword<WK, nw, x16>(w0, c, u.x, u.y);
+            unpack_dword<WK, nw, x16>(w1, c, u.z, u.w);
             ds_write16(h ? b_st1 : b_st0, st * TILE_BYTES, u);
         }
     };
@@ -297,20 +336,22 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             }
         }
 
-    // Fragment registers: A of the current K group, a 4-slot ring of B fragments and scales
-    // (slot = column % 4) and a 4-slot ring of MFMA results (slot = tile % 4). The ring slots a
+    // Fragment registers: A fragments of the current and the next K group (set = g % 2), a 4-slot
+    // ring of B fragments read three columns ahead (slot = column % 4), the scales of columns 0-3
+    // and 4-7 in two register quads, and a 4-slot ring of MFMA results (slot = tile % 4). The ring slots a
     // tile or column uses are the same in every group, so the pipeline state at a group boundary
     // does not depend on which unrolled copy ran last. Zeroed results and scales make the first
     // group's look-back fmas add nothing.
-    v4i fa[4], fb[4], d[4];
-    float fs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4i fa[2][4], fb[4], d[4];
+    f4 fs[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};   // scales of columns 0-3, 4-7
 #pragma unroll
     for (int q = 0; q < 4; ++q) d[q] = v4i{0, 0, 0, 0};
     const v4i seed = {kSeed, kSeed, kSeed, kSeed};
-    auto read_a = [&](int st, int i) { fa[i] = lds<v4i>(smem, a_rd + st * TILE_BYTES + i * 16 * TK); };
-    auto read_b = [&](int st, int col) {
-        fb[col & 3] = lds<v4i>(smem, b_rd + st * TILE_BYTES + col * 16 * TK);
-        if constexpr (EPI == Epi::GroupScale) fs[col & 3] = lds<float>(smem, s_rd + st * TN * 4 + 4 * col);
+    auto read_a = [&](int st, int set, int i) { fa[set][i] = lds<v4i>(smem, a_rd + st * TILE_BYTES + i * 16 * TK); };
+    auto read_b = [&](int st, int col) { fb[col & 3] = lds<v4i>(smem, b_rd + st * TILE_BYTES + col * 16 * TK); };
+    // the 4 scales of columns 4 h .. 4 h + 3 (adjacent in the transposed scale layout)
+    auto read_s = [&](int st, int h) {
+        if constexpr (EPI == Epi::GroupScale) fs[h] = lds<f4>(smem, s_rd + st * TN * 4 + 16 * h);
     };
     // Partials of tile tp (held in d[tp & 3]) of group gp.
     auto write_partials = [&](int tp, int gp, bool odd) {
@@ -329,7 +370,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         const int ip = tp & 3, jp = tp >> 2;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            acc[ip][jp][r] = __builtin_fmaf(__int_as_float(d[tp & 3][r]), fs[jp & 3], acc[ip][jp][r]);
+            acc[ip][jp][r] = __builtin_fmaf(__int_as_float(d[tp & 3][r]), fs[jp >> 2][jp & 3], acc[ip][jp][r]);
         asm volatile("" : "+v"(acc[ip][jp][0]), "+v"(acc[ip][jp][1]), "+v"(acc[ip][jp][2]), "+v"(acc[ip][jp][3]));
     };
 
@@ -344,6 +385,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     dma_group(1, 1);
     gload_b(0, 0);
     gload_b(1, 1);
+    MQ_WAIT_B(0, 0);
+    MQ_WAIT_B(0, 1);
     store_b(0, 0, I0{}, 0);
     store_b(0, 0, I0{}, 1);
     store_s(0, 0, I0{});
@@ -358,9 +401,12 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 4; ++i) read_a(0, i);
+    for (int i = 0; i < 4; ++i) read_a(0, 0, i);
     read_b(0, 0);
     read_b(0, 1);
+    read_b(0, 2);
+    read_s(0, 0);
+    read_s(0, 1);
 
     // VMEM instructions per group and thread, in issue order: the DMA of A(g + 3) (and int8 B) at
     // step 0, the packed B loads of group g + 4 at step 12. Before the barrier that ends group g,
@@ -370,6 +416,9 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     constexpr int kBOps = kPacked ? 1 + (WK == WKind::U4Asym) + (EPI == Epi::GroupScale) : 0;
     // (The partials variant also stores to global memory inside the loop; it waits for everything.)
     constexpr int kVmAfter = EPI == Epi::GroupPartials ? 0 : 2 * kBOps + kDmaOps;
+    // At step 8 of group g, register set g % 2 (B(g + 2), loaded at step 12 of group g - 2) must
+    // have arrived; issued after it: A(g + 2) at step 0 of g - 1, B(g + 3), A(g + 3).
+    constexpr int kWaitB = EPI == Epi::GroupPartials ? 0 : 2 * kDmaOps + kBOps;
 
     // K group g with A stage, B stage and register set fixed by U = g % 4 (compile-time). Step t = 4 j + i.
     auto group = [&](int g, auto Uc) {
@@ -381,10 +430,10 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         for (int t = 0; t < 32; ++t) {
             const int j = t >> 2, i = t & 3;
             if constexpr (kGroup) {
-                d[t & 3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j & 3], seed, 0, 0, 0);
+                d[t & 3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[SET][i], fb[j & 3], seed, 0, 0, 0);
             } else {
                 asm volatile("" : "+a"(acci[i][j]));
-                acci[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j & 3], acci[i][j], 0, 0, 0);
+                acci[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[SET][i], fb[j & 3], acci[i][j], 0, 0, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
             // tile t - LAG (for t < LAG: the last tiles of the previous group)
@@ -395,25 +444,33 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
                 if (gp >= 0 && gp < G) write_partials(tp, gp, t < LAG ? PAR == 0 : PAR == 1);
             }
             if (t == 0) dma_group(g + 3, ST3);
-            // every LDS store of this group (steps 8-10) has completed before the barrier that ends it
-            if (t == 12) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            // B fragments and scales two columns ahead (the next group's columns 0, 1 from stage ST1)
+            // B fragments three columns ahead (the next group's first columns from stage ST1,
+            // complete since the barrier that ended group g - 1)
             if (i == 0) {
-                if (j + 2 < 8) read_b(ST, j + 2);
-                else read_b(ST1, j + 2 - 8);
+                if (j + 3 < 8) read_b(ST, j + 3);
+                else read_b(ST1, j + 3 - 8);
             }
-            // fa[i]'s last use in this group: read the next group's
-            if (j == 7) read_a(ST1, i);
+            // Scales: columns 4-7 once the previous group's column 7 is done (its last fma is at step
+            // 2), columns 0-3 of the next group once column 3 is done (last fma at step 18).
+            if (t == 3) read_s(ST, 1);
+            if (t == 19) read_s(ST1, 0);
+            // the next group's A fragments into the other set, early in this group
+            if (i == 2 && j < 4) read_a(ST1, SET ^ 1, j);
             // unpack register set SET (group g + 2, parity PAR) into stage ST2, then reload it with g + 4
-            if (t == 8) store_b(ST2, SET, PARc{}, 0);
+            if (t == 8) {
+                MQ_WAIT_B(kWaitB, SET);
+                store_b(ST2, SET, PARc{}, 0);
+            }
             if (t == 9) store_b(ST2, SET, PARc{}, 1);
             if (t == 10) store_s(ST2, SET, PARc{});
             if (t == 12) gload_b(g + 4, SET);
             __builtin_amdgcn_sched_barrier(0);
         }
-        // A(g + 2) (and this group's B stores, complete since step 12) become visible to every wave;
-        // group g's own stages were last read by MFMAs that have issued. The next group's fragment
-        // reads stay in flight across the barrier.
+        // A(g + 2) and this group's B stores become visible to every wave. LDS operations of a wave
+        // complete in issue order, and the MFMAs of steps 16-31 waited for fragment reads issued
+        // after the stores of steps 8-10, so those stores are complete here without a wait. Group
+        // g's own stages were last read by MFMAs that have issued; the next group's fragment reads
+        // stay in flight across the barrier.
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kVmAfter) : "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
@@ -426,6 +483,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         group(g + 2, std::integral_constant<int, 2>{});
         group(g + 3, std::integral_constant<int, 3>{});
     }
+#undef MQ_WAIT_B
     // drain: the last LAG tiles of the last group run (dead unless G is a multiple of four)
 #pragma unroll
     for (int t = 0; t < LAG; ++t) {
