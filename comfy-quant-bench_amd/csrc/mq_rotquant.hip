@@ -7,14 +7,17 @@
 //   quantizer: tools/activation_balance.py:65-71, s = max(absmax/L, 1e-10f),
 //     q = clamp(rne(x / s), -L, L) with the IEEE quotient x / s.
 //
-// Layout: one wavefront per row. A row is processed in chunks of 1024 columns; in a chunk, lane
-// L holds the 16 consecutive columns 16L..16L+15 in registers r = 0..15 (two 16-byte loads), so
-// register bits r0..r3 are column bits e0..e3 and lane bits L0..L5 are column bits e4..e9.
-// The radix-4 stages over e0e1 and e2e3 run in registers. The stage over e4e5 (blocks 64, 256)
-// first swaps lane bits L0, L1 with register bits r2, r3 through DPP lane exchanges, and the
-// stage over e6e7 (block 256) swaps L2, L3 with r2, r3 the same way; every butterfly then runs in
-// registers in the reference's order. Afterwards r0r1 still hold e0e1, so each group of 4
-// registers is 4 consecutive codes and stores as one dword (int8) or one 16-bit word (int4).
+// Layout. One wavefront per row; a row is processed in chunks of 1024 columns. Within a chunk,
+// column c has bits c0..c9; lane L of the wave loads the 16 consecutive columns of segment
+// s = (L >> 2) + 16 (L & 3) (two 16-byte bf16 loads), so register bits r0..r3 hold c0..c3 and
+// lane bits L0..L5 hold c8 c9 c4 c5 c6 c7. The radix-4 stages over (c0 c1) and (c2 c3) run in
+// registers. The stage over (c4 c5) (blocks 64, 256) first swaps lane bits L2, L3 with register
+// bits r2, r3 through DPP row shifts; the stage over (c6 c7) (block 256) swaps L4, L5 with r2, r3
+// through v_permlane16_swap / v_permlane32_swap (one instruction per register pair). Every
+// butterfly then runs in registers in the reference's order. After quantization four codes of
+// consecutive columns (r0 r1) sit in each dword; a final exchange of dwords across lane bits L2,
+// L3 gives every lane 16 consecutive codes, written with one 16-byte (int8) or 8-byte (packed
+// int4) store.
 //
 // Quantization without a per-element division: with r = 1/s (IEEE), m = fma(v, r, 1.5*2^23)
 // rounds v*r to an integer n. |v*r - v/s| <= 2^-17 and |fl(v/s) - v/s| <= 2^-17 for |v/s| < 128,
@@ -48,77 +51,89 @@ __device__ __forceinline__ void stage_reg(float (&v)[16]) {
     }
 }
 
-// Exchange lane bit B with register bit J: afterwards the value with (lane bit B = u, register
-// bit J = w) is the one that was at (lane bit B = w, register bit J = u).
-template <int B, int J>
-__device__ __forceinline__ void swap_lane_reg(float (&v)[16], int lane) {
+// Exchange lane bit B (2..5) with register bit J of an array of N 32-bit values: afterwards the
+// value with (lane bit B = u, register bit J = w) is the one that was at (lane bit B = w,
+// register bit J = u).
+template <int B, int J, int N, typename T>
+__device__ __forceinline__ void swap_lane_reg(T (&v)[N], int lane) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
+    for (int r = 0; r < N; ++r) {
         if (r & (1 << J)) continue;
-        const float x = v[r], y = v[r | (1 << J)];
-        float xn, yn;
-        if constexpr (B == 0) {
-            const float ty = dpp_mov<kQuadPerm0022>(y);
-            const float tx = dpp_mov<kQuadPerm1133>(x);
-            const bool up = lane & 1;
+        const uint32_t x = __builtin_bit_cast(uint32_t, v[r]), y = __builtin_bit_cast(uint32_t, v[r | (1 << J)]);
+        uint32_t xn, yn;
+        if constexpr (B == 2 || B == 3) {
+            // lanes with the bit set take y from lane - 2^B, the others x from lane + 2^B (row
+            // shifts within 16-lane rows; the select folds into a DPP-sourced v_cndmask)
+            constexpr int shr = B == 2 ? kRowShr4 : kRowShr8, shl = B == 2 ? kRowShl4 : kRowShl8;
+            const bool up = (lane >> B) & 1;
+            const uint32_t ty = __builtin_amdgcn_mov_dpp(y, shr, 0xf, 0xf, true);
+            const uint32_t tx = __builtin_amdgcn_mov_dpp(x, shl, 0xf, 0xf, true);
             xn = up ? ty : x;
             yn = up ? y : tx;
-        } else if constexpr (B == 1) {
-            const float ty = dpp_mov<kQuadPerm0101>(y);
-            const float tx = dpp_mov<kQuadPerm2323>(x);
-            const bool up = lane & 2;
-            xn = up ? ty : x;
-            yn = up ? y : tx;
-        } else if constexpr (B == 2) {
-            xn = dpp_upd<kRowShr4, 0xA>(x, y);   // lanes 4-7, 12-15 of each row take y from lane-4
-            yn = dpp_upd<kRowShl4, 0x5>(y, x);   // lanes 0-3, 8-11 take x from lane+4
+        } else if constexpr (B == 4) {
+            const auto p = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+            xn = p[0];
+            yn = p[1];
         } else {
-            static_assert(B == 3, "lane bit");
-            xn = dpp_upd<kRowShr8, 0xC>(x, y);   // lanes 8-15 take y from lane-8
-            yn = dpp_upd<kRowShl8, 0x3>(y, x);   // lanes 0-7 take x from lane+8
+            static_assert(B == 5, "lane bit");
+            const auto p = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+            xn = p[0];
+            yn = p[1];
         }
-        v[r] = xn;
-        v[r | (1 << J)] = yn;
+        v[r] = __builtin_bit_cast(T, xn);
+        v[r | (1 << J)] = __builtin_bit_cast(T, yn);
     }
 }
 
 template <int BLK>
 __device__ __forceinline__ void rotate_chunk(float (&v)[16], int lane) {
     if constexpr (BLK >= 16) {
-        stage_reg<0>(v);          // element stride 1  (e0 e1)
-        stage_reg<2>(v);          // element stride 4  (e2 e3)
+        stage_reg<0>(v);          // element stride 1  (c0 c1)
+        stage_reg<2>(v);          // element stride 4  (c2 c3)
     }
     if constexpr (BLK >= 64) {
-        swap_lane_reg<0, 2>(v, lane);
-        swap_lane_reg<1, 3>(v, lane);
-        stage_reg<2>(v);          // element stride 16 (e4 e5)
-    }
-    if constexpr (BLK >= 256) {
         swap_lane_reg<2, 2>(v, lane);
         swap_lane_reg<3, 3>(v, lane);
-        stage_reg<2>(v);          // element stride 64 (e6 e7)
+        stage_reg<2>(v);          // element stride 16 (c4 c5)
+    }
+    if constexpr (BLK >= 256) {
+        swap_lane_reg<4, 2>(v, lane);
+        swap_lane_reg<5, 3>(v, lane);
+        stage_reg<2>(v);          // element stride 64 (c6 c7)
     }
 }
 
-// Column offset (within the chunk) of register group hi (registers 4*hi..4*hi+3) of lane L.
+// Column bit 6 (the parity of the 64-column group) of register r of lane L after rotate_chunk.
 template <int BLK>
-__device__ __forceinline__ int group_col(int lane, int hi) {
-    if constexpr (BLK >= 256) return 4 * (lane & 15) + 64 * hi + 256 * (lane >> 4);
-    else if constexpr (BLK >= 64) return 4 * (lane & 3) + 16 * hi + 64 * (lane >> 2);
-    else return 16 * lane + 4 * hi;
+__device__ __forceinline__ int col_bit6(int lane, int r) {
+    if constexpr (BLK >= 256) return (r >> 2) & 1;   // r2 r3 hold c6 c7
+    else return (lane >> 4) & 1;                      // L4 holds c6
 }
 
+// Quantize 16 values: fast path for all, then (rarely, per lane) the exact path for the values
+// whose product lies near a half-integer. Returns the magic-biased floats (code in the low bits).
 template <int LIMIT>
-__device__ __forceinline__ float quant_magic(float v, float r, float s) {
-    float m = __builtin_fmaf(v, r, kMagic);
-    const float n = m - kMagic;
-    const float d = __builtin_fmaf(v, r, -n);
-    if (__builtin_fabsf(d) > kTieWindow) {
-        float qf = __builtin_rintf(v / s);
-        qf = __builtin_fminf(__builtin_fmaxf(qf, -static_cast<float>(LIMIT)), static_cast<float>(LIMIT));
-        m = kMagic + qf;
+__device__ __forceinline__ void quant16(const float (&v)[16], float sg, float r, float s, float (&m)[16]) {
+    float dmax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const float x = sg * v[j];
+        m[j] = __builtin_fmaf(x, r, kMagic);
+        const float n = m[j] - kMagic;
+        dmax = __builtin_fmaxf(dmax, __builtin_fabsf(__builtin_fmaf(x, r, -n)));
     }
-    return m;
+    if (dmax > kTieWindow) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const float x = sg * v[j];
+            const float n = m[j] - kMagic;
+            if (__builtin_fabsf(__builtin_fmaf(x, r, -n)) > kTieWindow) {
+                float qf = __builtin_rintf(x / s);
+                qf = __builtin_fminf(__builtin_fmaxf(qf, -static_cast<float>(LIMIT)), static_cast<float>(LIMIT));
+                m[j] = kMagic + qf;
+            }
+        }
+    }
 }
 
 // OUT: 0 = int8 codes, 1 = int4 codes one per byte, 2 = int4 codes packed two per byte,
@@ -133,11 +148,12 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
     const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
     if (row >= M) return;
     const uint16_t* xr = x + row * ldx;
+    const int seg_ld = (lane >> 2) + 16 * (lane & 3);   // 16-column segment this lane loads
 
     float v[NCH][16];
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-        const int e = c * 1024 + lane * 16;
+        const int e = c * 1024 + seg_ld * 16;
         if (e < K) {
             const uint4 a = *reinterpret_cast<const uint4*>(xr + e);
             const uint4 b = *reinterpret_cast<const uint4*>(xr + e + 8);
@@ -167,24 +183,26 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
     const float r = 1.0f / s;
     if (lane == 0) scale[row] = s;
 
+    // After the final dword exchange a lane holds the 16 codes of segment seg_st.
+    const int seg_st = BLK >= 256 ? (lane >> 4) + 4 * ((lane >> 2) & 3) + 16 * (lane & 3) : seg_ld;
     uint8_t* qr = q + row * ldq;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-        if (c * 1024 + lane * 16 >= K) continue;
+        // quantization is odd-symmetric (rint and the clamp are), so negating the input of an odd
+        // 64-column group negates its codes exactly; for block 256 the group parity is register
+        // bit r2, so the sign applies per dword below instead
+        float mq[16];
+        quant16<LIMIT>(v[c], OUT == 3 && BLK < 256 && col_bit6<BLK>(lane, 0) ? -1.0f : 1.0f, r, s, mq);
         uint32_t word[4];
 #pragma unroll
         for (int hi = 0; hi < 4; ++hi) {
-            // quantization is odd-symmetric (rint and the clamp are), so negating the input of an
-            // odd 64-column group negates its codes exactly
-            float sg = 1.0f;
-            if constexpr (OUT == 3) {
-                const int col = c * 1024 + (BLK < 64 ? 16 * lane + 4 * hi : group_col<BLK>(lane, hi));
-                sg = (col >> 6) & 1 ? -1.0f : 1.0f;
+            uint32_t m0 = __float_as_uint(mq[4 * hi + 0]), m1 = __float_as_uint(mq[4 * hi + 1]);
+            uint32_t m2 = __float_as_uint(mq[4 * hi + 2]), m3 = __float_as_uint(mq[4 * hi + 3]);
+            if constexpr (OUT == 3 && BLK >= 256) {
+                if (col_bit6<BLK>(lane, 4 * hi)) {   // negate the four codes (two's complement bytes)
+                    m0 = -m0; m1 = -m1; m2 = -m2; m3 = -m3;
+                }
             }
-            uint32_t m0 = __float_as_uint(quant_magic<LIMIT>(sg * v[c][4 * hi + 0], r, s));
-            uint32_t m1 = __float_as_uint(quant_magic<LIMIT>(sg * v[c][4 * hi + 1], r, s));
-            uint32_t m2 = __float_as_uint(quant_magic<LIMIT>(sg * v[c][4 * hi + 2], r, s));
-            uint32_t m3 = __float_as_uint(quant_magic<LIMIT>(sg * v[c][4 * hi + 3], r, s));
             if constexpr (OUT == 3) {
                 m0 <<= 4; m1 <<= 4; m2 <<= 4; m3 <<= 4;
             }
@@ -196,25 +214,20 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
                 word[hi] = lo16 | hi16;
             }
         }
-        const int cbase = c * 1024;
-        if constexpr (BLK < 64) {
-            if constexpr (OUT == 2) {
-                uint2 out = {word[0] | (word[1] << 16), word[2] | (word[3] << 16)};
-                *reinterpret_cast<uint2*>(qr + (cbase + 16 * lane) / 2) = out;
-            } else {
-                uint4 out = {word[0], word[1], word[2], word[3]};
-                *reinterpret_cast<uint4*>(qr + cbase + 16 * lane) = out;
-            }
+        // dword index bits hold (c6 c7) for block 256 and (c4 c5) for block 64; lane bits L2 L3
+        // hold (c2 c3): exchange them so each lane's four dwords are consecutive columns
+        if constexpr (BLK >= 64) {
+            swap_lane_reg<2, 0>(word, lane);
+            swap_lane_reg<3, 1>(word, lane);
+        }
+        const int col = c * 1024 + seg_st * 16;
+        if (col >= K) continue;
+        if constexpr (OUT == 2) {
+            const uint2 out = {word[0] | (word[1] << 16), word[2] | (word[3] << 16)};
+            *reinterpret_cast<uint2*>(qr + col / 2) = out;
         } else {
-#pragma unroll
-            for (int hi = 0; hi < 4; ++hi) {
-                const int col = cbase + group_col<BLK>(lane, hi);
-                if constexpr (OUT == 2) {
-                    *reinterpret_cast<uint16_t*>(qr + col / 2) = static_cast<uint16_t>(word[hi]);
-                } else {
-                    *reinterpret_cast<uint32_t*>(qr + col) = word[hi];
-                }
-            }
+            const uint4 out = {word[0], word[1], word[2], word[3]};
+            *reinterpret_cast<uint4*>(qr + col) = out;
         }
     }
 }
