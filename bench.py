@@ -10,17 +10,23 @@ call of kitchen_amd.w4a8_int8_linear (two kernel launches on the current stream)
 
 Prints one JSON line: whole-linear int8 TOPS (2*M*N*K / step time), the GEMM kernel's roofline
 (average launch duration from HIP events on the launch stream, against the 5.0 POPS dense int8
-MFMA peak), the rotate+quantize kernel's HBM roofline at the video-token shape (M=32760), and the
-reference's CPU torch path timed on a bounded sample of the same workload.
+MFMA peak; HBM traffic per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE counters, calibrated
+on a device-to-device copy of known size), the rotate+quantize kernel's HBM roofline at the
+video-token shape (M=32760), and the reference's CPU torch path timed on a bounded sample of the
+same workload.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
 import platform
+import shutil
 import subprocess
 import sys
+import tempfile
 
 REPO = os.path.dirname(os.path.abspath(__file__))
 for _p in (REPO, os.path.join(REPO, "comfy-quant-bench_amd")):
@@ -30,6 +36,11 @@ for _p in (REPO, os.path.join(REPO, "comfy-quant-bench_amd")):
 METRIC = "int8-MFMA TOPS & % peak for W4A8/W4A4 linear (rot+quant+GEMM), M=4096"
 INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, 5.0 POPS
 HBM_PEAK_GBPS = 8000.0       # MI355X HBM3E, 8 TB/s
+RQ_M = 32760                 # video-token shape of the rotate+quantize roofline (302 MB, above the MALL)
+COPY_BYTES = 256 << 20       # calibration copy for the traffic counters
+GEMM_KERNEL = "gemm_wide_kernel"
+RQ_KERNEL = "rotquant_kernel"
+COPY_KERNEL = "copyBuffer"
 
 
 def cpu_model() -> str:
@@ -43,21 +54,119 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def time_launches(fn, iters: int, warm: int = 3) -> float:
-    """Average milliseconds per call of fn, HIP events on the current stream."""
+def time_launches(fn, iters: int, rounds: int = 5, warm: int = 3) -> float:
+    """Median over `rounds` of the average milliseconds per call of fn (HIP events recorded on
+    torch's current stream, which is the stream the library launches on)."""
     import torch
 
     for _ in range(warm):
         fn()
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(iters):
-        fn()
-    e1.record()
+    per = []
+    for _ in range(rounds):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) / iters)
+    per.sort()
+    return per[len(per) // 2]
+
+
+def make_inputs(m: int, k: int, n: int):
+    import numpy as np
+    import torch
+
+    import kitchen_amd as ck
+    from kitchen_amd import synth
+
+    dev = torch.device("cuda:0")
+    xb = synth.activations(m, k, seed=0)
+    w = synth.weight(n, k, seed=1)
+    rng = np.random.default_rng(2)
+    bias_f = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(rng.standard_normal(n).astype(np.float32) * 0.1))
+    qd, s16, zp = ck.quantize_w4a8_asym_weight(torch.from_numpy(w).to(dev), 64, 256)
+    x = synth.to_bf16_tensor(xb, dev)
+    bias = torch.from_numpy(bias_f).to(dev, torch.bfloat16)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / iters
+    return xb, bias_f, x, qd, s16, zp, bias
+
+
+def kernels_child(args) -> int:
+    """Launch each measured kernel a few times and exit (run under rocprofv3 by measure_traffic)."""
+    import torch
+
+    import kitchen_amd as ck
+    from kitchen_amd import synth
+
+    m, k, n = args.m, args.k, args.n
+    _, _, x, qd, s16, zp, bias = make_inputs(m, k, n)
+    qa, sa = ck.quantize_int8_rowwise_convrot(x, 256)
+    for _ in range(3):
+        ck.gemm_w4_group(qa, sa, qd.view(torch.uint8), s16, zp.view(torch.uint8), bias, n)
+    x3 = synth.to_bf16_tensor(synth.activations(RQ_M, k, seed=3), x.device)
+    for _ in range(3):
+        ck.quantize_int8_rowwise_convrot(x3, 256)
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.int32, device=x.device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return 0
+
+
+def _counter_means(csv_path: str, counter: str) -> dict:
+    sums: dict = {}
+    for row in csv.DictReader(open(csv_path)):
+        if row.get("Counter_Name") != counter:
+            continue
+        name = row["Kernel_Name"]
+        for key in (GEMM_KERNEL, RQ_KERNEL, COPY_KERNEL):
+            if key in name:
+                sums.setdefault(key, []).append(float(row["Counter_Value"]))
+    # the calibration copies are identical; other copy-kernel dispatches (smaller) are ignored
+    return {key: (max(v) if key == COPY_KERNEL else sum(v) / len(v)) for key, v in sums.items()}
+
+
+def measure_traffic(args) -> dict:
+    """HBM bytes per launch of the GEMM and rotate+quantize kernels from two rocprofv3 --pmc runs
+    (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by bytes / counter of a
+    device-to-device copy of COPY_BYTES in the same run."""
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        return {"error": "rocprofv3 not found"}
+    out: dict = {}
+    with tempfile.TemporaryDirectory(prefix="mq_bench_pmc_") as tmp:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            d = os.path.join(tmp, counter)
+            cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "pmc", "--",
+                   sys.executable, os.path.abspath(__file__), "--kernels-child",
+                   "--m", str(args.m), "--k", str(args.k), "--n", str(args.n)]
+            try:
+                res = subprocess.run(cmd, capture_output=True, text=True, timeout=180, env=dict(os.environ, TMPDIR=tmp))
+            except subprocess.TimeoutExpired:
+                return {"error": f"rocprofv3 {counter} run timed out"}
+            files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+            if res.returncode != 0 and not files:
+                return {"error": f"rocprofv3 {counter} run failed ({res.returncode})"}
+            if not files:
+                return {"error": f"no counter file for {counter}"}
+            means = _counter_means(files[0], counter)
+            if COPY_KERNEL not in means or GEMM_KERNEL not in means:
+                return {"error": f"{counter}: kernels not found in the counter file"}
+            out[counter] = means
+    f_fetch = COPY_BYTES / (out["FETCH_SIZE"][COPY_KERNEL] * 1024.0)
+    f_write = COPY_BYTES / (out["WRITE_SIZE"][COPY_KERNEL] * 1024.0)
+    res = {"fetch_scale": round(f_fetch, 4), "write_scale": round(f_write, 4)}
+    for key in (GEMM_KERNEL, RQ_KERNEL):
+        if key in out["FETCH_SIZE"] and key in out["WRITE_SIZE"]:
+            fetch = out["FETCH_SIZE"][key] * 1024.0 * f_fetch
+            write = out["WRITE_SIZE"][key] * 1024.0 * f_write
+            res[key] = {"fetch_bytes": int(fetch), "write_bytes": int(write), "bytes": int(fetch + write)}
+    return res
 
 
 def main() -> int:
@@ -69,29 +178,24 @@ def main() -> int:
     ap.add_argument("--k", type=int, default=3072)
     ap.add_argument("--n", type=int, default=12288)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 traffic counters")
+    ap.add_argument("--kernels-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "the W4A8 linear would shard over tokens or output channels with no exchange, see DESIGN.md.",
               file=sys.stderr)
         return 2
+    if args.kernels_child:
+        return kernels_child(args)
 
-    import numpy as np
     import torch
 
     import kitchen_amd as ck
     from kitchen_amd import synth
 
-    dev = torch.device("cuda:0")
     m, k, n = args.m, args.k, args.n
-    xb = synth.activations(m, k, seed=0)
-    w = synth.weight(n, k, seed=1)
-    rng = np.random.default_rng(2)
-    bias_f = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(rng.standard_normal(n).astype(np.float32) * 0.1))
-    qd, s16, zp = ck.quantize_w4a8_asym_weight(torch.from_numpy(w).to(dev), 64, 256)
-    x = synth.to_bf16_tensor(xb, dev)
-    bias = torch.from_numpy(bias_f).to(dev, torch.bfloat16)
-    torch.cuda.synchronize()
+    xb, bias_f, x, qd, s16, zp, bias = make_inputs(m, k, n)
 
     def step():
         return ck.w4a8_int8_linear(x, qd, s16, None, None, zp, bias, 64, 256, torch.bfloat16)
@@ -114,17 +218,20 @@ def main() -> int:
     # ---- dominant kernel (GEMM) alone, same stream, inputs resident
     qa, sa = ck.quantize_int8_rowwise_convrot(x, 256)
     qdu, zpu = qd.view(torch.uint8), zp.view(torch.uint8)
-    ms_gemm = time_launches(lambda: ck.gemm_w4_group(qa, sa, qdu, s16, zpu, bias, n), max(args.steps, 20))
+    ms_gemm = time_launches(lambda: ck.gemm_w4_group(qa, sa, qdu, s16, zpu, bias, n), 20)
     gemm_tops = ops / (ms_gemm * 1e-3) / 1e12
-    ms_rq_ns = time_launches(lambda: ck.quantize_int8_rowwise_convrot(x, 256), max(args.steps, 20))
+    ms_rq_ns = time_launches(lambda: ck.quantize_int8_rowwise_convrot(x, 256), 20)
 
     # ---- rotate+quantize kernel at the HBM-bound video-token shape (C3: 32760 x 3072, 302 MB)
-    m3 = 32760
-    x3 = synth.to_bf16_tensor(synth.activations(m3, k, seed=3), dev)
-    ms_rq = time_launches(lambda: ck.quantize_int8_rowwise_convrot(x3, 256), 50)
-    rq_bytes = m3 * k * 2 + m3 * k + 4 * m3
+    x3 = synth.to_bf16_tensor(synth.activations(RQ_M, k, seed=3), x.device)
+    ms_rq = time_launches(lambda: ck.quantize_int8_rowwise_convrot(x3, 256), 20)
+    rq_bytes = RQ_M * k * 2 + RQ_M * k + 4 * RQ_M
     rq_gbps = rq_bytes / (ms_rq * 1e-3) / 1e9
     del x3
+
+    traffic = None if args.no_traffic else measure_traffic(args)
+    gemm_traffic = traffic.get(GEMM_KERNEL, {}).get("bytes") if traffic else None
+    rq_traffic = traffic.get(RQ_KERNEL, {}).get("bytes") if traffic else None
 
     result = {
         "metric": METRIC,
@@ -141,15 +248,18 @@ def main() -> int:
         "data": "synthetic: seeded N(0,1) bf16 activations with 1% x20 outlier channels, N(0,0.02) weights",
         "config": {"workload": "w4a8_linear (rotate H256 + int8 per-token quant + uint4-asym g64 GEMM + epilogue)",
                    "M": m, "K": k, "N": n, "hadamard_block": 256, "group": 64, "out": "bf16"},
-        "roofline": {"bound": "mfma", "kernel": "gemm_kernel<U4Asym,GroupScale>",
+        "roofline": {"bound": "mfma", "kernel": "gemm_wide_kernel<U4Asym,GroupScale,0>",
                      "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
-                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": gemm_traffic,
                      "ops_per_launch": ops, "avg_launch_ms": round(ms_gemm, 5)},
-        "rotquant_roofline": {"bound": "hbm", "kernel": "rotquant_kernel<256,int8,3>", "M": m3, "K": k,
+        "rotquant_roofline": {"bound": "hbm", "kernel": "rotquant_kernel<256,int8,3>", "M": RQ_M, "K": k,
                               "achieved": round(rq_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                               "frac": round(rq_gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": rq_bytes,
-                              "avg_launch_ms": round(ms_rq, 5), "north_star_M_launch_ms": round(ms_rq_ns, 5)},
+                              "traffic": rq_traffic, "avg_launch_ms": round(ms_rq, 5),
+                              "north_star_M_launch_ms": round(ms_rq_ns, 5)},
     }
+    if traffic is not None:
+        result["traffic_counters"] = {k2: v for k2, v in traffic.items() if k2 in ("fetch_scale", "write_scale", "error")}
 
     if not args.no_cpu_baseline:
         from oracle import quant

@@ -1,0 +1,7 @@
+#!/bin/bash
+# Runs every microbenchmark once (each finishes in well under a second of GPU time).
+cd "$(dirname "$0")"
+for b in mfma_peak lds_read_bw mfma_fma_coissue_small mfma_fma_coissue_random; do
+  echo "== $b"
+  timeout -k 5 120 ./$b || exit $?
+done
