@@ -18,7 +18,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "kitchen_amd", "libmq.so")
-SOURCES = ["mq_abi.hip", "mq_rotquant.hip", "mq_gemm.hip", "mq_gemm_wide.hip"]
+SOURCES = ["mq_abi.hip", "mq_rotquant.hip", "mq_swiglu.hip", "mq_gemm.hip", "mq_gemm_wide.hip"]
 ARCH = "gfx950"
 
 
@@ -48,7 +48,7 @@ def flags() -> list[str]:
 
 def _compile(src: str, build_dir: str, verbose: bool) -> str:
     obj = os.path.join(build_dir, src.replace(".hip", ".o"))
-    cmd = [hipcc(), *flags(), "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *flags(), "-I", os.path.join(build_dir, "gen"), "-c", os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -63,7 +63,10 @@ def _compile(src: str, build_dir: str, verbose: bool) -> str:
 def build(verbose: bool = False) -> str:
     """Compile every source (in parallel) and link libmq.so; returns its path. Always recompiles."""
     build_dir = os.path.join(HERE, "_build")
-    os.makedirs(build_dir, exist_ok=True)
+    os.makedirs(os.path.join(build_dir, "gen"), exist_ok=True)
+    # generated constant table: correctly rounded fp32 silu of the bf16 gates (SwiGLU prologue)
+    subprocess.run([sys.executable, os.path.join(CSRC, "gen_silu_table.py"),
+                    os.path.join(build_dir, "gen", "mq_silu_table.h")], check=True)
     workers = max(1, min(len(SOURCES), os.cpu_count() or 1))
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
         objs = list(pool.map(lambda src: _compile(src, build_dir, verbose), SOURCES))

@@ -67,34 +67,61 @@ int mq_abi_version(void) { return MQ_ABI_VERSION; }
 
 const char* mq_last_error(void) { return g_err; }
 
-int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits, int packed, void* q,
-                int64_t ldq, float* scale, void* stream) {
-    clear_error();
-    MQ_REQUIRE(M >= 0 && K > 0, "rotquant: bad shape M=%lld K=%lld", (long long)M, (long long)K);
-    MQ_REQUIRE(M < (int64_t(1) << 31), "rotquant: M too large");
-    MQ_REQUIRE(bits == 8 || bits == 4, "rotquant: bits must be 8 or 4 (got %d)", bits);
-    MQ_REQUIRE(packed >= MQ_Q_BYTES && packed <= MQ_Q_X16ALT, "rotquant: unknown code layout %d", packed);
-    MQ_REQUIRE(packed == MQ_Q_BYTES || bits == 4, "rotquant: packed output needs bits = 4");
+}  // extern "C"
+
+namespace {
+
+// Argument checks shared by mq_rotquant and mq_swiglu_rotquant; x holds `cols` bf16 values per
+// row (K, or 2K for gate | up).
+int check_rotquant(const char* what, const void* x, int64_t M, int64_t K, int64_t cols, int64_t ldx, int hblock,
+                   int bits, int packed, const void* q, int64_t ldq, const float* scale) {
+    MQ_REQUIRE(M >= 0 && K > 0, "%s: bad shape M=%lld K=%lld", what, (long long)M, (long long)K);
+    MQ_REQUIRE(M < (int64_t(1) << 31), "%s: M too large", what);
+    MQ_REQUIRE(bits == 8 || bits == 4, "%s: bits must be 8 or 4 (got %d)", what, bits);
+    MQ_REQUIRE(packed >= MQ_Q_BYTES && packed <= MQ_Q_X16ALT, "%s: unknown code layout %d", what, packed);
+    MQ_REQUIRE(packed == MQ_Q_BYTES || bits == 4, "%s: packed output needs bits = 4", what);
     MQ_REQUIRE(hblock == 0 || hblock == 16 || hblock == 64 || hblock == 256,
-               "rotquant: convrot group size must be 16, 64 or 256 (got %d)", hblock);
-    MQ_REQUIRE(K % 16 == 0, "rotquant: K=%lld must be a multiple of 16", (long long)K);
-    MQ_REQUIRE(hblock == 0 || K % hblock == 0, "rotquant: K=%lld is not a multiple of the group size %d",
+               "%s: convrot group size must be 16, 64 or 256 (got %d)", what, hblock);
+    MQ_REQUIRE(K % 16 == 0, "%s: K=%lld must be a multiple of 16", what, (long long)K);
+    MQ_REQUIRE(hblock == 0 || K % hblock == 0, "%s: K=%lld is not a multiple of the group size %d", what,
                (long long)K, hblock);
     if (K > 16384) {
-        set_error("rotquant: K=%lld exceeds 16384", (long long)K);
+        set_error("%s: K=%lld exceeds 16384", what, (long long)K);
         return MQ_EUNSUPPORTED;
     }
     if (M == 0) return MQ_OK;
-    MQ_REQUIRE(x && q && scale, "rotquant: null pointer");
-    MQ_REQUIRE(ldx >= K && ldx % 8 == 0 && aligned(x, 16), "rotquant: x needs ldx >= K, ldx %% 8 == 0, 16-byte aligned base");
+    MQ_REQUIRE(x && q && scale, "%s: null pointer", what);
+    MQ_REQUIRE(ldx >= cols && ldx % 8 == 0 && aligned(x, 16),
+               "%s: x needs ldx >= %lld, ldx %% 8 == 0, 16-byte aligned base", what, (long long)cols);
     const int64_t row_bytes = packed == MQ_Q_PACKED ? K / 2 : K;
     const int64_t qalign = packed == MQ_Q_PACKED ? 8 : 16;
     MQ_REQUIRE(ldq >= row_bytes && ldq % qalign == 0 && aligned(q, qalign),
-               "rotquant: q needs ldq >= %lld bytes, ldq %% %lld == 0 and an aligned base", (long long)row_bytes,
+               "%s: q needs ldq >= %lld bytes, ldq %% %lld == 0 and an aligned base", what, (long long)row_bytes,
                (long long)qalign);
-    MQ_REQUIRE(aligned(scale, 4), "rotquant: scale must be 4-byte aligned");
+    MQ_REQUIRE(aligned(scale, 4), "%s: scale must be 4-byte aligned", what);
+    return MQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits, int packed, void* q,
+                int64_t ldq, float* scale, void* stream) {
+    clear_error();
+    const int rc = check_rotquant("rotquant", x, M, K, K, ldx, hblock, bits, packed, q, ldq, scale);
+    if (rc != MQ_OK || M == 0) return rc;
     return launch_rotquant(static_cast<const uint16_t*>(x), M, K, ldx, hblock, bits, packed, q, ldq, scale,
                            static_cast<hipStream_t>(stream));
+}
+
+int mq_swiglu_rotquant(const void* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits, int packed,
+                       void* q, int64_t ldq, float* scale, void* stream) {
+    clear_error();
+    const int rc = check_rotquant("swiglu_rotquant", h, M, K, 2 * K, ldh, hblock, bits, packed, q, ldq, scale);
+    if (rc != MQ_OK || M == 0) return rc;
+    return launch_swiglu_rotquant(static_cast<const uint16_t*>(h), M, K, ldh, hblock, bits, packed, q, ldq, scale,
+                                  static_cast<hipStream_t>(stream));
 }
 
 int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,

@@ -20,6 +20,10 @@ int launch_status(const char* what);
 int launch_rotquant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits,
                     int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
 
+// --- SwiGLU prologue + rotate + quantize (mq_swiglu.hip); h holds gate | up, K columns each
+int launch_swiglu_rotquant(const uint16_t* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
+                           int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
+
 // --- GEMMs (mq_gemm.hip)
 enum class WKind : int { U4Asym = 0, I4Sym = 1, I8 = 2 };
 enum class Epi : int { GroupScale = 0, GroupPartials = 1, RowScale = 2, RowAcc = 3 };

@@ -1,0 +1,393 @@
+// Fused Hadamard block rotation + per-token dynamic int8 / int4 quantizer for gfx950 (kernel
+// templates, instantiated by mq_rotquant.hip for plain inputs and by mq_swiglu.hip for the
+// SwiGLU prologue).
+//
+// Arithmetic (bit-exact with the CPU oracle):
+//   rotation: the fp32 radix-4 FWHT of experiments/qwen21-kernel/kernels/g64_quant.cu:68-86,
+//     stages with element strides 1, 4, 16, 64; each butterfly h = 0.5f*(((x0+x1)+x2)+x3),
+//     y_i = h - x_{3-i};
+//   quantizer: tools/activation_balance.py:65-71, s = max(absmax/L, 1e-10f),
+//     q = clamp(rne(x / s), -L, L) with the IEEE quotient x / s.
+//
+// Layout. A row is processed in chunks of 1024 columns by W wavefronts (W = 1, 2 or 4 by K, so
+// that each wave holds at most 4 chunks in registers and the kernel keeps several waves per SIMD);
+// wave w of a row takes chunks w, w + W, ... and the row's absmax is combined through LDS. A
+// workgroup of 4 waves handles 4 / W rows per step of a grid-stride loop over row groups. Within a chunk,
+// column c has bits c0..c9; lane L of the wave loads the 16 consecutive columns of segment
+// s = (L >> 2) + 16 (L & 3) (two 16-byte bf16 loads), so register bits r0..r3 hold c0..c3 and
+// lane bits L0..L5 hold c8 c9 c4 c5 c6 c7. The radix-4 stages over (c0 c1) and (c2 c3) run in
+// registers. The stage over (c4 c5) (blocks 64, 256) first swaps lane bits L2, L3 with register
+// bits r2, r3 through DPP row shifts written into the lanes of the receiving DPP banks only (one
+// v_mov_b32_dpp per moved value); the stage over (c6 c7) (block 256) swaps L4, L5 with r2, r3
+// through v_permlane16_swap / v_permlane32_swap (one instruction per register pair). Every
+// butterfly then runs in registers in the reference's order. After quantization four codes of
+// consecutive columns (r0 r1) sit in each dword; a final exchange of dwords across lane bits L2,
+// L3 gives every lane 16 consecutive codes, written with one 16-byte (int8) or 8-byte (packed
+// int4) store.
+//
+// Quantization without a per-element division: with r = 1/s (IEEE), m = fma(v, r, 1.5*2^23)
+// rounds v*r to an integer n. |v*r - v/s| <= 2^-17 and |fl(v/s) - v/s| <= 2^-17 for |v/s| < 128,
+// so rint(fl(v/s)) == n unless v*r lies within 2^-16 of a half-integer; those elements (flagged
+// by |fma(v, r, -n)| > 0.5 - 2^-15) recompute rint(v / s) with the IEEE division. The clamp to
+// [-L, L] never binds on the fast path: |v| <= absmax, so |v*r| <= L (1 + 2^-22).
+#pragma once
+
+#include <algorithm>
+
+#include "mq_device.h"
+#include "mq_silu_table.h"
+#include "mq_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace mq {
+namespace {
+
+constexpr int kWaves = 4;                 // wavefronts per workgroup
+constexpr float kTieWindow = 0.5f - 0x1p-15f;
+
+// --- SwiGLU prologue (tools/ck_swiglu/swiglu_quant.cu:56-66): a = silu(g) * u in fp32, rounded
+// once to bf16, formed from the gate | up halves while loading. silu(g) = g / (1 + exp(-g)) is
+// taken correctly rounded to fp32: the gate is a bf16 value, so every result that is not a closed
+// form comes from a 32 KB table (mq_silu_table.h, generated with exact decimal arithmetic) that
+// each workgroup stages in LDS. Closed forms: |g| < 2^-25 gives g / 2, g >= 128 gives g and
+// g <= -128 gives -0. Then a = bf16(fp32(silu(g) * u)).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float silu_f32(uint32_t b, float g, const float* tab) {
+    const uint32_t t = b & 0x7fffu;
+    const uint32_t j = __builtin_elementwise_min(t - kSiluLo, kSiluEntries - 1u);   // in bounds always
+    const uint32_t s = __float_as_uint(tab[j + ((b >> 15) << 12)]);
+    const uint32_t big = (b >> 15) ? 0x80000000u : __float_as_uint(g);
+    const uint32_t r = t < kSiluLo ? __float_as_uint(g * 0.5f) : s;
+    return __uint_as_float(t >= kSiluLo + kSiluEntries ? big : r);
+}
+
+// Two activations from one dword of gates and one of ups (two bf16 each), as bf16-valued floats.
+__device__ __forceinline__ void swiglu_pair(uint32_t wg, uint32_t wu, const float* tab, float& a0, float& a1) {
+    const float p0 = silu_f32(wg & 0xffffu, bf16lo(wg), tab) * bf16lo(wu);
+    const float p1 = silu_f32(wg >> 16, bf16hi(wg), tab) * bf16hi(wu);
+    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{p0, p1}, bf16x2));
+    a0 = __uint_as_float(h << 16);
+    a1 = __uint_as_float(h & 0xffff0000u);
+}
+
+// Radix-4 butterflies over register bits J, J+1 (element stride 4^d mapped to register stride 2^J).
+template <int J>
+__device__ __forceinline__ void stage_reg(float (&v)[16]) {
+    constexpr int st = 1 << J;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        if ((r >> J) & 3) continue;
+        const float x0 = v[r], x1 = v[r + st], x2 = v[r + 2 * st], x3 = v[r + 3 * st];
+        const float h = 0.5f * (((x0 + x1) + x2) + x3);
+        v[r] = h - x3;
+        v[r + st] = h - x2;
+        v[r + 2 * st] = h - x1;
+        v[r + 3 * st] = h - x0;
+    }
+}
+
+// Exchange lane bit B (2..5) with register bit J of an array of N 32-bit values: afterwards the
+// value with (lane bit B = u, register bit J = w) is the one that was at (lane bit B = w,
+// register bit J = u).
+template <int B, int J, int N, typename T>
+__device__ __forceinline__ void swap_lane_reg(T (&v)[N], [[maybe_unused]] int lane) {
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        if (r & (1 << J)) continue;
+        const uint32_t x = __builtin_bit_cast(uint32_t, v[r]), y = __builtin_bit_cast(uint32_t, v[r | (1 << J)]);
+        uint32_t xn, yn;
+        if constexpr (B == 2 || B == 3) {
+            // lanes with the bit set take y from lane - 2^B, the others x from lane + 2^B: row
+            // shifts within 16-lane rows, each written only into the lanes (DPP banks of 4 lanes =
+            // lane bits 2, 3) that take it, so every moved value costs one v_mov_b32_dpp
+            constexpr int shr = B == 2 ? kRowShr4 : kRowShr8, shl = B == 2 ? kRowShl4 : kRowShl8;
+            constexpr int up = B == 2 ? 0xA : 0xC;        // banks with the lane bit set
+            xn = __builtin_amdgcn_update_dpp(x, y, shr, 0xf, up, false);
+            yn = __builtin_amdgcn_update_dpp(y, x, shl, 0xf, up ^ 0xf, false);
+        } else if constexpr (B == 4) {
+            const auto p = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+            xn = p[0];
+            yn = p[1];
+        } else {
+            static_assert(B == 5, "lane bit");
+            const auto p = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+            xn = p[0];
+            yn = p[1];
+        }
+        v[r] = __builtin_bit_cast(T, xn);
+        v[r | (1 << J)] = __builtin_bit_cast(T, yn);
+    }
+}
+
+template <int BLK>
+__device__ __forceinline__ void rotate_chunk(float (&v)[16], int lane) {
+    if constexpr (BLK >= 16) {
+        stage_reg<0>(v);          // element stride 1  (c0 c1)
+        stage_reg<2>(v);          // element stride 4  (c2 c3)
+    }
+    if constexpr (BLK >= 64) {
+        swap_lane_reg<2, 2>(v, lane);
+        swap_lane_reg<3, 3>(v, lane);
+        stage_reg<2>(v);          // element stride 16 (c4 c5)
+    }
+    if constexpr (BLK >= 256) {
+        swap_lane_reg<4, 2>(v, lane);
+        swap_lane_reg<5, 3>(v, lane);
+        stage_reg<2>(v);          // element stride 64 (c6 c7)
+    }
+}
+
+// Column bit 6 (the parity of the 64-column group) of register r of lane L after rotate_chunk.
+template <int BLK>
+__device__ __forceinline__ int col_bit6(int lane, int r) {
+    if constexpr (BLK >= 256) return (r >> 2) & 1;   // r2 r3 hold c6 c7
+    else return (lane >> 4) & 1;                      // L4 holds c6
+}
+
+// Quantize 16 values: fast path for all, then (rarely, per lane) the exact path for the values
+// whose product lies near a half-integer. Returns the magic-biased floats (code in the low bits).
+template <int LIMIT>
+__device__ __forceinline__ void quant16(const float (&v)[16], float sg, float r, float s, float (&m)[16]) {
+    float dmax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const float x = sg * v[j];
+        m[j] = __builtin_fmaf(x, r, kMagic);
+        const float n = m[j] - kMagic;
+        dmax = __builtin_fmaxf(dmax, __builtin_fabsf(__builtin_fmaf(x, r, -n)));
+    }
+    if (dmax > kTieWindow) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const float x = sg * v[j];
+            const float n = m[j] - kMagic;
+            if (__builtin_fabsf(__builtin_fmaf(x, r, -n)) > kTieWindow) {
+                float qf = __builtin_rintf(x / s);
+                qf = __builtin_fminf(__builtin_fmaxf(qf, -static_cast<float>(LIMIT)), static_cast<float>(LIMIT));
+                m[j] = kMagic + qf;
+            }
+        }
+    }
+}
+
+// OUT: 0 = int8 codes, 1 = int4 codes one per byte, 2 = int4 codes packed two per byte,
+//      3 = int4 codes one per byte as 16 * q, negated in odd 64-column groups (the operand layout
+//          the group-scale GEMM takes for int4 activations: exact, and 16x finer in its fp32 step).
+// ACT: 0 = x is the activation itself; 1 = x holds gate | up halves of K columns each (the up
+// half starts K elements into the row) and the activation is swiglu_pair(gate, up).
+// NCH: chunks per wave; W: waves per row (NCH * W * 1024 >= K).
+template <int BLK, int OUT, int NCH, int ACT, int W>
+__global__ void __launch_bounds__(64 * kWaves)
+rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
+                uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale) {
+    constexpr int LIMIT = OUT == 0 ? 127 : 7;
+    constexpr int RPG = kWaves / W;                      // rows per workgroup step
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wr = wave % W;                             // this wave's share of its row
+    [[maybe_unused]] const float* tab = nullptr;
+    if constexpr (ACT == 1) {
+        __shared__ __attribute__((aligned(16))) uint32_t silu_lds[2 * kSiluEntries];
+        for (uint32_t i = threadIdx.x; i < 2 * kSiluEntries / 4; i += 64 * kWaves)
+            reinterpret_cast<uint4*>(silu_lds)[i] = reinterpret_cast<const uint4*>(kSiluTable)[i];
+        __syncthreads();
+        tab = reinterpret_cast<const float*>(silu_lds);
+    }
+    [[maybe_unused]] float* red = nullptr;               // per-wave absmax, double-buffered by step
+    if constexpr (W > 1) {
+        __shared__ float red_lds[2][kWaves];
+        red = &red_lds[0][0];
+    }
+    const int seg_ld = (lane >> 2) + 16 * (lane & 3);   // 16-column segment this lane loads
+    // after the final dword exchange a lane holds the 16 codes of segment seg_st
+    const int seg_st = BLK >= 256 ? (lane >> 4) + 4 * ((lane >> 2) & 3) + 16 * (lane & 3) : seg_ld;
+    const int64_t groups = (static_cast<int64_t>(M) + RPG - 1) / RPG;
+    int parity = 0;
+    // every wave runs the same number of steps (the bound is uniform over the workgroup), so the
+    // barrier inside is reached by all of them
+    for (int64_t rg = blockIdx.x; rg < groups; rg += gridDim.x, parity ^= 1) {
+        const int64_t row = rg * RPG + wave / W;
+        const bool live = row < M;
+        if constexpr (W == 1) {
+            if (!live) break;
+        }
+        const uint16_t* xr = x + row * ldx;
+
+        float v[NCH][16];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int e = (c * W + wr) * 1024 + seg_ld * 16;
+            if (live && e < K) {
+                const uint4 a = *reinterpret_cast<const uint4*>(xr + e);
+                const uint4 b = *reinterpret_cast<const uint4*>(xr + e + 8);
+                const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                if constexpr (ACT == 1) {
+                    const uint4 ua = *reinterpret_cast<const uint4*>(xr + K + e);
+                    const uint4 ub = *reinterpret_cast<const uint4*>(xr + K + e + 8);
+                    const uint32_t wu[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) swiglu_pair(w[j], wu[j], tab, v[c][2 * j], v[c][2 * j + 1]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        v[c][2 * j] = bf16lo(w[j]);
+                        v[c][2 * j + 1] = bf16hi(w[j]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[c][j] = 0.0f;
+            }
+        }
+
+        float am = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            rotate_chunk<BLK>(v[c], lane);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) am = __builtin_fmaxf(am, __builtin_fabsf(v[c][j]));
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) am = __builtin_fmaxf(am, __shfl_xor(am, o, 64));
+        if constexpr (W > 1) {
+            if (lane == 0) red[parity * kWaves + wave] = am;
+            __syncthreads();
+            const int first = wave - wr;
+#pragma unroll
+            for (int i = 0; i < W; ++i) am = __builtin_fmaxf(am, red[parity * kWaves + first + i]);
+            if (!live) continue;
+        }
+
+        const float s = __builtin_fmaxf(am / static_cast<float>(LIMIT), 1e-10f);
+        const float r = 1.0f / s;
+        if (lane == 0 && wr == 0) scale[row] = s;
+
+        uint8_t* qr = q + row * ldq;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            // quantization is odd-symmetric (rint and the clamp are), so negating the input of an
+            // odd 64-column group negates its codes exactly; for block 256 the group parity is
+            // register bit r2, so the sign applies per dword below instead
+            float mq[16];
+            quant16<LIMIT>(v[c], OUT == 3 && BLK < 256 && col_bit6<BLK>(lane, 0) ? -1.0f : 1.0f, r, s, mq);
+            uint32_t word[4];
+#pragma unroll
+            for (int hi = 0; hi < 4; ++hi) {
+                uint32_t m0 = __float_as_uint(mq[4 * hi + 0]), m1 = __float_as_uint(mq[4 * hi + 1]);
+                uint32_t m2 = __float_as_uint(mq[4 * hi + 2]), m3 = __float_as_uint(mq[4 * hi + 3]);
+                if constexpr (OUT == 3 && BLK >= 256) {
+                    if (col_bit6<BLK>(lane, 4 * hi)) {   // negate the four codes (two's complement bytes)
+                        m0 = -m0; m1 = -m1; m2 = -m2; m3 = -m3;
+                    }
+                }
+                if constexpr (OUT == 3) {
+                    m0 <<= 4; m1 <<= 4; m2 <<= 4; m3 <<= 4;
+                }
+                if constexpr (OUT == 2) {
+                    word[hi] = (m0 & 0xfu) | ((m1 & 0xfu) << 4) | ((m2 & 0xfu) << 8) | ((m3 & 0xfu) << 12);
+                } else {
+                    const uint32_t lo16 = __builtin_amdgcn_perm(m1, m0, 0x0c0c0400u);
+                    const uint32_t hi16 = __builtin_amdgcn_perm(m3, m2, 0x04000c0cu);
+                    word[hi] = lo16 | hi16;
+                }
+            }
+            // dword index bits hold (c6 c7) for block 256 and (c4 c5) for block 64; lane bits
+            // L2 L3 hold (c2 c3): exchange them so each lane's four dwords are consecutive columns
+            if constexpr (BLK >= 64) {
+                swap_lane_reg<2, 0>(word, lane);
+                swap_lane_reg<3, 1>(word, lane);
+            }
+            const int col = (c * W + wr) * 1024 + seg_st * 16;
+            if (col >= K) continue;
+            if constexpr (OUT == 2) {
+                const uint2 out = {word[0] | (word[1] << 16), word[2] | (word[3] << 16)};
+                *reinterpret_cast<uint2*>(qr + col / 2) = out;
+            } else {
+                const uint4 out = {word[0], word[1], word[2], word[3]};
+                *reinterpret_cast<uint4*>(qr + col) = out;
+            }
+        }
+    }
+}
+
+// Compute units of the current device.
+inline int device_cu_count() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        return 256;
+    return n;
+}
+
+template <int BLK, int OUT, int NCH, int ACT, int W>
+int launch_rq(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, void* q, int64_t ldq, float* scale,
+              hipStream_t stream) {
+    const int64_t groups = (M + kWaves / W - 1) / (kWaves / W);
+    // plain inputs: one workgroup per row group; SwiGLU: a grid-stride loop over the row groups,
+    // so each workgroup stages the LDS table once for many rows
+    int64_t wgs = groups;
+    if constexpr (ACT == 1) {
+        // as many workgroups as are resident at once (the same number on every CU), each
+        // striding over the row groups
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, reinterpret_cast<const void*>(&rotquant_kernel<BLK, OUT, NCH, ACT, W>), 64 * kWaves, 0) !=
+                hipSuccess ||
+            per_cu <= 0)
+            per_cu = 1;
+        wgs = std::min<int64_t>(groups, static_cast<int64_t>(device_cu_count()) * per_cu);
+    }
+    if (wgs == 0) return 0;
+    hipLaunchKernelGGL((rotquant_kernel<BLK, OUT, NCH, ACT, W>), dim3(static_cast<unsigned>(wgs)),
+                       dim3(64 * kWaves), 0, stream, x, ldx, static_cast<int>(M), static_cast<int>(K),
+                       static_cast<uint8_t*>(q), ldq, scale);
+    return launch_status("rotquant");
+}
+
+template <int BLK, int OUT, int ACT>
+int dispatch_nch(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, void* q, int64_t ldq,
+                 float* scale, hipStream_t stream) {
+    const int chunks = static_cast<int>((K + 1023) / 1024);
+    switch (chunks) {
+        case 1: return launch_rq<BLK, OUT, 1, ACT, 1>(x, M, K, ldx, q, ldq, scale, stream);
+        case 2: return launch_rq<BLK, OUT, 2, ACT, 1>(x, M, K, ldx, q, ldq, scale, stream);
+        case 3: return launch_rq<BLK, OUT, 3, ACT, 1>(x, M, K, ldx, q, ldq, scale, stream);
+        case 4: return launch_rq<BLK, OUT, 4, ACT, 1>(x, M, K, ldx, q, ldq, scale, stream);
+        case 5: case 6: return launch_rq<BLK, OUT, 3, ACT, 2>(x, M, K, ldx, q, ldq, scale, stream);
+        case 7: case 8: return launch_rq<BLK, OUT, 4, ACT, 2>(x, M, K, ldx, q, ldq, scale, stream);
+        case 9: case 10: case 11: case 12: return launch_rq<BLK, OUT, 3, ACT, 4>(x, M, K, ldx, q, ldq, scale, stream);
+        case 13: case 14: case 15: case 16: return launch_rq<BLK, OUT, 4, ACT, 4>(x, M, K, ldx, q, ldq, scale, stream);
+        default: break;
+    }
+    set_error("rotquant: K=%lld exceeds 16384", static_cast<long long>(K));
+    return -2;
+}
+
+template <int BLK, int ACT>
+int dispatch_out(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int bits, int packed, void* q,
+                 int64_t ldq, float* scale, hipStream_t stream) {
+    if (bits == 8) return dispatch_nch<BLK, 0, ACT>(x, M, K, ldx, q, ldq, scale, stream);
+    if (packed == 1) return dispatch_nch<BLK, 2, ACT>(x, M, K, ldx, q, ldq, scale, stream);
+    if (packed == 2) return dispatch_nch<BLK, 3, ACT>(x, M, K, ldx, q, ldq, scale, stream);
+    return dispatch_nch<BLK, 1, ACT>(x, M, K, ldx, q, ldq, scale, stream);
+}
+
+template <int ACT>
+int launch_rotquant_impl(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits,
+                         int packed, void* q, int64_t ldq, float* scale, hipStream_t stream) {
+    switch (hblock) {
+        case 0: return dispatch_out<1, ACT>(x, M, K, ldx, bits, packed, q, ldq, scale, stream);
+        case 16: return dispatch_out<16, ACT>(x, M, K, ldx, bits, packed, q, ldq, scale, stream);
+        case 64: return dispatch_out<64, ACT>(x, M, K, ldx, bits, packed, q, ldq, scale, stream);
+        case 256: return dispatch_out<256, ACT>(x, M, K, ldx, bits, packed, q, ldq, scale, stream);
+        default: break;
+    }
+    set_error("rotquant: hblock must be 0, 16, 64 or 256 (got %d)", hblock);
+    return -1;
+}
+
+}  // namespace
+}  // namespace mq

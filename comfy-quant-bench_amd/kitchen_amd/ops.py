@@ -11,6 +11,12 @@ Names, keyword arguments and error messages follow the reference's contract:
       tools/verify_w4a4.py:342-370
   quantize_int4_rowwise_convrot64(x, convrot_groupsize) -> (qact int8 [M, K/2], x_scale f32 [M])
       patches/comfy_kitchen_swiglu_w4a4_fused.patch:37
+  swiglu_quantize_int4_rowwise_convrot64(h) -> (qact int8 [M, K/2], x_scale f32 [M])
+      tools/ck_swiglu/swiglu_quant.cu:111-120 (h = gate | up [M, 2K])
+input_act="swiglu" takes x as the [gate | up] pair and folds silu(gate) * up into the activation
+quantizer (patches/comfy_kitchen_swiglu_w4a4_fused.patch:17-33,60-63;
+patches/comfyui_swiglu_triton_env.patch:65-97), for every convrot group size and both activation
+widths.
 Every op is a thin host wrapper: the caller's tensors are validated, outputs are allocated with
 torch on the input's device, and the HIP kernels run asynchronously on the current stream.
 """
@@ -50,26 +56,50 @@ def _finish(y: torch.Tensor, x: torch.Tensor, n: int, out_dtype) -> torch.Tensor
 
 # --------------------------------------------------------------------------- activation quantizers
 
-def rotate_quantize(x: torch.Tensor, convrot_groupsize: int | None, bits: int, packed: bool | int = False):
+def rotate_quantize(x: torch.Tensor, convrot_groupsize: int | None, bits: int, packed: bool | int = False,
+                    swiglu: bool = False):
     """Rotate x [.., K] by H_cg per block and quantize per token to int8 (bits 8) or int4 (bits 4).
 
     packed: False / Q_BYTES one code per byte, True / Q_PACKED packed int4 [M, K/2], Q_X16ALT the
     group GEMM's int4 operand layout (16 * q, negated in odd 64-column groups).
+    swiglu: x is [.., 2K] = gate | up and the quantized activation is bf16(silu(gate) * up).
     Returns (q, scale): q int8 [M, K] or [M, K/2], scale float32 [M]."""
     layout = int(packed)
-    k = x.shape[-1]
-    x2 = _as_bf16_2d(x, k)
+    width = x.shape[-1]
+    if swiglu and width % 2:
+        raise ValueError("h must hold gate | up halves")
+    k = width // 2 if swiglu else width
+    x2 = _as_bf16_2d(x, width)
     m = x2.shape[0]
     q = torch.empty((m, k // 2 if layout == _lib.Q_PACKED else k), dtype=torch.int8, device=x2.device)
     s = torch.empty((m,), dtype=torch.float32, device=x2.device)
-    _lib.call("mq_rotquant", x2.data_ptr(), m, k, k, int(convrot_groupsize or 0), int(bits), layout,
-              q.data_ptr(), q.stride(0), s.data_ptr(), _lib.stream_of(x2))
+    _lib.call("mq_swiglu_rotquant" if swiglu else "mq_rotquant", x2.data_ptr(), m, k, width,
+              int(convrot_groupsize or 0), int(bits), layout, q.data_ptr(), q.stride(0), s.data_ptr(),
+              _lib.stream_of(x2))
     return q, s
+
+
+def _input_act_swiglu(input_act: str | None) -> bool:
+    """True for the fused SwiGLU prologue; the reference's other eager activations are not built."""
+    if input_act is None:
+        return False
+    if input_act == "swiglu":
+        return True
+    raise NotImplementedError(f"input_act={input_act!r} is not fused in this build (only 'swiglu')")
 
 
 def quantize_int4_rowwise_convrot64(x: torch.Tensor, convrot_groupsize: int = 256):
     """comfy-kitchen's activation quantizer: (qact int8 [M, K/2] packed int4, x_scale f32 [M])."""
     return rotate_quantize(x, convrot_groupsize, 4, packed=True)
+
+
+def swiglu_quantize_int4_rowwise_convrot64(h: torch.Tensor, convrot_groupsize: int = 256):
+    """The fused SwiGLU quantizer of tools/ck_swiglu/swiglu_quant.cu:111-120: h [M, 2K] = gate | up,
+    returns (qact int8 [M, K/2] packed int4, x_scale f32 [M]) of bf16(silu(gate) * up)."""
+    k = h.shape[-1] // 2
+    if k % 256 != 0 or k > 16384:
+        raise ValueError("K must be a multiple of 256 and <= 16384")
+    return rotate_quantize(h, convrot_groupsize, 4, packed=True, swiglu=True)
 
 
 def quantize_int8_rowwise_convrot(x: torch.Tensor, convrot_groupsize: int | None = 256):
@@ -155,20 +185,20 @@ def convrot_w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.T
         raise ValueError(f"ConvRot W4A4 linear_dtype must be 'int4' or 'int8', got {linear_dtype!r}")
     if quant_group_size != INT4_GROUP_SIZE:
         raise ValueError(f"int4 MMA kernel requires quant_group_size {INT4_GROUP_SIZE}")
-    if input_act is not None:
-        raise NotImplementedError(f"input_act={input_act!r} is not fused in this build")
-    if x.shape[-1] != qweight.shape[-1] * 2:
-        raise ValueError(f"Input K={x.shape[-1]} does not match qweight K={qweight.shape[-1] * 2}")
-    if x.shape[-1] % convrot_groupsize != 0:
-        raise ValueError(f"Input K={x.shape[-1]} is not divisible by convrot_groupsize={convrot_groupsize}")
-    n, k = qweight.shape[0], x.shape[-1]
+    swiglu = _input_act_swiglu(input_act)
+    k = x.shape[-1] // 2 if swiglu else x.shape[-1]
+    if k != qweight.shape[-1] * 2:
+        raise ValueError(f"Input K={k} does not match qweight K={qweight.shape[-1] * 2}")
+    if k % convrot_groupsize != 0:
+        raise ValueError(f"Input K={k} is not divisible by convrot_groupsize={convrot_groupsize}")
+    n = qweight.shape[0]
     bits = 4 if linear_dtype == "int4" else 8
     if wscales.dim() == 2 and wscales.shape[1] > 1:
         if wscales.shape != (n, k // quant_group_size):
             raise ValueError(f"per-group wscales must be [{n}, {k // quant_group_size}], got {list(wscales.shape)}")
         # int4 activations go to the group GEMM in its x16 operand layout
         layout = _lib.Q_X16ALT if bits == 4 else _lib.Q_BYTES
-        qa, sa = rotate_quantize(x, convrot_groupsize, bits, layout)
+        qa, sa = rotate_quantize(x, convrot_groupsize, bits, layout, swiglu)
         b = _bias_bf16(bias, n, qa.device)
         ws = wscales.to(torch.float16).contiguous()
         act = _lib.ACT_X16ALT if bits == 4 else _lib.ACT_I8
@@ -177,7 +207,7 @@ def convrot_w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.T
         ws = wscales.reshape(-1).to(torch.float32).contiguous()
         if ws.numel() != n:
             raise ValueError(f"per-row wscales must have {n} elements, got {ws.numel()}")
-        qa, sa = rotate_quantize(x, convrot_groupsize, bits)
+        qa, sa = rotate_quantize(x, convrot_groupsize, bits, swiglu=swiglu)
         b = _bias_bf16(bias, n, qa.device)
         y = gemm_rowscale(qa, sa, qweight.contiguous(), ws, b, n, 4)
     return _finish(y, x, n, x.dtype if x.dtype in (torch.float16, torch.float32) else None)
@@ -220,15 +250,14 @@ def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tenso
                 input_act: str | None = None) -> torch.Tensor:
     """int8_tensorwise linear: int8 per-row weights [N, K] + F32 scale [N, 1], int8 per-token
     activations (after H_cg when convrot), full-K int32 accumulation."""
-    if input_act is not None:
-        raise NotImplementedError(f"input_act={input_act!r} is not fused in this build")
-    k = x.shape[-1]
+    swiglu = _input_act_swiglu(input_act)
+    k = x.shape[-1] // 2 if swiglu else x.shape[-1]
     n = weight.shape[0]
     if weight.shape[1] != k:
         raise ValueError(f"Input K={k} does not match weight K={weight.shape[1]}")
     if convrot and k % convrot_groupsize:
         raise ValueError(f"Input K={k} is not divisible by convrot_groupsize={convrot_groupsize}")
-    qa, sa = rotate_quantize(x, convrot_groupsize if convrot else None, 8)
+    qa, sa = rotate_quantize(x, convrot_groupsize if convrot else None, 8, swiglu=swiglu)
     b = _bias_bf16(bias, n, qa.device)
     ws = weight_scale.reshape(-1).to(torch.float32).contiguous()
     y = gemm_rowscale(qa, sa, weight.contiguous(), ws, b, n, 8)

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MQ_ABI_VERSION 2
+#define MQ_ABI_VERSION 3
 
 enum {
     MQ_OK = 0,
@@ -75,6 +75,26 @@ const char* mq_last_error(void);
  */
 int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits, int packed,
                 void* q, int64_t ldq, float* scale, void* stream);
+
+/*
+ * SwiGLU prologue fused into rotate + quantize: the activation is
+ *   a[m,k] = bf16( silu(h[m,k]) * h[m,K+k] )      (fp32 arithmetic, one rounding to bf16)
+ * formed while loading the gate | up row, then rotated and quantized exactly as mq_rotquant does
+ * with x = a. The bf16 intermediate never touches memory.
+ *
+ * Replaces swiglu_quantize_int4_rowwise_convrot64(h) (tools/ck_swiglu/swiglu_quant.cu:23-97 and
+ * :111-120, dispatched by convrot_w4a4_linear(..., input_act="swiglu") at
+ * patches/comfy_kitchen_swiglu_w4a4_fused.patch:17-33) and generalises it to every Hadamard block,
+ * int8 codes and the group GEMM's code layouts. silu(g) = g / (1 + exp(-g)) with this library's
+ * own fp32 exp (within 2 ulp; the reference uses a hardware approximation) and an IEEE division.
+ *
+ *   h      bf16 [M, 2K]: gate in columns [0, K), up in [K, 2K); row stride ldh >= 2K elements
+ *          (ldh % 8 == 0, 16-byte aligned base)
+ *   other arguments as mq_rotquant (K is the width of the activation, half of h's).
+ * Requires K % 16 == 0, K <= 16384, K % hblock == 0.
+ */
+int mq_swiglu_rotquant(const void* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits, int packed,
+                       void* q, int64_t ldq, float* scale, void* stream);
 
 /*
  * Quantized GEMM with per-group weight scales (W4A8 asym / W4A4 sym, configs' scheme):

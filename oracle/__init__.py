@@ -10,6 +10,7 @@ file:line it follows. The modules are:
 
     hadamard   closed-form H_b and the pinned-order radix-4 FWHT
     quant      per-token activation quantizers, weight quantizers, int4 packing
+    swiglu     the SwiGLU prologue (silu correctly rounded to fp32, product rounded to bf16)
     gemm       exact integer per-group partials and the fp64 epilogue
     torch_path the reference's CPU torch path (rotate, quantize, dequantize, fp32 matmul),
                timed as the CPU baseline

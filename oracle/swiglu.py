@@ -1,0 +1,62 @@
+"""SwiGLU prologue of the activation quantizer, restated in numpy float32.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+Reference: `tools/ck_swiglu/swiglu_quant.cu:23-97`. The input h [M, 2K] holds gate | up; each
+element of the activation is `a = g / (1 + exp(-g)) * u` computed in fp32 and rounded once to the
+input dtype (bf16), straight from h (:56-66, "silu(g) * u in fp32, one rounding below"); the
+rounded activation then goes through the same rotation and per-token quantization as an ordinary
+input. The dispatch (`patches/comfyui_swiglu_triton_env.patch:65-97`,
+`patches/comfy_kitchen_swiglu_w4a4_fused.patch:17-33`) passes the whole `[gate | up]` row, K a
+multiple of 256 and at most 16384.
+
+The reference evaluates exp with CUDA's hardware approximation `__expf`, whose bits are not
+published. This build takes silu correctly rounded to fp32 instead, the exact function the
+reference approximates:
+
+    silu32(g) = RN_fp32(g / (1 + exp(-g)))            (exact real arithmetic, one rounding)
+    swiglu_bf16(g, u) = RN_bf16(RN_fp32(silu32(g) * u))
+
+Here silu32 is evaluated in float64 and rounded to fp32. For the bf16 gate values this path sees,
+that equals the correctly rounded value; tests/test_oracle_swiglu.py checks all 65536 bf16
+patterns against exact decimal arithmetic. Closed forms it reproduces: |g| < 2^-25 gives g / 2,
+g >= 128 gives g and g <= -128 gives -0.
+
+Pinning (tests/test_oracle_swiglu.py): exhaustive comparison with Python's decimal module at
+60 digits over every finite bf16 gate (rounded to the nearest fp32 with ties to even), the
+closed-form regions, silu's identities (silu(g) - silu(-g) = g, sign and monotonicity on
+g > -1.27), the bf16 rounding of the product against a float64 product, and the composition
+with the rotation and quantizer.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .quant import bf16_bits_to_f32, f32_to_bf16_bits, rotquant
+
+F32 = np.float32
+
+
+def silu32(g: np.ndarray) -> np.ndarray:
+    """silu(g) = g / (1 + exp(-g)) correctly rounded to fp32, for g holding bf16 values."""
+    g64 = np.asarray(g, dtype=F32).astype(np.float64)
+    with np.errstate(over="ignore"):
+        return (g64 / (1.0 + np.exp(-g64))).astype(F32)
+
+
+def swiglu_bf16(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """bf16-rounded silu(g) * u (swiglu_quant.cu:64 with silu correctly rounded), returned as
+    float32 holding bf16 values."""
+    prod = (silu32(g) * np.asarray(u, dtype=F32)).astype(F32)
+    return bf16_bits_to_f32(f32_to_bf16_bits(prod))
+
+
+def swiglu_rotquant(h: np.ndarray, block: int, bits: int) -> tuple[np.ndarray, np.ndarray]:
+    """Fused SwiGLU quantizer: h float32 (bf16 values) [M, 2K] = gate | up -> rotquant of the
+    bf16 activation [M, K] (swiglu_quant.cu:23-97 with the per-token int8 / int4 quantizer of
+    this path). Returns (q int8 codes [M, K], s float32 [M])."""
+    h = np.asarray(h, dtype=F32)
+    if h.shape[1] % 2:
+        raise ValueError("h must hold gate | up halves")
+    k = h.shape[1] // 2
+    return rotquant(swiglu_bf16(h[:, :k], h[:, k:]), block, bits)

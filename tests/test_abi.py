@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mq_abi_version() == 2
+    assert lib.mq_abi_version() == 3
 
 
 def _err(lib):
@@ -65,6 +65,18 @@ def test_rotquant_validation_rejects_before_launch(lib):
     assert "layout" in _err(lib)
     # M == 0 is a valid no-op
     assert lib.mq_rotquant(None, 0, 256, 256, 256, 8, 0, None, 256, None, None) == 0
+
+
+def test_swiglu_rotquant_validation_rejects_before_launch(lib):
+    # h holds gate | up: its row stride must cover 2K columns
+    assert lib.mq_swiglu_rotquant(None, 4, 256, 256, 256, 8, 0, None, 256, None, None) == -1
+    assert "null" in _err(lib)
+    assert lib.mq_swiglu_rotquant(None, 4, 256, 384, 256, 8, 0, None, 256, None, None) == -1
+    assert "swiglu_rotquant" in _err(lib)
+    assert lib.mq_swiglu_rotquant(None, 4, 320, 640, 256, 8, 0, None, 320, None, None) == -1
+    assert "not a multiple of the group size" in _err(lib)
+    assert lib.mq_swiglu_rotquant(None, 4, 32768, 65536, 256, 8, 0, None, 32768, None, None) == -2
+    assert lib.mq_swiglu_rotquant(None, 0, 256, 512, 256, 4, 1, None, 128, None, None) == 0
 
 
 def test_gemm_validation_rejects_before_launch(lib):
