@@ -124,6 +124,30 @@ int mq_swiglu_rotquant(const void* h, int64_t M, int64_t K, int64_t ldh, int hbl
                                   static_cast<hipStream_t>(stream));
 }
 
+int mq_decode_w4a8_codebook(const void* qdata, int64_t ldq, const void* s_rel, int64_t lds, const float* s_channel,
+                            const float* codebook, int group_size, int64_t N, int64_t K, int8_t* q8, int64_t ldq8,
+                            float* row_scale, void* stream) {
+    clear_error();
+    MQ_REQUIRE(N >= 0 && K > 0, "decode_w4a8_codebook: bad shape N=%lld K=%lld", (long long)N, (long long)K);
+    MQ_REQUIRE(N < (int64_t(1) << 31) && K < (int64_t(1) << 30), "decode_w4a8_codebook: shape too large");
+    MQ_REQUIRE(group_size >= 4 && (16 % group_size == 0 || group_size % 16 == 0),
+               "decode_w4a8_codebook: group_size must be >= 4 and divide or be a multiple of 16 (got %d)", group_size);
+    MQ_REQUIRE(K % 16 == 0 && K % group_size == 0,
+               "decode_w4a8_codebook: K=%lld must be a multiple of 16 and of group_size %d", (long long)K, group_size);
+    if (N == 0) return MQ_OK;
+    MQ_REQUIRE(qdata && s_rel && s_channel && q8 && row_scale, "decode_w4a8_codebook: null pointer");
+    MQ_REQUIRE(ldq >= K / 2 && ldq % 4 == 0 && aligned(qdata, 4),
+               "decode_w4a8_codebook: qdata needs ldq >= K/2 bytes, ldq %% 4 == 0 and a 4-byte aligned base");
+    MQ_REQUIRE(lds >= K / group_size, "decode_w4a8_codebook: s_rel needs lds >= K / group_size bytes");
+    MQ_REQUIRE(ldq8 >= K && ldq8 % 8 == 0 && aligned(q8, 8),
+               "decode_w4a8_codebook: q8 needs ldq8 >= K bytes, ldq8 %% 8 == 0 and an 8-byte aligned base");
+    MQ_REQUIRE(aligned(s_channel, 4) && aligned(row_scale, 4) && (!codebook || aligned(codebook, 4)),
+               "decode_w4a8_codebook: fp32 operands must be 4-byte aligned");
+    return launch_decode_w4a8_codebook(static_cast<const uint8_t*>(qdata), ldq, static_cast<const uint8_t*>(s_rel),
+                                       lds, s_channel, codebook, group_size, N, K, q8, ldq8, row_scale,
+                                       static_cast<hipStream_t>(stream));
+}
+
 int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
                      const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
                      const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,

@@ -24,6 +24,11 @@ int launch_rotquant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int hb
 int launch_swiglu_rotquant(const uint16_t* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
                            int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
 
+// --- load-time decode of the shipped asym_w4a8_int8 codebook weights (mq_codebook.hip)
+int launch_decode_w4a8_codebook(const uint8_t* qdata, int64_t ldq, const uint8_t* s_rel, int64_t lds,
+                                const float* s_channel, const float* codebook, int group_size, int64_t N,
+                                int64_t K, int8_t* q8, int64_t ldq8, float* row_scale, hipStream_t stream);
+
 // --- GEMMs (mq_gemm.hip)
 enum class WKind : int { U4Asym = 0, I4Sym = 1, I8 = 2 };
 enum class Epi : int { GroupScale = 0, GroupPartials = 1, RowScale = 2, RowAcc = 3 };

@@ -13,6 +13,7 @@ from . import weights
 from ._lib import LIB_PATH, MQError, load
 from .ops import (
     convrot_w4a4_linear,
+    decode_w4a8_codebook_weight,
     gemm_rowscale,
     gemm_rowscale_acc,
     gemm_w4_group,
@@ -21,6 +22,7 @@ from .ops import (
     quantize_int4_rowwise_convrot64,
     quantize_int8_rowwise_convrot,
     rotate_quantize,
+    swiglu_quantize_int4_rowwise_convrot64,
     w4a8_int8_linear,
 )
 from .weights import (
@@ -34,6 +36,7 @@ __all__ = [
     "LIB_PATH", "MQError", "load", "weights",
     "convrot_w4a4_linear", "w4a8_int8_linear", "int8_linear",
     "quantize_int4_rowwise_convrot64", "quantize_int8_rowwise_convrot", "rotate_quantize",
+    "swiglu_quantize_int4_rowwise_convrot64", "decode_w4a8_codebook_weight",
     "gemm_w4_group", "gemm_w4_group_partials", "gemm_rowscale", "gemm_rowscale_acc",
     "quantize_w4a8_asym_weight", "quantize_w4a4_group_weight", "quantize_convrot_w4a4_weight",
     "quantize_int8_convrot_weight",

@@ -11,7 +11,7 @@ import os
 
 import torch  # noqa: F401  (must be imported before the library is loaded)
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmq.so")
 
@@ -26,6 +26,8 @@ _SIGNATURES = {
     "mq_last_error": ([], ctypes.c_char_p),
     "mq_rotquant": ([c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_vp], c_int),
     "mq_swiglu_rotquant": ([c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_vp], c_int),
+    "mq_decode_w4a8_codebook": ([c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_int, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp],
+                                c_int),
     "mq_gemm_w4_group": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_vp,
                           c_i64, c_i64, c_i64, c_i64, c_vp], c_int),
     "mq_gemm_w4_group_partials": ([c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_i64, c_i64, c_i64,

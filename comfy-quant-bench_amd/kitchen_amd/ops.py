@@ -107,6 +107,43 @@ def quantize_int8_rowwise_convrot(x: torch.Tensor, convrot_groupsize: int | None
     return rotate_quantize(x, convrot_groupsize, 8)
 
 
+# --------------------------------------------------------------------------- shipped W4A8 decode
+
+def _u8(t: torch.Tensor) -> torch.Tensor:
+    """Raw bytes of an 8-bit tensor (int8, uint8 or float8_e4m3fn)."""
+    if t.element_size() != 1:
+        raise ValueError(f"expected an 8-bit tensor, got {t.dtype}")
+    return t.contiguous().view(torch.uint8)
+
+
+def decode_w4a8_codebook_weight(qdata: torch.Tensor, s_rel: torch.Tensor, s_channel: torch.Tensor,
+                                codebook=None, group_size: int = 16):
+    """Decode comfy-kitchen's shipped asym_w4a8_int8 weight (qdata I8 [N, K/2], s_rel fp8 e4m3fn
+    or its U8 bytes [N, K/gs], s_channel F32 [N], codebook F32 [16] or None) to
+    (q8 int8 [N, K], row_scale float32 [N]) for the int8 row-scale GEMM; the rule is in
+    include/mq.h (mq_decode_w4a8_codebook)."""
+    if not qdata.is_cuda:
+        raise ValueError("kitchen_amd ops run on the GPU: qdata must be a device tensor")
+    q = _u8(qdata)
+    n, k = q.shape[0], q.shape[1] * 2
+    sr = _u8(s_rel)
+    if sr.shape != (n, k // group_size):
+        raise ValueError(f"s_rel must be [{n}, {k // group_size}] for group_size {group_size}, got {list(sr.shape)}")
+    sc = s_channel.reshape(-1).to(torch.float32).contiguous()
+    if sc.numel() != n:
+        raise ValueError(f"s_channel must have {n} elements, got {sc.numel()}")
+    cb = None
+    if codebook is not None:
+        cb = codebook.reshape(-1).to(device=q.device, dtype=torch.float32).contiguous()
+        if cb.numel() != 16:
+            raise ValueError(f"codebook must have 16 levels, got {cb.numel()}")
+    q8 = torch.empty((n, k), dtype=torch.int8, device=q.device)
+    rs = torch.empty((n,), dtype=torch.float32, device=q.device)
+    _lib.call("mq_decode_w4a8_codebook", q.data_ptr(), q.stride(0), sr.data_ptr(), sr.stride(0), sc.data_ptr(),
+              _lib.ptr(cb), int(group_size), n, k, q8.data_ptr(), q8.stride(0), rs.data_ptr(), _lib.stream_of(q))
+    return q8, rs
+
+
 # --------------------------------------------------------------------------- GEMMs
 
 def _check_w4_group(qa, qweight, wscales, wzeros, n, group_size):
@@ -216,23 +253,36 @@ def convrot_w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.T
 def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, s_channel=None, codebook=None,
                      correction=None, bias=None, group_size: int = INT4_GROUP_SIZE, convrot_groupsize: int = 256,
                      out_dtype=torch.bfloat16) -> torch.Tensor:
-    """W4A8 linear: H_cg rotation + int8 per-token activations + 4-bit weights.
+    """W4A8 linear: H_cg rotation + int8 per-token activations + 4-bit weights. Two layouts:
 
-    Configs' scheme (uint4 asymmetric per group): qdata uint8 [N, K/2] packed codes, s_rel fp16
-    [N, K/group] per-group scales, correction uint8 [N, ceil(K/group/2)] packed uint4 zero-points
-    (None = signed int4 weights), s_channel and codebook None. The comfy-kitchen codebook layout
-    (fp8 s_rel + F32 s_channel + F32 codebook[16]) is not implemented in this build."""
-    if codebook is not None or s_channel is not None or s_rel.dtype != torch.float16:
-        raise NotImplementedError("comfy-kitchen codebook W4A8 layout (fp8 s_rel, s_channel, codebook) "
-                                  "is not implemented; pass fp16 per-group s_rel and packed uint4 zero-points")
-    if group_size != INT4_GROUP_SIZE:
-        raise ValueError(f"W4A8 kernel requires group_size {INT4_GROUP_SIZE}, got {group_size}")
+    * configs' scheme (uint4 asymmetric per group): qdata uint8 [N, K/2] packed codes, s_rel fp16
+      [N, K/group] per-group scales, correction uint8 [N, ceil(K/group/2)] packed uint4
+      zero-points (None = signed int4 weights), s_channel and codebook None; group GEMM.
+    * comfy-kitchen's shipped asym_w4a8_int8 (tools/_formats.py:79-125): qdata I8 [N, K/2] codes,
+      s_rel fp8 e4m3fn (or its U8 bytes) [N, K/group], s_channel F32 [N], codebook F32 [16] or
+      None, no correction; the weight is decoded to int8 with a per-row scale on each call
+      (decode_w4a8_codebook_weight) and runs on the int8 row-scale GEMM."""
     k = x.shape[-1]
     if k != qdata.shape[-1] * 2:
         raise ValueError(f"Input K={k} does not match qdata K={qdata.shape[-1] * 2}")
     if convrot_groupsize and k % convrot_groupsize:
         raise ValueError(f"Input K={k} is not divisible by convrot_groupsize={convrot_groupsize}")
     n = qdata.shape[0]
+    if s_channel is not None or codebook is not None or s_rel.element_size() == 1:
+        if correction is not None:
+            raise NotImplementedError("asym_w4a8_int8 with a correction tensor (asymmetric) is not supported; "
+                                      "the reference's loader drops it as well")
+        if s_channel is None:
+            raise ValueError("the shipped asym_w4a8_int8 layout needs s_channel")
+        q8, rs = decode_w4a8_codebook_weight(qdata, s_rel, s_channel, codebook, group_size)
+        qa, sa = rotate_quantize(x, convrot_groupsize, 8)
+        b = _bias_bf16(bias, n, qa.device)
+        y = gemm_rowscale(qa, sa, q8, rs, b, n, 8)
+        return _finish(y, x, n, out_dtype)
+    if s_rel.dtype != torch.float16:
+        raise ValueError(f"per-group s_rel must be float16 (configs' scheme) or fp8 bytes, got {s_rel.dtype}")
+    if group_size != INT4_GROUP_SIZE:
+        raise ValueError(f"W4A8 kernel requires group_size {INT4_GROUP_SIZE}, got {group_size}")
     if s_rel.shape != (n, k // group_size):
         raise ValueError(f"s_rel must be [{n}, {k // group_size}], got {list(s_rel.shape)}")
     if correction is not None and correction.shape != (n, (k // group_size + 1) // 2):

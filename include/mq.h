@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MQ_ABI_VERSION 3
+#define MQ_ABI_VERSION 4
 
 enum {
     MQ_OK = 0,
@@ -95,6 +95,29 @@ int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, in
  */
 int mq_swiglu_rotquant(const void* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits, int packed,
                        void* q, int64_t ldq, float* scale, void* stream);
+
+/*
+ * Load-time decode of comfy-kitchen's shipped asym_w4a8_int8 weight (tools/_formats.py:79-125:
+ * qdata I8 [N, K/2] 4-bit codes, s_rel fp8 e4m3fn stored as U8 [N, K/gs], s_channel F32 [N],
+ * codebook F32 [16] or none) to an int8 weight with a per-row scale, which the int8 row-scale GEMM
+ * (mq_gemm_rowscale, wbits 8) then takes; comfy-kitchen finishes the same way ("Decoded W4A8 is a
+ * ConvRot INT8 weight with a per-row scale", patches/comfy_kitchen_w4a8_dequant_fused.patch:12-15).
+ * comfy-kitchen's own decode rule is not in the reference tree; this one is:
+ *   level = codebook[code] (unsigned nibble, low nibble = even k), or the signed nibble if
+ *           codebook is NULL
+ *   t[n,k] = fp32(level * fp8(s_rel[n, k / group_size])),  s[n] = fp32(max_k |t[n,k]| / 127)
+ *   q8[n,k] = clamp(rne(t[n,k] / s[n]), -127, 127)  (0 for an all-zero row)
+ *   row_scale[n] = fp32(s[n] * s_channel[n])
+ *
+ *   qdata  [N, K/2] bytes, stride ldq (ldq % 4 == 0, 4-byte aligned)
+ *   s_rel  [N, K/group_size] fp8 bytes, stride lds
+ *   q8     int8 [N, K], stride ldq8 (ldq8 % 8 == 0, 8-byte aligned); row_scale fp32 [N]
+ * Requires K % 16 == 0, K % group_size == 0, group_size >= 4 dividing or a multiple of 16
+ * (the accepts() rule of tools/_formats.py:86-97).
+ */
+int mq_decode_w4a8_codebook(const void* qdata, int64_t ldq, const void* s_rel, int64_t lds, const float* s_channel,
+                            const float* codebook, int group_size, int64_t N, int64_t K, int8_t* q8, int64_t ldq8,
+                            float* row_scale, void* stream);
 
 /*
  * Quantized GEMM with per-group weight scales (W4A8 asym / W4A4 sym, configs' scheme):

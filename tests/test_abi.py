@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mq_abi_version() == 3
+    assert lib.mq_abi_version() == 4
 
 
 def _err(lib):
@@ -77,6 +77,16 @@ def test_swiglu_rotquant_validation_rejects_before_launch(lib):
     assert "not a multiple of the group size" in _err(lib)
     assert lib.mq_swiglu_rotquant(None, 4, 32768, 65536, 256, 8, 0, None, 32768, None, None) == -2
     assert lib.mq_swiglu_rotquant(None, 0, 256, 512, 256, 4, 1, None, 128, None, None) == 0
+
+
+def test_decode_codebook_validation_rejects_before_launch(lib):
+    assert lib.mq_decode_w4a8_codebook(None, 128, None, 16, None, None, 12, 8, 192, None, 192, None, None) == -1
+    assert "group_size" in _err(lib)
+    assert lib.mq_decode_w4a8_codebook(None, 128, None, 16, None, None, 16, 8, 200, None, 200, None, None) == -1
+    assert "multiple of 16" in _err(lib)
+    assert lib.mq_decode_w4a8_codebook(None, 128, None, 16, None, None, 16, 8, 256, None, 256, None, None) == -1
+    assert "null" in _err(lib)
+    assert lib.mq_decode_w4a8_codebook(None, 128, None, 16, None, None, 16, 0, 256, None, 256, None, None) == 0
 
 
 def test_gemm_validation_rejects_before_launch(lib):
