@@ -1,0 +1,161 @@
+"""The caller side of the boundary: opaque torch custom ops for torch.compile, the backend swap
+for ComfyUI's `quant_ops.ck`, and a loader that turns a quantized checkpoint's layers into
+callables.
+
+* `register_custom_ops()` wraps the linears in `torch.library.custom_op(..., mutates_args=())`
+  with fakes returning `x.new_empty((*x.shape[:-1], N))`, the fix `compile_support.py:75-117`
+  applies to comfy-kitchen's `convrot_w4a4_linear` (Dynamo otherwise traces into the kernel call
+  and fails on a FakeTensor data pointer). Namespace `kitchen_amd`; idempotent.
+* `install_backend(ck)` sets the drop-in ops on a comfy-kitchen-like namespace (ComfyUI calls
+  `quant_ops.ck.<op>(...)` with keyword arguments, `patches/comfyui_swiglu_triton_env.patch:88-95`).
+* `layer_linear(tensors, config)` maps one layer's tensors and its `_quantization_metadata` entry
+  (`tools/_formats.py:109-111`, `tools/verify_w4a4.py:205-212`) to the op the loader would call,
+  with the loader's constants (`quant_group_size=64`, `linear_dtype="int4"`,
+  `tools/_native_probe.py:81-100`); `load_quantized(path)` does it for every layer of a file.
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+from typing import Callable
+
+import torch
+
+from . import convert as _conv
+from . import ops
+
+LOADER_QUANT_GROUP_SIZE = 64
+LOADER_LINEAR_DTYPE = "int4"
+
+_registered: dict[str, Callable] = {}
+
+
+def register_custom_ops() -> dict[str, Callable]:
+    """Register the opaque ops once; returns {name: dispatching wrapper with the ops' signature}."""
+    if _registered:
+        return dict(_registered)
+
+    @torch.library.custom_op("kitchen_amd::convrot_w4a4_linear", mutates_args=())
+    def _convrot(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.Tensor, bias: torch.Tensor | None,
+                 convrot_groupsize: int, quant_group_size: int, linear_dtype: str,
+                 input_act: str | None) -> torch.Tensor:
+        return ops.convrot_w4a4_linear(x, qweight, wscales, bias, convrot_groupsize=convrot_groupsize,
+                                       quant_group_size=quant_group_size, linear_dtype=linear_dtype,
+                                       input_act=input_act)
+
+    @_convrot.register_fake
+    def _(x, qweight, wscales, bias, convrot_groupsize, quant_group_size, linear_dtype, input_act):
+        return x.new_empty((*x.shape[:-1], qweight.shape[0]))
+
+    @torch.library.custom_op("kitchen_amd::w4a8_int8_linear", mutates_args=())
+    def _w4a8(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, s_channel: torch.Tensor | None,
+              codebook: torch.Tensor | None, correction: torch.Tensor | None, bias: torch.Tensor | None,
+              group_size: int, convrot_groupsize: int, out_dtype: torch.dtype) -> torch.Tensor:
+        return ops.w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook, correction, bias, group_size,
+                                    convrot_groupsize, out_dtype)
+
+    @_w4a8.register_fake
+    def _(x, qdata, s_rel, s_channel, codebook, correction, bias, group_size, convrot_groupsize, out_dtype):
+        return x.new_empty((*x.shape[:-1], qdata.shape[0]), dtype=out_dtype)
+
+    @torch.library.custom_op("kitchen_amd::int8_linear", mutates_args=())
+    def _int8(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, bias: torch.Tensor | None,
+              out_dtype: torch.dtype, convrot: bool, convrot_groupsize: int, input_act: str | None) -> torch.Tensor:
+        return ops.int8_linear(x, weight, weight_scale, bias, out_dtype, convrot, convrot_groupsize, input_act)
+
+    @_int8.register_fake
+    def _(x, weight, weight_scale, bias, out_dtype, convrot, convrot_groupsize, input_act):
+        return x.new_empty((*x.shape[:-1], weight.shape[0]), dtype=out_dtype)
+
+    def convrot_w4a4_linear(x, qweight, wscales, bias=None, convrot_groupsize=256, quant_group_size=64,
+                            linear_dtype="int4", input_act=None):
+        return torch.ops.kitchen_amd.convrot_w4a4_linear(x, qweight, wscales, bias, int(convrot_groupsize),
+                                                         int(quant_group_size), str(linear_dtype), input_act)
+
+    def w4a8_int8_linear(x, qdata, s_rel, s_channel=None, codebook=None, correction=None, bias=None,
+                         group_size=64, convrot_groupsize=256, out_dtype=torch.bfloat16):
+        return torch.ops.kitchen_amd.w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook, correction, bias,
+                                                      int(group_size), int(convrot_groupsize), out_dtype)
+
+    def int8_linear(x, weight, weight_scale, bias=None, out_dtype=torch.bfloat16, convrot=False,
+                    convrot_groupsize=256, input_act=None):
+        return torch.ops.kitchen_amd.int8_linear(x, weight, weight_scale, bias, out_dtype, bool(convrot),
+                                                 int(convrot_groupsize), input_act)
+
+    _registered.update(convrot_w4a4_linear=convrot_w4a4_linear, w4a8_int8_linear=w4a8_int8_linear,
+                       int8_linear=int8_linear)
+    return dict(_registered)
+
+
+BACKEND_OPS = ("convrot_w4a4_linear", "w4a8_int8_linear", "int8_linear")
+BACKEND_FUNCTIONS = ("quantize_int4_rowwise_convrot64", "swiglu_quantize_int4_rowwise_convrot64",
+                     "quantize_convrot_w4a4_weight")
+
+
+def install_backend(ck, compile_safe: bool = True) -> list[str]:
+    """Point a comfy-kitchen-like namespace (`comfy.quant_ops.ck`) at this backend; the linears go
+    through the opaque custom ops when compile_safe. Returns the names set."""
+    from . import weights
+
+    lin = register_custom_ops() if compile_safe else {n: getattr(ops, n) for n in BACKEND_OPS}
+    names = []
+    for name in BACKEND_OPS:
+        setattr(ck, name, lin[name])
+        names.append(name)
+    for name in BACKEND_FUNCTIONS:
+        setattr(ck, name, getattr(ops, name, None) or getattr(weights, name))
+        names.append(name)
+    return names
+
+
+def _t(tensors: dict, key: str, required: bool = True):
+    if key in tensors:
+        return tensors[key]
+    if required:
+        raise KeyError(f"quantized layer is missing tensor {key!r}")
+    return None
+
+
+def layer_linear(tensors: dict, layer: str, config: dict, compile_safe: bool = False) -> Callable:
+    """f(x, bias=None) for one quantized layer, dispatched the way the loader dispatches its format."""
+    fmt = config.get("format")
+    lin = register_custom_ops() if compile_safe else {n: getattr(ops, n) for n in BACKEND_OPS}
+    cg = int(config.get("convrot_groupsize", 256))
+    w = _t(tensors, f"{layer}.weight")
+    scale = _t(tensors, f"{layer}.weight_scale", required=fmt != "asym_w4a8_int8")
+    if fmt in ("convrot_w4a4", "w4a4_sym_g64"):
+        dtype = config.get("linear_dtype", LOADER_LINEAR_DTYPE)
+        return lambda x, bias=None, input_act=None: lin["convrot_w4a4_linear"](
+            x, w, scale, bias, convrot_groupsize=cg, quant_group_size=LOADER_QUANT_GROUP_SIZE, linear_dtype=dtype,
+            input_act=input_act)
+    if fmt == "w4a8_asym_g64":
+        zero = _t(tensors, f"{layer}.weight_zero")
+        gs = int(config.get("group_size", 64))
+        return lambda x, bias=None, out_dtype=torch.bfloat16: lin["w4a8_int8_linear"](
+            x, w, scale, None, None, zero, bias, group_size=gs, convrot_groupsize=cg, out_dtype=out_dtype)
+    if fmt == "asym_w4a8_int8":
+        s_rel = _t(tensors, f"{layer}.weight_s_rel")
+        s_ch = _t(tensors, f"{layer}.weight_s_channel")
+        cb = _t(tensors, f"{layer}.weight_codebook", required=False)
+        gs = int(config["group_size"])
+        return lambda x, bias=None, out_dtype=torch.bfloat16: lin["w4a8_int8_linear"](
+            x, w, s_rel, s_ch, cb, None, bias, group_size=gs, convrot_groupsize=cg, out_dtype=out_dtype)
+    if fmt == "int8_tensorwise":
+        convrot = bool(config.get("convrot", cg > 0))
+        return lambda x, bias=None, out_dtype=torch.bfloat16, input_act=None: lin["int8_linear"](
+            x, w, scale, bias, out_dtype, convrot, cg if cg else 256, input_act)
+    raise NotImplementedError(f"{layer}: format {fmt!r} is not on this path")
+
+
+def load_quantized(path, device="cuda", compile_safe: bool = False) -> dict[str, Callable]:
+    """{layer: f(x, bias=None)} for every layer listed in the file's _quantization_metadata."""
+    path = Path(path)
+    header, metadata, data_start = _conv.read_header(path)
+    qm = json.loads(metadata.get("_quantization_metadata", "{}") or "{}")
+    layers = qm.get("layers", {})
+    out = {}
+    for layer, config in layers.items():
+        keys = [k for k in header if k == f"{layer}.weight" or k.startswith(f"{layer}.weight_")]
+        tensors = {k: _conv.read_tensor(path, header[k], data_start).to(device) for k in keys}
+        out[layer] = layer_linear(tensors, layer, config, compile_safe)
+    return out
