@@ -264,7 +264,12 @@ int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     const bool fits32 = a.M * a.lda < (int64_t(1) << 31) && a.N * a.ldw < (int64_t(1) << 31) &&
                         (a.N * a.ldws + a.K / 64) * 2 < (int64_t(1) << 31) && wbytes <= a.ldw;
     // (activation layout 1, int4 codes scaled in the kernel, is served by the 128-tile kernel only)
-    if (a.M > 128 && fits32 && a.act_mode != 1) return launch_gemm_wide(a, wk, epi, stream);
+    // the wide kernel loads the zero-points of four groups as one 2-byte word and two groups'
+    // scales as one dword per weight row
+    const bool zs_aligned =
+        (wk != WKind::U4Asym || (a.ldwz % 2 == 0 && reinterpret_cast<uintptr_t>(a.wz) % 2 == 0)) &&
+        (epi != Epi::GroupScale || (a.ldws % 2 == 0 && reinterpret_cast<uintptr_t>(a.ws16) % 4 == 0));
+    if (a.M > 128 && fits32 && zs_aligned && a.act_mode != 1) return launch_gemm_wide(a, wk, epi, stream);
     switch (wk) {
         case WKind::U4Asym:
             if (epi == Epi::RowScale || epi == Epi::RowAcc) break;

@@ -5,20 +5,23 @@
 // Layout. Waves form a 4 (M) x 2 (N) grid; each owns a 64 x 128 output tile made of 4 x 8 MFMA
 // 16x16 tiles. In the 16x16 output layout lane l holds column l % 16 and rows 4 * (l / 16) + r,
 // r = 0..3, so every lane needs one weight scale per column tile. A (int8 activation codes) and
-// B (weights, unpacked to int8 on their way into LDS) live in a 3-stage LDS ring of 64-byte rows
+// B (weights, unpacked to int8 on their way into LDS) live in a 4-stage LDS ring of 64-byte rows
 // whose four 16-byte chunks are XOR-swizzled by (row >> 1) & 3: the fragment reads (lane l reads
 // chunk l / 16 of row l % 16) are then free of bank conflicts on gfx950, which a padded pitch of 80
 // bytes is not (measured).
 //
-// Pipeline. The main loop is unrolled over six K groups, so the LDS stage (g % 3) and the sign
+// Pipeline. The main loop is unrolled over four K groups, so the LDS stage (g % 4) and the sign
 // parity (g % 2) of every group are compile-time constants and every LDS access is a base register
 // plus an immediate offset. Inside a group the 32 MFMA tiles run column by column (t = 4 j + i);
 // step t issues tile t's MFMA and then the fmas of tile t - 3, so a result is read three MFMAs
-// after it was produced (no wait states) while the MFMA and VALU pipes overlap. B fragments and
-// scales sit in a 4-slot register ring read two columns ahead; A fragments of group g + 1 are
-// read right after their last MFMA in group g. Global loads of group g + 3 are issued in group g,
-// stored (B unpacked) into the stage of group g + 2 at steps 8-11, and one barrier per group
-// closes the ring.
+// after it was produced while the MFMA and VALU pipes overlap. B fragments sit in a 4-slot
+// register ring read three columns ahead; A fragments of group g + 1 are read early in group g.
+// A tiles go from HBM to LDS by buffer_load ... lds, three groups ahead; packed B is loaded into
+// one of two register sets four groups ahead (inline-asm loads with explicit vmcnt waits), unpacked
+// into the stage of group g + 2 at steps 8-9, and one barrier per group closes the ring.
+// Zero-points and scales are loaded once per block of four groups (one 2-byte and one 4-byte load
+// per weight row), not per group: each such load touches one cache line per row, and per-group
+// loads of 1-2 bytes per row were a third of the kernel's L1 -> L2 requests.
 //
 // Per-group scale epilogue without an int->float conversion. The MFMA accumulator of group g
 // is seeded with the bit pattern of 1.5 * 2^23, so the int32 result D = seed + X reads as the
@@ -136,15 +139,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
                                             static_cast<int>(bytes), 0x00020000);
 }
-__device__ __forceinline__ uint4 ld128(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-    return make_uint4(v[0], v[1], v[2], v[3]);
-}
 
 // Buffer loads written as inline asm, so that the kernel alone decides when to wait for them
 // (s_waitcnt vmcnt with counts that follow the pipeline's fixed issue order; the compiler's own
 // count is conservative at the loop header and would wait for loads issued a group later).
 // The descriptor is the same as make_buffer_rsrc builds: base, stride 0, byte range, format word.
+// Each load starts with s_nop 4: the compiler may have just restored the descriptor or the scalar
+// offset from a VGPR lane (v_readlane), and a VMEM instruction reading an SGPR written by VALU
+// needs 5 wait states, which the compiler does not insert in front of inline asm.
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u4v sdesc(const void* base, int64_t bytes) {
     const uint64_t p = reinterpret_cast<uint64_t>(base);
@@ -157,17 +159,17 @@ __device__ __forceinline__ u4v sdesc(const void* base, int64_t bytes) {
 }
 __device__ __forceinline__ u4v asm_ld128(u4v d, int voff, int soff) {
     u4v v;
-    asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
     return v;
 }
-__device__ __forceinline__ uint32_t asm_ld8(u4v d, int voff, int soff) {
+__device__ __forceinline__ uint32_t asm_ld32(u4v d, int voff, int soff) {
     uint32_t v;
-    asm volatile("buffer_load_ubyte %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
+    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
     return v;
 }
 __device__ __forceinline__ uint32_t asm_ld16(u4v d, int voff, int soff) {
     uint32_t v;
-    asm volatile("buffer_load_ushort %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
+    asm volatile("s_nop 4\n\tbuffer_load_ushort %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
     return v;
 }
 
@@ -252,7 +254,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     const u4v ds = sdesc(has_s ? static_cast<const void*>(a.ws16 + n0 * a.ldws) : a.qw,
                          has_s ? ((rows_n - 1) * a.ldws + G) * 2 : 0);
     const int z_off = has_z && b_ok ? static_cast<int>(brow * a.ldwz) : kOob;
-    const int s_off = has_s && b_ok ? static_cast<int>(brow * a.ldws * 2) : kOob;
+    const int s_off = has_s && b_ok ? static_cast<int>(brow * a.ldws * 2) + 4 * bhalf : kOob;
     const int b_st00 = B_LDS + lds_off(brow, 2 * bhalf);
     const int b_st10 = B_LDS + lds_off(brow, 2 * bhalf + 1);
     // scales stored transposed, [wn][column % 16][column tile], so a lane's 8 scales are adjacent
@@ -285,27 +287,36 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     };
     // Two register sets carry packed B groups from their global load to their LDS store.
     u4v rb[2] = {u4v{0u, 0u, 0u, 0u}, u4v{0u, 0u, 0u, 0u}};
-    uint32_t rz[2] = {0u, 0u}, rs[2] = {0u, 0u};
     auto gload_b = [&](int g, int set) {
-        if constexpr (kPacked) {
-            rb[set] = asm_ld128(db, b_off, soff(g, TK / 2));
-            if constexpr (WK == WKind::U4Asym) rz[set] = asm_ld8(dz, z_off, g < G ? g >> 1 : kDead);
-            if constexpr (EPI == Epi::GroupScale) rs[set] = asm_ld16(ds, s_off, soff(g, 2));
-        }
+        if constexpr (kPacked) rb[set] = asm_ld128(db, b_off, soff(g, TK / 2));
+    };
+    // Zero-points and scales of a block of four K groups b4 .. b4 + 3 (b4 % 4 == 0), one load each
+    // per block instead of one per group: zq holds the four zero-point nibbles (group b4 + u in
+    // bits 4u .. 4u + 3), sq the fp16 scales of groups b4 + 2 bhalf and b4 + 2 bhalf + 1. Groups
+    // past the last one read zero or another row's values; their scales are zeroed at the store
+    // and their activations are zero.
+    uint32_t zq = 0u, sq = 0u;
+    auto gload_zs = [&](int b4) {
+        if constexpr (WK == WKind::U4Asym) zq = asm_ld16(dz, z_off, b4 < G ? b4 >> 1 : kDead);
+        if constexpr (EPI == Epi::GroupScale) sq = asm_ld32(ds, s_off, soff(b4, 2));
     };
     // Wait until at most N VMEM operations are outstanding; register set SET counts as written by
     // the wait, so no use of it moves above it.
 #define MQ_WAIT_B(N, SET) \
-    asm volatile("s_waitcnt vmcnt(%3)" : "+v"(rb[SET]), "+v"(rz[SET]), "+v"(rs[SET]) : "n"(N) : "memory")
-    float cs = 0.0f;   // sum_g (-1)^g s[n, g] for this thread's weight row (GroupScale)
+    asm volatile("s_waitcnt vmcnt(%3)" : "+v"(rb[SET]), "+v"(zq), "+v"(sq) : "n"(N) : "memory")
+    // sum_g (-1)^g s[n, g] over the groups whose scale this thread stores (half of them: the two
+    // threads of a weight row add their sums in the epilogue)
+    float cs = 0.0f;
     // LDS stores of register set `set` (a group of parity PAR) into stage ST, in two halves of the
     // unpacked row (spread over two steps) and the scale.
-    auto store_b = [&](int st, int set, auto PARc, int h) {
+    // PARc: parity of the group stored, Uc: its position in its block of four (u = g % 4)
+    auto store_b = [&](int st, int set, auto PARc, auto Uc, int h) {
         if constexpr (kPacked) {
             constexpr bool neg = kGroup && decltype(PARc)::value == 1;
             constexpr bool x16 = AM == 2 && kGroup;
             constexpr bool nw = neg && AM != 2;
-            const uint32_t c = unpack_const<WK, nw>((rz[set] >> (neg ? 4 : 0)) & 0xfu);
+            constexpr int pos = decltype(Uc)::value;
+            const uint32_t c = unpack_const<WK, nw>((zq >> (4 * pos)) & 0xfu);
             uint4 u;
             const uint32_t w0 = h ? rb[set].z : rb[set].x, w1 = h ? rb[set].w : rb[set].y;
             unpack_dword<WK, nw, x16>(w0, c, u.x, u.y);
@@ -313,13 +324,17 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             ds_write16(h ? b_st1 : b_st0, st * TILE_BYTES, u);
         }
     };
-    auto store_s = [&](int st, int set, auto PARc) {
+    // scale of group g (position u in its block) by the thread of its row that loaded it
+    auto store_s = [&](int st, int g, auto PARc, auto Uc) {
         if constexpr (EPI == Epi::GroupScale) {
             constexpr bool neg = decltype(PARc)::value == 1;
-            float sv = f16_bits_to_f32(static_cast<uint16_t>(rs[set])) * kSfac;   // exact: power of two
-            sv = neg ? -sv : sv;
-            ds_write4(s_st, st * TN * 4, sv);
-            cs += sv;
+            constexpr int u = decltype(Uc)::value;
+            if (bhalf == (u >> 1)) {
+                float sv = f16_bits_to_f32(static_cast<uint16_t>(sq >> (16 * (u & 1)))) * kSfac;   // exact
+                sv = g < G ? (neg ? -sv : sv) : 0.0f;
+                ds_write4(s_st, st * TN * 4, sv);
+                cs += sv;
+            }
         }
     };
 
@@ -383,16 +398,17 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // complete once the compiler has waited for B(1)'s registers.
     dma_group(0, 0);
     dma_group(1, 1);
+    gload_zs(0);
     gload_b(0, 0);
     gload_b(1, 1);
     MQ_WAIT_B(0, 0);
     MQ_WAIT_B(0, 1);
-    store_b(0, 0, I0{}, 0);
-    store_b(0, 0, I0{}, 1);
-    store_s(0, 0, I0{});
-    store_b(1, 1, I1{}, 0);
-    store_b(1, 1, I1{}, 1);
-    store_s(1, 1, I1{});
+    store_b(0, 0, I0{}, I0{}, 0);
+    store_b(0, 0, I0{}, I0{}, 1);
+    store_s(0, 0, I0{}, I0{});
+    store_b(1, 1, I1{}, I1{}, 0);
+    store_b(1, 1, I1{}, I1{}, 1);
+    store_s(1, 1, I1{}, I1{});
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // A(0), A(1) of every kind (int8 B has no B loads)
     gload_b(2, 0);
     dma_group(2, 2);
@@ -409,22 +425,33 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     read_s(0, 1);
 
     // VMEM instructions per group and thread, in issue order: the DMA of A(g + 3) (and int8 B) at
-    // step 0, the packed B loads of group g + 4 at step 12. Before the barrier that ends group g,
-    // A(g + 2) (issued at step 0 of group g - 1) must be complete: everything issued after it may
-    // still be in flight.
+    // step 0, the packed B load of group g + 4 at step 12 and, in groups with g % 4 == 1, the
+    // zero-points and scales of the block g + 3 .. g + 6 right after it. Waits count the VMEM
+    // operations issued after the one awaited.
     constexpr int kDmaOps = kPacked ? 2 : 4;
-    constexpr int kBOps = kPacked ? 1 + (WK == WKind::U4Asym) + (EPI == Epi::GroupScale) : 0;
-    // (The partials variant also stores to global memory inside the loop; it waits for everything.)
-    constexpr int kVmAfter = EPI == Epi::GroupPartials ? 0 : 2 * kBOps + kDmaOps;
+    constexpr int kB = kPacked ? 1 : 0;
+    constexpr int kZS = (WK == WKind::U4Asym) + (EPI == Epi::GroupScale);
+    // Before the barrier that ends group g, A(g + 2) (issued at step 0 of group g - 1) must be
+    // complete; issued after it: B(g + 3), [zs if (g - 1) % 4 == 1], A(g + 3), B(g + 4),
+    // [zs if g % 4 == 1]. (The partials variant also stores to global memory; it waits for all.)
+    constexpr int kVmAfter[4] = {
+        EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB, EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB + kZS,
+        EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB + kZS, EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB};
     // At step 8 of group g, register set g % 2 (B(g + 2), loaded at step 12 of group g - 2) must
-    // have arrived; issued after it: A(g + 2) at step 0 of g - 1, B(g + 3), A(g + 3).
-    constexpr int kWaitB = EPI == Epi::GroupPartials ? 0 : 2 * kDmaOps + kBOps;
+    // have arrived, and in groups with g % 4 == 2 the block of zero-points and scales loaded at the
+    // end of group g - 1. Issued after B(g + 2): [zs if g % 4 == 3], A(g + 2), B(g + 3),
+    // [zs if g % 4 == 2], A(g + 3).
+    constexpr int kWaitB[4] = {
+        EPI == Epi::GroupPartials ? 0 : 2 * kDmaOps + kB, EPI == Epi::GroupPartials ? 0 : 2 * kDmaOps + kB,
+        EPI == Epi::GroupPartials ? 0 : (kZS > 0 ? kDmaOps : 2 * kDmaOps + kB),
+        EPI == Epi::GroupPartials ? 0 : 2 * kDmaOps + kB + kZS};
 
     // K group g with A stage, B stage and register set fixed by U = g % 4 (compile-time). Step t = 4 j + i.
     auto group = [&](int g, auto Uc) {
         constexpr int U = decltype(Uc)::value;
         constexpr int ST = U, ST1 = (U + 1) % 4, ST2 = (U + 2) % 4, ST3 = (U + 3) % 4, SET = U % 2;
         using PARc = std::integral_constant<int, U % 2>;
+        using U2c = std::integral_constant<int, (U + 2) % 4>;   // position of group g + 2 in its block
         constexpr int PAR = PARc::value;
 #pragma unroll
         for (int t = 0; t < 32; ++t) {
@@ -458,12 +485,15 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             if (i == 2 && j < 4) read_a(ST1, SET ^ 1, j);
             // unpack register set SET (group g + 2, parity PAR) into stage ST2, then reload it with g + 4
             if (t == 8) {
-                MQ_WAIT_B(kWaitB, SET);
-                store_b(ST2, SET, PARc{}, 0);
+                MQ_WAIT_B(kWaitB[U], SET);
+                store_b(ST2, SET, PARc{}, U2c{}, 0);
             }
-            if (t == 9) store_b(ST2, SET, PARc{}, 1);
-            if (t == 10) store_s(ST2, SET, PARc{});
-            if (t == 12) gload_b(g + 4, SET);
+            if (t == 9) store_b(ST2, SET, PARc{}, U2c{}, 1);
+            if (t == 10) store_s(ST2, g + 2, PARc{}, U2c{});
+            if (t == 12) {
+                gload_b(g + 4, SET);
+                if constexpr (U == 1) gload_zs(g + 3);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
         // A(g + 2) and this group's B stores become visible to every wave. LDS operations of a wave
@@ -471,7 +501,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         // after the stores of steps 8-10, so those stores are complete here without a wait. Group
         // g's own stages were last read by MFMAs that have issued; the next group's fragment reads
         // stay in flight across the barrier.
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kVmAfter) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kVmAfter[U]) : "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
@@ -514,7 +544,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // ---- output epilogue: scale, bias, bf16, staged through LDS for 16-byte row stores
     __syncthreads();   // every wave is done with the pipeline stages the staging area reuses
     if constexpr (EPI == Epi::GroupScale) {
-        if (bhalf == 0) lds<float>(smem, C_LDS + 4 * brow) = cs * kMagic;
+        const float cs_row = cs + __shfl_xor(cs, 1, 64);   // the two threads of the row
+        if (bhalf == 0) lds<float>(smem, C_LDS + 4 * brow) = cs_row * kMagic;
         __syncthreads();
     }
     float colv[8], biasv[8];
