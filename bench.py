@@ -169,6 +169,43 @@ def measure_traffic(args) -> dict:
     return res
 
 
+def measure_stack(steps: int = 3) -> dict:
+    """ms per pass over the config-4 linear stack (every linear: rotate + quantize + GEMM +
+    epilogue, inputs resident, random-init quantized weights); 1 untimed pass, then `steps`."""
+    import torch
+
+    from kitchen_amd import synth
+
+    dev = torch.device("cuda:0")
+    layers = synth.mmdit_linear_stack(blocks=60, device=dev)
+    acts = synth.stack_activations(dev)
+
+    def one_pass():
+        for layer in layers:
+            synth.stack_layer(layer, acts[(layer["M"], layer["K"])])
+
+    one_pass()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        one_pass()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    ops = synth.stack_ops(layers)
+    w4 = sum(l["fmt"] == "w4a4" for l in layers)
+    out = {"workload": "config 4: 60 dual-stream MMDiT blocks x 14 linears (q k v out mlp_up mlp_down mod), "
+                       "image M=4096, text M=256, mod M=1; seeded 35% W4A4 (H64, int4 acts, int4 g64 fp16 "
+                       "weights), rest W8A8 (H256, int8 per-token acts, int8 per-row weights)",
+           "ms_per_step": round(ms, 3), "tops": round(ops / (ms * 1e-3) / 1e12, 1), "ops_per_step": ops,
+           "linears": len(layers), "w4a4_linears": w4, "steps": steps}
+    del layers, acts
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -179,6 +216,7 @@ def main() -> int:
     ap.add_argument("--n", type=int, default=12288)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 traffic counters")
+    ap.add_argument("--no-stack", action="store_true", help="skip the config-4 linear stack")
     ap.add_argument("--kernels-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -229,6 +267,9 @@ def main() -> int:
     rq_gbps = rq_bytes / (ms_rq * 1e-3) / 1e9
     del x3
 
+    # ---- the mixed W4A4 / W8A8 MMDiT linear stack (60 blocks x 14 linears)
+    stack = None if args.no_stack else measure_stack()
+
     traffic = None if args.no_traffic else measure_traffic(args)
     gemm_traffic = traffic.get(GEMM_KERNEL, {}).get("bytes") if traffic else None
     rq_traffic = traffic.get(RQ_KERNEL, {}).get("bytes") if traffic else None
@@ -258,6 +299,8 @@ def main() -> int:
                               "traffic": rq_traffic, "avg_launch_ms": round(ms_rq, 5),
                               "north_star_M_launch_ms": round(ms_rq_ns, 5)},
     }
+    if stack is not None:
+        result["c4_linear_stack"] = stack
     if traffic is not None:
         result["traffic_counters"] = {k2: v for k2, v in traffic.items() if k2 in ("fetch_scale", "write_scale", "error")}
 

@@ -41,3 +41,74 @@ def weight(n: int, k: int, seed: int = 1, std: float = 0.02) -> np.ndarray:
 
 def to_bf16_tensor(bits: np.ndarray, device="cpu") -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(device)
+
+
+# --------------------------------------------------------------------------- config 4: linear stack
+
+MMDIT_HIDDEN = 3072
+MMDIT_LINEARS = (  # (name, K, N) of the 7 linear types of one stream of one dual-stream block
+    ("q", 3072, 3072), ("k", 3072, 3072), ("v", 3072, 3072), ("out", 3072, 3072),
+    ("mlp_up", 3072, 12288), ("mlp_down", 12288, 3072), ("mod", 3072, 18432))
+MMDIT_TOKENS = {"image": 4096, "text": 256}
+
+
+def mmdit_linear_stack(blocks: int = 60, w4a4_frac: float = 0.35, seed: int = 4, device="cuda"):
+    """The linear stack of BASELINE config 4: `blocks` dual-stream MMDiT blocks (hidden 3072,
+    MLP ratio 4), 7 linear types per stream (q, k, v, out, mlp up, mlp down, adaLN modulation at
+    M = 1), image M = 4096 and text M = 256. A seeded Bernoulli draw puts each linear on W4A4
+    (int4 per-token activations after H_64, int4 symmetric group-64 fp16-scale weights) with
+    probability w4a4_frac, the rest on W8A8 (int8 per-row weights, int8 per-token activations
+    after H_256). Weights are random-init directly in the quantized domain (random codes,
+    random positive scales), which is what quantizing random-init weights produces.
+
+    Returns a list of dicts: {"name", "stream", "M", "K", "N", "fmt", "tensors"}."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    pick = torch.rand(blocks * 2 * len(MMDIT_LINEARS), generator=gen) < w4a4_frac
+    dgen = torch.Generator(device=device).manual_seed(seed + 1)
+    layers = []
+    i = 0
+    for b in range(blocks):
+        for stream, m_tok in MMDIT_TOKENS.items():
+            for name, k, n in MMDIT_LINEARS:
+                m = 1 if name == "mod" else m_tok
+                bias = (torch.randn(n, generator=dgen, device=device) * 0.02).to(torch.bfloat16)
+                if bool(pick[i]):
+                    q = torch.randint(-128, 128, (n, k // 2), generator=dgen, device=device, dtype=torch.int8)
+                    s = (torch.rand(n, k // 64, generator=dgen, device=device) * 0.004 + 0.004).to(torch.float16)
+                    tensors = {"qweight": q, "wscales": s, "bias": bias}
+                    fmt = "w4a4"
+                else:
+                    w = torch.randint(-127, 128, (n, k), generator=dgen, device=device, dtype=torch.int8)
+                    s = torch.rand(n, 1, generator=dgen, device=device) * 2e-4 + 3e-4
+                    tensors = {"weight": w, "weight_scale": s, "bias": bias}
+                    fmt = "w8a8"
+                layers.append({"name": f"blocks.{b}.{stream}.{name}", "stream": stream, "M": m, "K": k, "N": n,
+                               "fmt": fmt, "tensors": tensors})
+                i += 1
+    return layers
+
+
+def stack_ops(layers) -> float:
+    """Integer operations of one pass over the stack (2 M N K per linear)."""
+    return float(sum(2 * l["M"] * l["N"] * l["K"] for l in layers))
+
+
+def stack_activations(device="cuda", seed: int = 5) -> dict:
+    """bf16 input buffers of the stack, one per (M, K): resident inputs for every linear."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    out = {}
+    for m in (*MMDIT_TOKENS.values(), 1):
+        for k in (MMDIT_HIDDEN, 4 * MMDIT_HIDDEN):
+            out[(m, k)] = torch.randn(m, k, generator=gen, device=device).to(torch.bfloat16)
+    return out
+
+
+def stack_layer(layer, x):
+    """One linear of the stack through the drop-in ops."""
+    from . import ops
+
+    t = layer["tensors"]
+    if layer["fmt"] == "w4a4":
+        return ops.convrot_w4a4_linear(x, t["qweight"], t["wscales"], t["bias"], convrot_groupsize=64,
+                                       quant_group_size=64, linear_dtype="int4")
+    return ops.int8_linear(x, t["weight"], t["weight_scale"], t["bias"], torch.bfloat16, True, 256)

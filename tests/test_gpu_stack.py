@@ -1,0 +1,46 @@
+"""BASELINE config 4 (the mixed W4A4 / W8A8 MMDiT linear stack): one seeded block of 14 linears
+through the drop-in ops against the oracle (rel-L2 < 4e-3 on sampled rows), and the assignment
+and op count of the full 60-block stack."""
+import numpy as np
+import pytest
+import torch
+
+from kitchen_amd import synth
+from oracle import gemm, linear, quant
+
+pytestmark = pytest.mark.gpu
+
+
+def test_stack_assignment_and_ops(gpu_device):
+    print("[stack] 60-block assignment", flush=True)
+    layers = synth.mmdit_linear_stack(blocks=60, device=gpu_device)
+    assert len(layers) == 60 * 14
+    frac = np.mean([l["fmt"] == "w4a4" for l in layers])
+    assert 0.30 < frac < 0.40
+    assert synth.stack_ops(layers) == pytest.approx(5.9155e13, rel=1e-4)
+    del layers
+    torch.cuda.empty_cache()
+
+
+def test_one_block_against_oracle(gpu_device):
+    layers = synth.mmdit_linear_stack(blocks=1, device=gpu_device)
+    acts = synth.stack_activations(gpu_device)
+    assert {l["fmt"] for l in layers} == {"w4a4", "w8a8"}
+    for layer in layers:
+        m, k, n = layer["M"], layer["K"], layer["N"]
+        print(f"[stack] {layer['name']} {layer['fmt']} M={m} K={k} N={n}", flush=True)
+        x = acts[(m, k)]
+        y = synth.stack_layer(layer, x)
+        torch.cuda.synchronize()
+        rows = np.r_[0:32, m - 32:m] if m > 64 else np.arange(m)
+        xf = x.float().cpu().numpy()[rows]
+        t = {kk: v.cpu() for kk, v in layer["tensors"].items()}
+        bias = t["bias"].float().numpy()
+        if layer["fmt"] == "w4a4":
+            qa, sa = quant.rotquant(xf, 64, 4)
+            p = gemm.partials(qa, quant.unpack_i4(t["qweight"].numpy()), 64)
+            ref = gemm.epilogue_group(p, sa, t["wscales"].numpy().astype(np.float64), bias)
+        else:
+            ref = linear.w8a8_linear(xf, t["weight"].numpy(), t["weight_scale"].numpy(), bias, 256).y
+        err = gemm.rel_l2(ref, y.float().cpu().numpy()[rows])
+        assert err < 4e-3, (layer["name"], err)
