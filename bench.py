@@ -171,7 +171,9 @@ def measure_traffic(args) -> dict:
 
 def measure_stack(steps: int = 3) -> dict:
     """ms per pass over the config-4 linear stack (every linear: rotate + quantize + GEMM +
-    epilogue, inputs resident, random-init quantized weights); 1 untimed pass, then `steps`."""
+    epilogue, inputs resident, random-init quantized weights): eager (one Python call per linear,
+    as a loader runs it) and replayed from one captured HIP graph (the 840 linears' kernels,
+    workspaces and outputs from the graph's memory pool); 1 untimed pass each, then `steps`."""
     import torch
 
     from kitchen_amd import synth
@@ -184,24 +186,38 @@ def measure_stack(steps: int = 3) -> dict:
         for layer in layers:
             synth.stack_layer(layer, acts[(layer["M"], layer["K"])])
 
-    one_pass()
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    ms_eager = timed(one_pass)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        one_pass()                                   # warm the allocator on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
+    with torch.cuda.graph(graph):
         one_pass()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    ms_graph = timed(graph.replay)
     ops = synth.stack_ops(layers)
     w4 = sum(l["fmt"] == "w4a4" for l in layers)
     out = {"workload": "config 4: 60 dual-stream MMDiT blocks x 14 linears (q k v out mlp_up mlp_down mod), "
                        "image M=4096, text M=256, mod M=1; seeded 35% W4A4 (H64, int4 acts, int4 g64 fp16 "
                        "weights), rest W8A8 (H256, int8 per-token acts, int8 per-row weights)",
-           "ms_per_step": round(ms, 3), "tops": round(ops / (ms * 1e-3) / 1e12, 1), "ops_per_step": ops,
-           "linears": len(layers), "w4a4_linears": w4, "steps": steps}
-    del layers, acts
+           "ms_per_step": round(ms_graph, 3), "tops": round(ops / (ms_graph * 1e-3) / 1e12, 1),
+           "ms_per_step_eager": round(ms_eager, 3), "timing": "HIP graph replay of one pass (eager alongside)",
+           "ops_per_step": ops, "linears": len(layers), "w4a4_linears": w4, "steps": steps}
+    del graph, layers, acts
     torch.cuda.empty_cache()
     return out
 

@@ -148,10 +148,10 @@ int mq_decode_w4a8_codebook(const void* qdata, int64_t ldq, const void* s_rel, i
                                        static_cast<hipStream_t>(stream));
 }
 
-int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
-                     const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
-                     const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
-                     void* stream) {
+int mq_gemm_w4_group_ws(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
+                        const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
+                        const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                        void* workspace, int64_t workspace_bytes, void* stream) {
     clear_error();
     MQ_REQUIRE(group == 64, "gemm_w4_group: quant group size must be 64 (got %d)", group);
     MQ_REQUIRE(act_mode >= MQ_ACT_I8 && act_mode <= MQ_ACT_X16ALT, "gemm_w4_group: unknown act_mode %d", act_mode);
@@ -161,11 +161,22 @@ int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8
     MQ_REQUIRE(ldws >= K / group, "gemm_w4_group: ldws < K/group");
     MQ_REQUIRE(!wz || ldwz >= (K / group + 1) / 2, "gemm_w4_group: ldwz < ceil(K/group/2)");
     MQ_REQUIRE(ldy >= N, "gemm_w4_group: ldy < N");
+    MQ_REQUIRE(workspace_bytes >= 0 && (!workspace || aligned(workspace, 16)),
+               "gemm_w4_group: workspace must be 16-byte aligned");
     GemmArgs a{};
     a.qa = qa; a.lda = lda; a.sa = sa; a.qw = qw; a.ldw = ldw; a.ws16 = ws; a.ldws = ldws;
     a.wz = wz; a.ldwz = ldwz; a.bias = bias; a.y = y; a.ldy = ldy; a.M = M; a.N = N; a.K = K;
     a.act_mode = act_mode;
+    a.work = workspace; a.work_bytes = workspace ? workspace_bytes : 0;
     return launch_gemm(a, wz ? WKind::U4Asym : WKind::I4Sym, Epi::GroupScale, static_cast<hipStream_t>(stream));
+}
+
+int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
+                     const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
+                     const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                     void* stream) {
+    return mq_gemm_w4_group_ws(qa, lda, sa, qw, ldw, ws, ldws, wz, ldwz, group, act_mode, bias, y, ldy, M, N, K,
+                               nullptr, 0, stream);
 }
 
 int mq_gemm_w4_group_partials(const int8_t* qa, int64_t lda, const uint8_t* qw, int64_t ldw, const uint8_t* wz,
@@ -185,19 +196,35 @@ int mq_gemm_w4_group_partials(const int8_t* qa, int64_t lda, const uint8_t* qw, 
     return launch_gemm(a, wz ? WKind::U4Asym : WKind::I4Sym, Epi::GroupPartials, static_cast<hipStream_t>(stream));
 }
 
-int mq_gemm_rowscale(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw, int wbits,
-                     const float* ws, const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N,
-                     int64_t K, void* stream) {
+int mq_gemm_rowscale_ws(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw, int wbits,
+                        const float* ws, const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N,
+                        int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
     clear_error();
     MQ_REQUIRE(wbits == 4 || wbits == 8, "gemm_rowscale: wbits must be 4 or 8 (got %d)", wbits);
     int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, wbits == 4 ? K / 2 : K);
     if (rc) return rc;
     MQ_REQUIRE(sa && ws && y, "gemm_rowscale: null pointer");
     MQ_REQUIRE(ldy >= N, "gemm_rowscale: ldy < N");
+    MQ_REQUIRE(workspace_bytes >= 0 && (!workspace || aligned(workspace, 16)),
+               "gemm_rowscale: workspace must be 16-byte aligned");
     GemmArgs a{};
     a.qa = qa; a.lda = lda; a.sa = sa; a.qw = static_cast<const uint8_t*>(qw); a.ldw = ldw; a.ws32 = ws;
     a.bias = bias; a.y = y; a.ldy = ldy; a.M = M; a.N = N; a.K = K;
+    a.work = workspace; a.work_bytes = workspace ? workspace_bytes : 0;
     return launch_gemm(a, wbits == 4 ? WKind::I4Sym : WKind::I8, Epi::RowScale, static_cast<hipStream_t>(stream));
+}
+
+int mq_gemm_rowscale(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw, int wbits,
+                     const float* ws, const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N,
+                     int64_t K, void* stream) {
+    return mq_gemm_rowscale_ws(qa, lda, sa, qw, ldw, wbits, ws, bias, y, ldy, M, N, K, nullptr, 0, stream);
+}
+
+int64_t mq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    int kgroups = 0;
+    const int s = choose_ksplit(M, N, K, INT64_MAX, &kgroups);
+    return s > 1 ? static_cast<int64_t>(s) * M * N * 4 : 0;
 }
 
 int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t ldw, int wbits, int32_t* acc,

@@ -269,7 +269,13 @@ int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     const bool zs_aligned =
         (wk != WKind::U4Asym || (a.ldwz % 2 == 0 && reinterpret_cast<uintptr_t>(a.wz) % 2 == 0)) &&
         (epi != Epi::GroupScale || (a.ldws % 2 == 0 && reinterpret_cast<uintptr_t>(a.ws16) % 4 == 0));
-    if (a.M > 128 && fits32 && zs_aligned && a.act_mode != 1) return launch_gemm_wide(a, wk, epi, stream);
+    if (a.M > 128 && fits32 && zs_aligned && a.act_mode != 1) {
+        GemmArgs w = a;
+        w.ksplit = 1;
+        if (a.work && (epi == Epi::GroupScale || epi == Epi::RowScale))
+            w.ksplit = choose_ksplit(a.M, a.N, a.K, a.work_bytes, &w.kgroups);
+        return launch_gemm_wide(w, wk, epi, stream);
+    }
     switch (wk) {
         case WKind::U4Asym:
             if (epi == Epi::RowScale || epi == Epi::RowAcc) break;

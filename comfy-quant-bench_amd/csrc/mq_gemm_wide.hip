@@ -44,6 +44,7 @@
 // kernel) stores 16 * q negated in odd groups, and signed int4 weights then enter as 16 * v. The
 // MFMA result is 2^gshift times the partial (gshift 4 or 8) and the scales are divided by the same
 // power of two, so every step stays exact.
+#include <algorithm>
 #include <type_traits>
 
 #include "mq_device.h"
@@ -206,8 +207,9 @@ __device__ __forceinline__ T& lds(uint8_t* smem, int off) {
 // One workgroup: a 256 x 256 output tile. AM is the activation layout of the group epilogues
 // (0 int8 codes; 2 int4 codes stored as 16 * q and negated in odd groups, signed int4 weights then
 // entering as 16 * v); row epilogues use 0.
-template <WKind WK, Epi EPI, int AM>
+template <WKind WK, Epi EPI, int AM, bool SPLIT>
 __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, int tiles_n) {
+    static_assert(!SPLIT || EPI == Epi::GroupScale || EPI == Epi::RowScale, "split-K outputs partial results");
     static_assert(AM == 0 || AM == 2, "activation layout 1 is served by the 128-tile kernel");
     constexpr bool kGroup = EPI == Epi::GroupScale || EPI == Epi::GroupPartials;
     constexpr bool kPacked = WK != WKind::I8;
@@ -219,10 +221,17 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     int tm, tn;
-    map_tile(static_cast<int>(blockIdx.x), tiles_m, tiles_n, tm, tn);
+    const int tiles = tiles_m * tiles_n;
+    const int slice = SPLIT ? static_cast<int>(blockIdx.x) / tiles : 0;
+    map_tile(SPLIT ? static_cast<int>(blockIdx.x) % tiles : static_cast<int>(blockIdx.x), tiles_m, tiles_n, tm, tn);
     const int64_t m0 = static_cast<int64_t>(tm) * TM, n0 = static_cast<int64_t>(tn) * TN;
     const int64_t M = a.M, N = a.N;
     const int G = static_cast<int>(a.K / TK);
+    const int G4 = (G + 3) / 4 * 4;   // groups run, live and dead
+    // this workgroup's K groups [g0, g1) (all of them without split-K); g0 % 4 == 0
+    const int g0 = SPLIT ? slice * a.kgroups : 0;
+    const int g1 = SPLIT ? min(g0 + a.kgroups, G4) : G4;
+    const int gend = min(g1, G);      // groups whose products this workgroup accumulates
     const int rows_m = M - m0 < TM ? static_cast<int>(M - m0) : TM;   // valid rows of this tile
     const int rows_n = N - n0 < TN ? static_cast<int>(N - n0) : TN;
     const int kbytes_w = kPacked ? static_cast<int>(a.K / 2) : static_cast<int>(a.K);
@@ -331,7 +340,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             constexpr int u = decltype(Uc)::value;
             if (bhalf == (u >> 1)) {
                 float sv = f16_bits_to_f32(static_cast<uint16_t>(sq >> (16 * (u & 1)))) * kSfac;   // exact
-                sv = g < G ? (neg ? -sv : sv) : 0.0f;
+                sv = g >= g0 && g < gend ? (neg ? -sv : sv) : 0.0f;
                 ds_write4(s_st, st * TN * 4, sv);
                 cs += sv;
             }
@@ -396,23 +405,23 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // register set g % 2 holds (or is loading) B(g + 2), set (g + 1) % 2 B(g + 3).
     // The VMEM issue order leaves B(2), A(2), B(3) in flight, as in the steady state; A(0), A(1) are
     // complete once the compiler has waited for B(1)'s registers.
-    dma_group(0, 0);
-    dma_group(1, 1);
-    gload_zs(0);
-    gload_b(0, 0);
-    gload_b(1, 1);
+    dma_group(g0, 0);
+    dma_group(g0 + 1, 1);
+    gload_zs(g0);
+    gload_b(g0, 0);
+    gload_b(g0 + 1, 1);
     MQ_WAIT_B(0, 0);
     MQ_WAIT_B(0, 1);
     store_b(0, 0, I0{}, I0{}, 0);
     store_b(0, 0, I0{}, I0{}, 1);
-    store_s(0, 0, I0{}, I0{});
+    store_s(0, g0, I0{}, I0{});
     store_b(1, 1, I1{}, I1{}, 0);
     store_b(1, 1, I1{}, I1{}, 1);
-    store_s(1, 1, I1{}, I1{});
+    store_s(1, g0 + 1, I1{}, I1{});
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // A(0), A(1) of every kind (int8 B has no B loads)
-    gload_b(2, 0);
-    dma_group(2, 2);
-    gload_b(3, 1);
+    gload_b(g0 + 2, 0);
+    dma_group(g0 + 2, 2);
+    gload_b(g0 + 3, 1);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -506,8 +515,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
     };
-    const int G4 = (G + 3) / 4 * 4;   // groups run, live and dead
-    for (int g = 0; g < G4; g += 4) {
+    for (int g = g0; g < g1; g += 4) {
         group(g, std::integral_constant<int, 0>{});
         group(g + 1, std::integral_constant<int, 1>{});
         group(g + 2, std::integral_constant<int, 2>{});
@@ -520,7 +528,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         const int tp = 32 - LAG + t;
         if constexpr (EPI == Epi::GroupScale) fma_tile(tp);
         if constexpr (EPI == Epi::GroupPartials)
-            if (G4 - 1 < G) write_partials(tp, G4 - 1, true);
+            if (g1 - 1 < G) write_partials(tp, g1 - 1, true);
     }
 
     if constexpr (EPI == Epi::GroupPartials) return;
@@ -547,6 +555,30 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         const float cs_row = cs + __shfl_xor(cs, 1, 64);   // the two threads of the row
         if (bhalf == 0) lds<float>(smem, C_LDS + 4 * brow) = cs_row * kMagic;
         __syncthreads();
+    }
+    if constexpr (SPLIT) {
+        // partial outputs of this K slice: fp32 sum_g s P (offset removed) or the int32 sum
+        const int64_t slice_off = static_cast<int64_t>(slice) * M * N;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int lc = wn * 128 + j * 16 + fr;
+            const int64_t col = n0 + lc;
+            if (col >= N) continue;
+            float cv = 0.0f;
+            if constexpr (EPI == Epi::GroupScale) cv = lds<float>(smem, C_LDS + 4 * lc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
+                    if (row >= M) continue;
+                    if constexpr (EPI == Epi::GroupScale)
+                        static_cast<float*>(a.work)[slice_off + row * N + col] = acc[i][j][r] - cv;
+                    else
+                        static_cast<int32_t*>(a.work)[slice_off + row * N + col] = acci[i][j][r];
+                }
+        }
+        return;
     }
     float colv[8], biasv[8];
 #pragma unroll
@@ -611,11 +643,80 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     }
 }
 
+// y[m, n] = bf16(sum_s part[s][m][n] * sa[m] + bias[n]) (GroupScale: fp32 partials) or
+// bf16(float(sum_s part[s][m][n]) * sa[m] * ws[n] + bias[n]) (RowScale: int32 partials, the
+// non-split epilogue's arithmetic on the exact full-K sum). 8 consecutive columns per thread.
+template <bool INT>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a) {
+    const int64_t M = a.M, N = a.N;
+    const int64_t cols8 = (N + 7) / 8;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= M * cols8) return;
+    const int64_t row = idx / cols8, col0 = (idx % cols8) * 8;
+    const bool full = col0 + 8 <= N && N % 4 == 0;   // two aligned 16-byte loads per slice
+    float t[8];
+    if constexpr (INT) {
+        int32_t sum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int s = 0; s < a.ksplit; ++s) {
+            const int32_t* p = static_cast<const int32_t*>(a.work) + (s * M + row) * N + col0;
+            if (full) {
+                const int4 u = *reinterpret_cast<const int4*>(p), v = *reinterpret_cast<const int4*>(p + 4);
+                sum[0] += u.x; sum[1] += u.y; sum[2] += u.z; sum[3] += u.w;
+                sum[4] += v.x; sum[5] += v.y; sum[6] += v.z; sum[7] += v.w;
+            } else {
+                for (int e = 0; e < 8 && col0 + e < N; ++e) sum[e] += p[e];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t[e] = static_cast<float>(sum[e]) * a.sa[row] * (col0 + e < N ? a.ws32[col0 + e] : 0.0f);
+    } else {
+        float sum[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s = 0; s < a.ksplit; ++s) {
+            const float* p = static_cast<const float*>(a.work) + (s * M + row) * N + col0;
+            if (full) {
+                const float4 u = *reinterpret_cast<const float4*>(p), v = *reinterpret_cast<const float4*>(p + 4);
+                sum[0] += u.x; sum[1] += u.y; sum[2] += u.z; sum[3] += u.w;
+                sum[4] += v.x; sum[5] += v.y; sum[6] += v.z; sum[7] += v.w;
+            } else {
+                for (int e = 0; e < 8 && col0 + e < N; ++e) sum[e] += p[e];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t[e] = sum[e] * a.sa[row];
+    }
+    uint32_t out[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        if (col0 + e >= N) break;
+        float v = t[e];
+        if (a.bias) v += __uint_as_float(static_cast<uint32_t>(a.bias[col0 + e]) << 16);
+        out[e >> 1] |= f32_to_bf16_bits(v) << (16 * (e & 1));
+    }
+    uint16_t* dst = a.y + row * a.ldy + col0;
+    if (col0 + 8 <= N && a.ldy % 8 == 0) {
+        *reinterpret_cast<uint4*>(dst) = uint4{out[0], out[1], out[2], out[3]};
+    } else {
+        for (int e = 0; e < 8 && col0 + e < N; ++e) dst[e] = static_cast<uint16_t>(out[e >> 1] >> (16 * (e & 1)));
+    }
+}
+
 template <WKind WK, Epi EPI, int AM>
 int launch_one(const GemmArgs& a, hipStream_t stream) {
     const int tiles_m = static_cast<int>((a.M + TM - 1) / TM);
     const int tiles_n = static_cast<int>((a.N + TN - 1) / TN);
-    hipLaunchKernelGGL((gemm_wide_kernel<WK, EPI, AM>), dim3(static_cast<unsigned>(tiles_m * tiles_n)), dim3(NT), 0,
+    if constexpr (EPI == Epi::GroupScale || EPI == Epi::RowScale) {
+        if (a.ksplit > 1) {
+            hipLaunchKernelGGL((gemm_wide_kernel<WK, EPI, AM, true>), dim3(static_cast<unsigned>(tiles_m * tiles_n * a.ksplit)),
+                               dim3(NT), 0, stream, a, tiles_m, tiles_n);
+            const int rc = launch_status("gemm_wide");
+            if (rc) return rc;
+            const int64_t threads = a.M * ((a.N + 7) / 8);
+            hipLaunchKernelGGL(splitk_reduce_kernel<EPI == Epi::RowScale>, dim3(static_cast<unsigned>((threads + 255) / 256)),
+                               dim3(256), 0, stream, a);
+            return launch_status("gemm_splitk_reduce");
+        }
+    }
+    hipLaunchKernelGGL((gemm_wide_kernel<WK, EPI, AM, false>), dim3(static_cast<unsigned>(tiles_m * tiles_n)), dim3(NT), 0,
                        stream, a, tiles_m, tiles_n);
     return launch_status("gemm_wide");
 }
@@ -646,6 +747,25 @@ int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
 }
 
 }  // namespace
+
+int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups) {
+    *kgroups = 0;
+    if (M <= 128 || K % TK) return 1;                           // the 128-tile kernel has no split
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return 1;
+    const int64_t tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+    const int64_t blocks = (K / TK + 3) / 4;                    // blocks of four K groups
+    if (2 * tiles > cus || blocks < 4) return 1;
+    // at least two blocks per slice; as many slices as keep every compute unit busy
+    int64_t s = std::min<int64_t>(cus / tiles, blocks / 2);
+    const int64_t per = (blocks + s - 1) / s;                   // blocks per slice
+    s = (blocks + per - 1) / per;
+    if (s < 2 || s * M * N * 4 > work_bytes) return 1;
+    *kgroups = static_cast<int>(per * 4);
+    return static_cast<int>(s);
+}
 
 int launch_gemm_wide(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     switch (wk) {

@@ -50,7 +50,18 @@ struct GemmArgs {
     int32_t* part;          // int32 partials / accumulators
     int64_t M, N, K;
     int act_mode;           // group-scale GEMMs: MQ_ACT_* layout of qa (include/mq.h)
+    // split-K (wide kernel, GroupScale / RowScale only): ksplit slices of kgroups K groups each
+    // (a multiple of 4) write fp32 (GroupScale) or int32 (RowScale) partial outputs [ksplit][M][N]
+    // to work, which a reduction kernel sums and finishes; ksplit 1 = no split
+    int ksplit = 1;
+    int kgroups = 0;
+    void* work = nullptr;
+    int64_t work_bytes = 0;   // capacity of work offered by the caller
 };
+
+// K slices for a GEMM of this shape with a workspace of work_bytes (1 = no split): used when the
+// 256 x 256 tiles leave most compute units idle (small M).
+int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups);
 
 // Power-of-two factor by which a group GEMM's MFMA result exceeds the true partial, per
 // activation layout and weight kind (see mq_gemm_wide.hip).

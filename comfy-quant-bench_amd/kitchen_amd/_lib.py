@@ -11,7 +11,7 @@ import os
 
 import torch  # noqa: F401  (must be imported before the library is loaded)
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmq.so")
 
@@ -30,10 +30,15 @@ _SIGNATURES = {
                                 c_int),
     "mq_gemm_w4_group": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_vp,
                           c_i64, c_i64, c_i64, c_i64, c_vp], c_int),
+    "mq_gemm_w4_group_ws": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_vp,
+                             c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp], c_int),
+    "mq_gemm_workspace_bytes": ([c_i64, c_i64, c_i64], c_i64),
     "mq_gemm_w4_group_partials": ([c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_i64, c_i64, c_i64,
                                    c_vp], c_int),
     "mq_gemm_rowscale": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp],
                          c_int),
+    "mq_gemm_rowscale_ws": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64,
+                             c_vp, c_i64, c_vp], c_int),
     "mq_gemm_rowscale_acc": ([c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_vp], c_int),
 }
 

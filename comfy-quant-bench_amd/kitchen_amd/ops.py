@@ -160,19 +160,27 @@ def _check_w4_group(qa, qweight, wscales, wzeros, n, group_size):
         raise ValueError(f"zero-points must be packed uint4 [{n}, {(groups + 1) // 2}]")
 
 
+def _workspace(m: int, n: int, k: int, device):
+    """Split-K workspace for an M x N x K product when the library wants one (small M), else None."""
+    nbytes = _lib.load().mq_gemm_workspace_bytes(m, n, k)
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes > 0 else None
+
+
 def gemm_w4_group(qa, sa, qweight, wscales, wzeros, bias, n: int, group_size: int = INT4_GROUP_SIZE,
                   act_mode: int = _lib.ACT_I8):
     """y bf16 [M, N] = sa * sum_g wscales[:, g] * P_g + bias with P_g exact int32 group partials.
 
     act_mode: ACT_I8 int8 codes, ACT_I4 int4 codes one per byte, ACT_X16ALT the layout written by
-    rotate_quantize(..., packed=Q_X16ALT)."""
+    rotate_quantize(..., packed=Q_X16ALT). Small M splits K over a torch-allocated workspace."""
     m, k = qa.shape
     _check_w4_group(qa, qweight, wscales, wzeros, n, group_size)
     y = torch.empty((m, n), dtype=torch.bfloat16, device=qa.device)
     ldwz = wzeros.stride(0) if wzeros is not None else 0
-    _lib.call("mq_gemm_w4_group", qa.data_ptr(), qa.stride(0), sa.data_ptr(), qweight.data_ptr(),
+    work = _workspace(m, n, k, qa.device)
+    _lib.call("mq_gemm_w4_group_ws", qa.data_ptr(), qa.stride(0), sa.data_ptr(), qweight.data_ptr(),
               qweight.stride(0), wscales.data_ptr(), wscales.stride(0), _lib.ptr(wzeros), ldwz, int(group_size),
-              int(act_mode), _lib.ptr(bias), y.data_ptr(), y.stride(0), m, n, k, _lib.stream_of(qa))
+              int(act_mode), _lib.ptr(bias), y.data_ptr(), y.stride(0), m, n, k, _lib.ptr(work),
+              0 if work is None else work.numel(), _lib.stream_of(qa))
     return y
 
 
@@ -190,12 +198,14 @@ def gemm_w4_group_partials(qa, qweight, wzeros, n: int, group_size: int = INT4_G
 
 
 def gemm_rowscale(qa, sa, qweight, wscales, bias, n: int, wbits: int):
-    """y bf16 [M, N] = (qa . w^T) * sa[m] * wscales[n] + bias, full-K int32 accumulator."""
+    """y bf16 [M, N] = (qa . w^T) * sa[m] * wscales[n] + bias, full-K int32 accumulator (split over
+    K into int32 partial sums for small M, summed exactly)."""
     m, k = qa.shape
     y = torch.empty((m, n), dtype=torch.bfloat16, device=qa.device)
-    _lib.call("mq_gemm_rowscale", qa.data_ptr(), qa.stride(0), sa.data_ptr(), qweight.data_ptr(),
+    work = _workspace(m, n, k, qa.device)
+    _lib.call("mq_gemm_rowscale_ws", qa.data_ptr(), qa.stride(0), sa.data_ptr(), qweight.data_ptr(),
               qweight.stride(0), int(wbits), wscales.data_ptr(), _lib.ptr(bias), y.data_ptr(), y.stride(0),
-              m, n, k, _lib.stream_of(qa))
+              m, n, k, _lib.ptr(work), 0 if work is None else work.numel(), _lib.stream_of(qa))
     return y
 
 

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MQ_ABI_VERSION 4
+#define MQ_ABI_VERSION 5
 
 enum {
     MQ_OK = 0,
@@ -146,6 +146,25 @@ int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8
                      void* stream);
 
 /*
+ * mq_gemm_w4_group with a caller-provided workspace. When the 256 x 256 output tiles would leave
+ * most compute units idle (small M: the text-token linears, the adaLN-sized outputs) the K groups
+ * are split into slices, each slice's workgroups write fp32 partial outputs [slices][M][N] into
+ * the workspace, and a reduction kernel sums them in slice order (deterministic) and applies
+ * sa, bias and the bf16 rounding. mq_gemm_workspace_bytes(M, N, K) gives the size that enables
+ * the split on the current device (0: no split for this shape); a smaller or NULL workspace
+ * runs without it. No reference counterpart: comfy-kitchen's GEMMs allocate internally.
+ *   workspace  device memory, 16-byte aligned, workspace_bytes long (or NULL)
+ */
+int mq_gemm_w4_group_ws(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
+                        const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
+                        const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes mq_gemm_w4_group_ws / mq_gemm_rowscale_ws use for an M x N x K product on the
+ * current device (0 when the shape fills the device without splitting K). */
+int64_t mq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/*
  * Debug / parity entry: the exact per-group int32 partials P[g,m,n] of mq_gemm_w4_group
  * (same tile loaders, unpack and MFMA code), written to part int32 [K/group, M, N] (dense).
  * P is the partial of the codes themselves: the x16 / sign of layout MQ_ACT_X16ALT is undone.
@@ -170,6 +189,12 @@ int mq_gemm_w4_group_partials(const int8_t* qa, int64_t lda, const uint8_t* qw, 
 int mq_gemm_rowscale(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw,
                      int wbits, const float* ws, const uint16_t* bias, uint16_t* y, int64_t ldy,
                      int64_t M, int64_t N, int64_t K, void* stream);
+
+/* mq_gemm_rowscale with a caller-provided workspace (int32 partial sums per K slice, summed
+ * exactly before the epilogue: the same result as without the split). */
+int mq_gemm_rowscale_ws(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw, int wbits,
+                        const float* ws, const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N,
+                        int64_t K, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Debug / parity entry: the full-K int32 accumulator of mq_gemm_rowscale, acc int32 [M, N]. */
 int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t ldw, int wbits,

@@ -44,3 +44,29 @@ def test_one_block_against_oracle(gpu_device):
             ref = linear.w8a8_linear(xf, t["weight"].numpy(), t["weight_scale"].numpy(), bias, 256).y
         err = gemm.rel_l2(ref, y.float().cpu().numpy()[rows])
         assert err < 4e-3, (layer["name"], err)
+
+
+def test_graph_replay_matches_eager(gpu_device):
+    # one block captured in a HIP graph, replayed several times with eager work and syncs in
+    # between; every replay's outputs equal the eager outputs bit for bit
+    print("[stack] graph capture of one block", flush=True)
+    layers = synth.mmdit_linear_stack(blocks=1, device=gpu_device)
+    acts = synth.stack_activations(gpu_device)
+    eager = [synth.stack_layer(l, acts[(l["M"], l["K"])]).clone() for l in layers]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for l in layers:
+            synth.stack_layer(l, acts[(l["M"], l["K"])])
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [synth.stack_layer(l, acts[(l["M"], l["K"])]) for l in layers]
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for l, y, ref in zip(layers, outs, eager):
+            assert torch.equal(y, ref), (rep, l["name"])
+        synth.stack_layer(layers[0], acts[(layers[0]["M"], layers[0]["K"])])   # eager work between replays
+        torch.cuda.synchronize()
