@@ -259,6 +259,9 @@ int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
 
 int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     if (a.M == 0 || a.N == 0) return 0;
+    // a few rows: HBM-bound, served by the dot4 kernel (activation rows staged in LDS)
+    if (a.M <= 4 && a.M * a.K <= 131072 && (epi == Epi::GroupScale || epi == Epi::RowScale))
+        return launch_gemv(a, wk, epi, stream);
     // The 256 x 256-tile kernel addresses each operand with 32-bit buffer offsets.
     const int64_t wbytes = wk == WKind::I8 ? a.K : a.K / 2;
     const bool fits32 = a.M * a.lda < (int64_t(1) << 31) && a.N * a.ldw < (int64_t(1) << 31) &&

@@ -73,6 +73,9 @@ __host__ __device__ inline int group_shift(int act_mode, WKind wk) {
 
 int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream);
 
+// M <= 4 rows, GroupScale / RowScale only (mq_gemv.hip).
+int launch_gemv(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream);
+
 // 256 x 256-tile kernel for large M (mq_gemm_wide.hip).
 int launch_gemm_wide(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream);
 
