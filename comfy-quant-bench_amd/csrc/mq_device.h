@@ -39,6 +39,10 @@ __device__ __forceinline__ float dpp_upd(float old, float src) {
 }
 
 // DPP controls (GFX9 encoding).
+constexpr int kQuadXor1 = 0xB1;       // quad_perm [1, 0, 3, 2]: lane ^ 1
+constexpr int kQuadXor2 = 0x4E;       // quad_perm [2, 3, 0, 1]: lane ^ 2
+constexpr int kRowRor4 = 0x124;       // rotate right by 4 within a row of 16
+constexpr int kRowRor8 = 0x128;
 constexpr int kQuadPerm0022 = 0xA0;   // lane <- lane & ~1 within the quad
 constexpr int kQuadPerm1133 = 0xF5;   // lane <- lane | 1
 constexpr int kQuadPerm0101 = 0x44;   // lane <- lane & ~2
@@ -47,5 +51,20 @@ constexpr int kRowShl4 = 0x104;       // lane <- lane + 4 (within a row of 16)
 constexpr int kRowShl8 = 0x108;
 constexpr int kRowShr4 = 0x114;       // lane <- lane - 4
 constexpr int kRowShr8 = 0x118;
+
+// Maximum over the 64 lanes of a wavefront, returned in every lane: four DPP steps give each
+// 16-lane row its maximum, then the four row maxima are read as scalars (no LDS round trip).
+__device__ __forceinline__ float wave_max(float v) {
+    v = __builtin_fmaxf(v, dpp_mov<kQuadXor1>(v));
+    v = __builtin_fmaxf(v, dpp_mov<kQuadXor2>(v));
+    v = __builtin_fmaxf(v, dpp_mov<kRowRor4>(v));
+    v = __builtin_fmaxf(v, dpp_mov<kRowRor8>(v));
+    const int b = __float_as_int(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+    return __builtin_fmaxf(__builtin_fmaxf(r0, r1), __builtin_fmaxf(r2, r3));
+}
 
 }  // namespace mq

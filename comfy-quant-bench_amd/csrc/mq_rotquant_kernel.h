@@ -250,8 +250,7 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
 #pragma unroll
             for (int j = 0; j < 16; ++j) am = __builtin_fmaxf(am, __builtin_fabsf(v[c][j]));
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) am = __builtin_fmaxf(am, __shfl_xor(am, o, 64));
+        am = wave_max(am);
         if constexpr (W > 1) {
             if (lane == 0) red[parity * kWaves + wave] = am;
             __syncthreads();
