@@ -74,6 +74,10 @@ __device__ __forceinline__ void swiglu_pair(uint32_t wg, uint32_t wu, const floa
 }
 
 // Radix-4 butterflies over register bits J, J+1 (element stride 4^d mapped to register stride 2^J).
+// y_i = fma(t, 0.5, -x_{3-i}) with t = ((x0 + x1) + x2) + x3 is the reference's h - x_{3-i},
+// h = 0.5f * t: halving is exact, so the fma rounds the same real number once. (For a subnormal t
+// the product is exact where 0.5f * t may round; such values quantize to code 0 under any scale
+// the quantizer can choose, s >= 1e-10, so codes and scales are unchanged.)
 template <int J>
 __device__ __forceinline__ void stage_reg(float (&v)[16]) {
     constexpr int st = 1 << J;
@@ -81,11 +85,11 @@ __device__ __forceinline__ void stage_reg(float (&v)[16]) {
     for (int r = 0; r < 16; ++r) {
         if ((r >> J) & 3) continue;
         const float x0 = v[r], x1 = v[r + st], x2 = v[r + 2 * st], x3 = v[r + 3 * st];
-        const float h = 0.5f * (((x0 + x1) + x2) + x3);
-        v[r] = h - x3;
-        v[r + st] = h - x2;
-        v[r + 2 * st] = h - x1;
-        v[r + 3 * st] = h - x0;
+        const float t = ((x0 + x1) + x2) + x3;
+        v[r] = __builtin_fmaf(t, 0.5f, -x3);
+        v[r + st] = __builtin_fmaf(t, 0.5f, -x2);
+        v[r + 2 * st] = __builtin_fmaf(t, 0.5f, -x1);
+        v[r + 3 * st] = __builtin_fmaf(t, 0.5f, -x0);
     }
 }
 
@@ -214,32 +218,35 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
         if constexpr (W == 1) {
             if (!live) break;
         }
-        const uint16_t* xr = x + row * ldx;
+        // Lanes past the end of the row (a last chunk that K does not fill) and the waves of a
+        // row past M (W > 1: they still take part in the barrier) load in-bounds data from the
+        // row's start or from row M - 1 instead, and their values are left out of the absmax; their
+        // codes are not stored. A Hadamard block lies wholly inside or outside the row (K is a
+        // multiple of the block), so the rotation never mixes such values into stored ones.
+        const uint16_t* xr = x + (live ? row : static_cast<int64_t>(M) - 1) * ldx;
 
         float v[NCH][16];
+        bool in[NCH];
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
-            const int e = (c * W + wr) * 1024 + seg_ld * 16;
-            if (live && e < K) {
-                const uint4 a = *reinterpret_cast<const uint4*>(xr + e);
-                const uint4 b = *reinterpret_cast<const uint4*>(xr + e + 8);
-                const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-                if constexpr (ACT == 1) {
-                    const uint4 ua = *reinterpret_cast<const uint4*>(xr + K + e);
-                    const uint4 ub = *reinterpret_cast<const uint4*>(xr + K + e + 8);
-                    const uint32_t wu[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
+            const int e0 = (c * W + wr) * 1024 + seg_ld * 16;
+            in[c] = e0 < K;
+            const int e = in[c] ? e0 : 0;
+            const uint4 a = *reinterpret_cast<const uint4*>(xr + e);
+            const uint4 b = *reinterpret_cast<const uint4*>(xr + e + 8);
+            const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            if constexpr (ACT == 1) {
+                const uint4 ua = *reinterpret_cast<const uint4*>(xr + K + e);
+                const uint4 ub = *reinterpret_cast<const uint4*>(xr + K + e + 8);
+                const uint32_t wu[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) swiglu_pair(w[j], wu[j], tab, v[c][2 * j], v[c][2 * j + 1]);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        v[c][2 * j] = bf16lo(w[j]);
-                        v[c][2 * j + 1] = bf16hi(w[j]);
-                    }
-                }
+                for (int j = 0; j < 8; ++j) swiglu_pair(w[j], wu[j], tab, v[c][2 * j], v[c][2 * j + 1]);
             } else {
 #pragma unroll
-                for (int j = 0; j < 16; ++j) v[c][j] = 0.0f;
+                for (int j = 0; j < 8; ++j) {
+                    v[c][2 * j] = bf16lo(w[j]);
+                    v[c][2 * j + 1] = bf16hi(w[j]);
+                }
             }
         }
 
@@ -247,8 +254,10 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             rotate_chunk<BLK>(v[c], lane);
+            float amc = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) am = __builtin_fmaxf(am, __builtin_fabsf(v[c][j]));
+            for (int j = 0; j < 16; ++j) amc = __builtin_fmaxf(amc, __builtin_fabsf(v[c][j]));
+            am = __builtin_fmaxf(am, live && in[c] ? amc : 0.0f);
         }
         am = wave_max(am);
         if constexpr (W > 1) {

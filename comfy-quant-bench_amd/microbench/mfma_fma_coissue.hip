@@ -14,9 +14,13 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 template <int LAG, int PIN>
 __global__ void __launch_bounds__(512) k(int iters, float* outf) {
     const uint32_t lane = threadIdx.x + blockIdx.x * 512u;
-    v4i a[4], b[4];
+    // 4 A and 8 B operands: the 32 MFMAs of a step sequence are all distinct (with fewer operand
+    // combinations the compiler merges identical MFMAs)
+    v4i a[4], b[8];
     for (int i = 0; i < 4; ++i)
-        for (int r = 0; r < 4; ++r) { a[i][r] = (int)((lane * 0x9E3779B1u + i * 3 + r) * 2654435761u) & (int)MASK; b[i][r] = (int)((lane * 0x85EBCA77u + i + r * 11) * 2246822519u) & (int)MASK; }
+        for (int r = 0; r < 4; ++r) a[i][r] = (int)((lane * 0x9E3779B1u + i * 3 + r) * 2654435761u) & (int)MASK;
+    for (int i = 0; i < 8; ++i)
+        for (int r = 0; r < 4; ++r) b[i][r] = (int)((lane * 0x85EBCA77u + i + r * 11) * 2246822519u) & (int)MASK;
     v4i c = {0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000};
     v4i d[8];
     float acc[32][4];
@@ -27,7 +31,7 @@ __global__ void __launch_bounds__(512) k(int iters, float* outf) {
 #pragma unroll
         for (int t = 0; t < 32; ++t) {
             if constexpr (PIN & 1) asm volatile("" : "+v"(c));
-            d[t & 7] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t & 3], b[(t >> 2) & 3], c, 0, 0, 0);
+            d[t & 7] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t & 3], b[t >> 2], c, 0, 0, 0);
             if constexpr (PIN & 2) __builtin_amdgcn_sched_barrier(0);
             const int tp = (t + 32 - LAG) & 31;
 #pragma unroll
