@@ -119,6 +119,9 @@ def kernels_child(args) -> int:
 
 
 def _counter_means(csv_path: str, counter: str) -> dict:
+    """Per kernel, the counter's mean over the dispatches of the largest grid: the measured shape
+    (the child also quantizes the M=4096 GEMM input, a smaller rotquant grid); for the copy kernel
+    the maximum (the calibration copies are identical, other copies are smaller)."""
     sums: dict = {}
     for row in csv.DictReader(open(csv_path)):
         if row.get("Counter_Name") != counter:
@@ -126,9 +129,16 @@ def _counter_means(csv_path: str, counter: str) -> dict:
         name = row["Kernel_Name"]
         for key in (GEMM_KERNEL, RQ_KERNEL, COPY_KERNEL):
             if key in name:
-                sums.setdefault(key, []).append(float(row["Counter_Value"]))
-    # the calibration copies are identical; other copy-kernel dispatches (smaller) are ignored
-    return {key: (max(v) if key == COPY_KERNEL else sum(v) / len(v)) for key, v in sums.items()}
+                sums.setdefault(key, []).append((int(row.get("Grid_Size") or 0), float(row["Counter_Value"])))
+    out = {}
+    for key, v in sums.items():
+        if key == COPY_KERNEL:
+            out[key] = max(val for _, val in v)
+        else:
+            grid = max(g for g, _ in v)
+            vals = [val for g, val in v if g == grid]
+            out[key] = sum(vals) / len(vals)
+    return out
 
 
 def measure_traffic(args) -> dict:

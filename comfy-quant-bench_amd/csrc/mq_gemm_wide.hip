@@ -608,7 +608,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
                 for (int e = 0; e < 2; ++e) {
                     float t;
                     if constexpr (EPI == Epi::GroupScale)
-                        t = (acc[i][j][r + e] - colv[j]) * sav[r + e] + biasv[j];
+                        t = __builtin_fmaf(acc[i][j][r + e] - colv[j], sav[r + e], biasv[j]);
                     else
                         t = static_cast<float>(acci[i][j][r + e]) * sav[r + e] * colv[j] + biasv[j];
                     v[e] = t;
