@@ -148,6 +148,42 @@ int mq_decode_w4a8_codebook(const void* qdata, int64_t ldq, const void* s_rel, i
                                        static_cast<hipStream_t>(stream));
 }
 
+int mq_quantize_weight(const void* w, int dtype, int64_t N, int64_t K, int64_t ldw, int hblock, int format,
+                       void* q, int64_t ldq, void* scale, int64_t ld_scale, void* zero, int64_t ld_zero,
+                       void* stream) {
+    clear_error();
+    MQ_REQUIRE(dtype >= MQ_DT_BF16 && dtype <= MQ_DT_F32, "quantize_weight: unknown dtype %d", dtype);
+    MQ_REQUIRE(format >= MQ_WFMT_U4_ASYM_G64 && format <= MQ_WFMT_I8_ROW, "quantize_weight: unknown format %d", format);
+    MQ_REQUIRE(N >= 0 && K > 0, "quantize_weight: bad shape N=%lld K=%lld", (long long)N, (long long)K);
+    MQ_REQUIRE(N < (int64_t(1) << 31), "quantize_weight: N too large");
+    MQ_REQUIRE(K <= 32768, "quantize_weight: K=%lld exceeds 32768", (long long)K);
+    const bool group = format == MQ_WFMT_U4_ASYM_G64 || format == MQ_WFMT_I4_SYM_G64;
+    MQ_REQUIRE(group ? K % 64 == 0 : K % 16 == 0, "quantize_weight: K=%lld must be a multiple of %d", (long long)K,
+               group ? 64 : 16);
+    MQ_REQUIRE(hblock == 0 || hblock == 16 || hblock == 64 || hblock == 256,
+               "quantize_weight: convrot group size must be 0, 16, 64 or 256 (got %d)", hblock);
+    MQ_REQUIRE(hblock == 0 || K % hblock == 0, "quantize_weight: K=%lld is not a multiple of the group size %d",
+               (long long)K, hblock);
+    if (N == 0) return MQ_OK;
+    const int64_t esz = dtype == MQ_DT_F32 ? 4 : 2;
+    MQ_REQUIRE(w && q && scale, "quantize_weight: null pointer");
+    MQ_REQUIRE(ldw >= K && aligned(w, esz), "quantize_weight: w needs ldw >= K and an element-aligned base");
+    const bool i8 = format == MQ_WFMT_I8_ROW;
+    const int64_t qalign = i8 ? 8 : 4;
+    MQ_REQUIRE(ldq >= (i8 ? K : K / 2) && ldq % qalign == 0 && aligned(q, qalign),
+               "quantize_weight: q needs ldq >= %lld bytes, ldq %% %lld == 0 and an aligned base",
+               (long long)(i8 ? K : K / 2), (long long)qalign);
+    if (group) {
+        MQ_REQUIRE(ld_scale >= K / 64 && aligned(scale, 2), "quantize_weight: scale needs ld_scale >= K/64 (fp16)");
+    } else {
+        MQ_REQUIRE(aligned(scale, 4), "quantize_weight: scale must be 4-byte aligned (fp32 [N])");
+    }
+    if (format == MQ_WFMT_U4_ASYM_G64)
+        MQ_REQUIRE(zero && ld_zero >= (K / 64 + 1) / 2, "quantize_weight: zero needs ld_zero >= ceil(K/128)");
+    return launch_quantize_weight(w, dtype, N, K, ldw, hblock, format, q, ldq, scale, ld_scale, zero, ld_zero,
+                                  static_cast<hipStream_t>(stream));
+}
+
 int mq_gemm_w4_group_ws(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
                         const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
                         const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,

@@ -29,6 +29,11 @@ int launch_decode_w4a8_codebook(const uint8_t* qdata, int64_t ldq, const uint8_t
                                 const float* s_channel, const float* codebook, int group_size, int64_t N,
                                 int64_t K, int8_t* q8, int64_t ldq8, float* row_scale, hipStream_t stream);
 
+// --- offline weight quantizer (mq_wquant.hip); dtype / format are MQ_DT_* / MQ_WFMT_*
+int launch_quantize_weight(const void* w, int dtype, int64_t N, int64_t K, int64_t ldw, int hblock, int format,
+                           void* q, int64_t ldq, void* scale, int64_t ld_scale, void* zero, int64_t ld_zero,
+                           hipStream_t stream);
+
 // --- GEMMs (mq_gemm.hip)
 enum class WKind : int { U4Asym = 0, I4Sym = 1, I8 = 2 };
 enum class Epi : int { GroupScale = 0, GroupPartials = 1, RowScale = 2, RowAcc = 3 };

@@ -11,7 +11,7 @@ import os
 
 import torch  # noqa: F401  (must be imported before the library is loaded)
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmq.so")
 
@@ -28,6 +28,8 @@ _SIGNATURES = {
     "mq_swiglu_rotquant": ([c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_vp], c_int),
     "mq_decode_w4a8_codebook": ([c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_int, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp],
                                 c_int),
+    "mq_quantize_weight": ([c_vp, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp],
+                           c_int),
     "mq_gemm_w4_group": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_vp,
                           c_i64, c_i64, c_i64, c_i64, c_vp], c_int),
     "mq_gemm_w4_group_ws": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_vp,
@@ -47,6 +49,8 @@ EXPORTED = tuple(_SIGNATURES)
 # code layouts (include/mq.h)
 Q_BYTES, Q_PACKED, Q_X16ALT = 0, 1, 2
 ACT_I8, ACT_I4, ACT_X16ALT = 0, 1, 2
+DT_BF16, DT_F16, DT_F32 = 0, 1, 2
+WFMT_U4_ASYM_G64, WFMT_I4_SYM_G64, WFMT_I4_ROW, WFMT_I8_ROW = 0, 1, 2, 3
 
 
 class MQError(RuntimeError):

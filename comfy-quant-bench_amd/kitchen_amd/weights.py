@@ -1,9 +1,11 @@
-"""Offline weight quantizers (the converter side of the path), in torch float32 arithmetic.
+"""Offline weight quantizers (the converter side of the path).
 
-They run once per layer at conversion or load time, on whatever device the weight is on, and
-produce the packed tensors the GEMM entry points consume. Rotation uses the same fp32 radix-4
-FWHT order as the online activation kernel (experiments/qwen21-kernel/kernels/g64_quant.cu:68-86),
-so codes are reproducible bit for bit.
+They run once per layer at conversion or load time and produce the packed tensors the GEMM entry
+points consume. A weight on the GPU is quantized by the library's HIP kernel (mq_quantize_weight);
+a weight in host memory by the same arithmetic in torch float32 on the CPU (for conversions on a
+machine without the GPU). Rotation uses the fp32 radix-4 FWHT order of the online activation
+kernel (experiments/qwen21-kernel/kernels/g64_quant.cu:68-86), and both implementations use IEEE
+divisions, so codes and scales are identical bit for bit.
 
     quantize_w4a8_asym_weight     configs' W4A8: uint4 asymmetric per group, fp16 scale, uint4 zero
     quantize_w4a4_group_weight    configs' W4A4: int4 symmetric per group, fp16 scale
@@ -62,6 +64,39 @@ def pack_u4(q: torch.Tensor) -> torch.Tensor:
     return (lo | (hi << 4)).to(torch.uint8).contiguous()
 
 
+def _hip_quantize(weight: torch.Tensor, convrot_groupsize: int | None, fmt: int):
+    """mq_quantize_weight on a device-resident weight [N, K]: (q, scale[, zero]) as the torch
+    quantizers below return them."""
+    from . import _lib
+
+    if weight.dim() != 2:
+        raise ValueError("weight must be 2-D [N, K]")
+    dts = {torch.bfloat16: _lib.DT_BF16, torch.float16: _lib.DT_F16, torch.float32: _lib.DT_F32}
+    w = weight if weight.dtype in dts else weight.to(torch.float32)
+    if w.stride(1) != 1:
+        w = w.contiguous()
+    n, k = w.shape
+    cg = int(convrot_groupsize or 0)
+    if cg and cg not in HADAMARD_BLOCKS:
+        raise ValueError(f"convrot_groupsize must be one of {HADAMARD_BLOCKS}, got {cg}")
+    dev = w.device
+    group = fmt in (_lib.WFMT_U4_ASYM_G64, _lib.WFMT_I4_SYM_G64)
+    qdt = torch.uint8 if fmt == _lib.WFMT_U4_ASYM_G64 else torch.int8
+    q = torch.empty((n, k if fmt == _lib.WFMT_I8_ROW else k // 2), dtype=qdt, device=dev)
+    s = torch.empty((n, k // 64) if group else (n,), dtype=torch.float16 if group else torch.float32, device=dev)
+    z = torch.empty((n, (k // 64 + 1) // 2), dtype=torch.uint8, device=dev) if fmt == _lib.WFMT_U4_ASYM_G64 else None
+    _lib.call("mq_quantize_weight", w.data_ptr(), dts[w.dtype], n, k, w.stride(0), cg, fmt, q.data_ptr(),
+              q.stride(0), s.data_ptr(), s.stride(0) if group else 1, _lib.ptr(z), z.stride(0) if z is not None else 0,
+              _lib.stream_of(w))
+    if group and not torch.isfinite(s).all():
+        raise ValueError("group range overflows the fp16 scale")
+    return (q, s) if z is None else (q, s, z)
+
+
+def _on_gpu(weight: torch.Tensor) -> bool:
+    return weight.device.type == "cuda"
+
+
 def _rotated(weight: torch.Tensor, convrot_groupsize: int | None) -> torch.Tensor:
     if weight.dim() != 2:
         raise ValueError("weight must be 2-D [N, K]")
@@ -74,6 +109,9 @@ def quantize_w4a8_asym_weight(weight: torch.Tensor, group_size: int = 64, convro
     lo = min(min w, 0), hi = max(max w, 0), s = fp16((hi - lo) / 15), z = clamp(rne(-lo / s), 0, 15),
     q = clamp(rne(w / s) + z, 0, 15); an all-zero group stores s = z = q = 0.
     Returns (qdata uint8 [N, K/2], scales float16 [N, K/G], zeros uint8 [N, ceil(K/G/2)])."""
+    if _on_gpu(weight) and group_size == 64:
+        from . import _lib
+        return _hip_quantize(weight, convrot_groupsize, _lib.WFMT_U4_ASYM_G64)
     w = _rotated(weight, convrot_groupsize)
     n, k = w.shape
     if k % group_size:
@@ -99,6 +137,9 @@ def quantize_w4a4_group_weight(weight: torch.Tensor, group_size: int = 64, convr
     """Configs' W4A4 weight: rotate by H_cg, int4 symmetric per group with fp16 scale
     (tools/svdquant_probe.py:105-115): s = fp16(absmax / 7), q = clamp(rne(w / s), -7, 7).
     Returns (qweight int8 [N, K/2] packed signed, wscales float16 [N, K/G])."""
+    if _on_gpu(weight) and group_size == 64:
+        from . import _lib
+        return _hip_quantize(weight, convrot_groupsize, _lib.WFMT_I4_SYM_G64)
     w = _rotated(weight, convrot_groupsize)
     n, k = w.shape
     if k % group_size:
@@ -121,6 +162,9 @@ def quantize_convrot_w4a4_weight(weight: torch.Tensor, convrot_groupsize: int = 
         raise ValueError(f"int4 MMA kernel requires quant_group_size 64")
     if stochastic_rounding:
         raise NotImplementedError("stochastic rounding is not part of this path")
+    if _on_gpu(weight):
+        from . import _lib
+        return _hip_quantize(weight, convrot_groupsize, _lib.WFMT_I4_ROW)
     w = _rotated(weight, convrot_groupsize)
     s = _div(torch.clamp(w.abs().amax(dim=1), min=1e-10), 7.0)
     q = torch.clamp(torch.round(w / s[:, None]), -7, 7).to(torch.int8)
@@ -131,6 +175,10 @@ def quantize_int8_convrot_weight(weight: torch.Tensor, group_size: int | None = 
     """int8_tensorwise weight (tools/_formats.py:128-167; group_size is the rotation block, None
     for --no-convrot): s = absmax.clamp(min=1e-10) / 127, q = (w / s).round().clamp(-127, 127).
     Returns (qdata int8 [N, K], scale f32 [N, 1])."""
+    if _on_gpu(weight):
+        from . import _lib
+        q, s = _hip_quantize(weight, group_size, _lib.WFMT_I8_ROW)
+        return q, s[:, None]
     w = _rotated(weight, group_size)
     s = _div(torch.clamp(w.abs().amax(dim=1), min=1e-10), 127.0)
     q = torch.clamp(torch.round(w / s[:, None]), -127, 127).to(torch.int8)

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MQ_ABI_VERSION 5
+#define MQ_ABI_VERSION 6
 
 enum {
     MQ_OK = 0,
@@ -85,8 +85,10 @@ int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, in
  * Replaces swiglu_quantize_int4_rowwise_convrot64(h) (tools/ck_swiglu/swiglu_quant.cu:23-97 and
  * :111-120, dispatched by convrot_w4a4_linear(..., input_act="swiglu") at
  * patches/comfy_kitchen_swiglu_w4a4_fused.patch:17-33) and generalises it to every Hadamard block,
- * int8 codes and the group GEMM's code layouts. silu(g) = g / (1 + exp(-g)) with this library's
- * own fp32 exp (within 2 ulp; the reference uses a hardware approximation) and an IEEE division.
+ * int8 codes and the group GEMM's code layouts. silu(g) = g / (1 + exp(-g)) is taken correctly
+ * rounded to fp32 (the reference uses a hardware exp approximation and an fp32 division): a table of
+ * the exact results for every bf16 gate outside the closed forms |g| < 2^-25 -> g / 2,
+ * g >= 128 -> g, g <= -128 -> -0.
  *
  *   h      bf16 [M, 2K]: gate in columns [0, K), up in [K, 2K); row stride ldh >= 2K elements
  *          (ldh % 8 == 0, 16-byte aligned base)
@@ -95,6 +97,44 @@ int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, in
  */
 int mq_swiglu_rotquant(const void* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits, int packed,
                        void* q, int64_t ldq, float* scale, void* stream);
+
+/* Element types of mq_quantize_weight's input. */
+#define MQ_DT_BF16 0
+#define MQ_DT_F16 1
+#define MQ_DT_F32 2
+
+/* Weight formats written by mq_quantize_weight. */
+#define MQ_WFMT_U4_ASYM_G64 0   /* configs' W4A8: uint4 asymmetric per 64, fp16 scale, uint4 zero   */
+#define MQ_WFMT_I4_SYM_G64 1    /* configs' W4A4: int4 symmetric per 64, fp16 scale                  */
+#define MQ_WFMT_I4_ROW 2        /* shipped ConvRot W4A4: int4 per row, fp32 scale [N]                */
+#define MQ_WFMT_I8_ROW 3        /* int8_tensorwise: int8 per row, fp32 scale [N]                     */
+
+/*
+ * Offline weight quantizer (the converter side of the path): rotate each weight row by H_hblock
+ * (hblock 0 = no rotation; the pinned fp32 radix-4 order of mq_rotquant, folded into the weight
+ * as W_rot = W H, experiments/qwen21-kernel/node/__init__.py:69-71) and quantize it. Replaces the
+ * quantizers the converters call: quantize_convrot_w4a4_weight (tools/_formats.py:53-76,
+ * MQ_WFMT_I4_ROW), the int8_tensorwise quantizer (tools/_formats.py:128-167, MQ_WFMT_I8_ROW) and,
+ * for the configs' group schemes, the packed-uint4 writer behind tools/quant_w4a8.py:91-168.
+ * Arithmetic (fp32, IEEE division, round half to even):
+ *   U4_ASYM_G64  per group of 64: lo = min(min w, 0), hi = max(max w, 0), s = fp16((hi - lo) / 15),
+ *                z = clamp(rne(-lo / s), 0, 15), q = clamp(rne(w / s) + z, 0, 15); s = 0 -> q = z = 0
+ *   I4_SYM_G64   per group of 64: s = fp16(max |w| / 7), q = clamp(rne(w / s), -7, 7); s = 0 -> q = 0
+ *   I4_ROW       s = max(max |w|, 1e-10) / 7,   q = clamp(rne(w / s), -7, 7)
+ *   I8_ROW       s = max(max |w|, 1e-10) / 127, q = clamp(rne(w / s), -127, 127)
+ * A group whose range overflows fp16 stores an infinite scale (callers check the scales).
+ *
+ *   w      [N, K] of dtype MQ_DT_*, row stride ldw elements (>= K)
+ *   q      packed 4-bit codes [N, K/2] (low nibble = even k; unsigned for U4_ASYM, signed
+ *          otherwise) or int8 [N, K] for I8_ROW; row stride ldq bytes
+ *   scale  fp16 [N, K/64] (stride ld_scale elements) for the group formats, fp32 [N] otherwise
+ *   zero   U4_ASYM_G64 only: packed uint4 [N, ceil(K/128)] (group 2j low nibble), stride ld_zero
+ * Requires K % 64 == 0 (group formats) or K % 16 == 0, K % hblock == 0, K <= 32768. Output rows
+ * are written by plain stores; no alignment beyond the element size is needed.
+ */
+int mq_quantize_weight(const void* w, int dtype, int64_t N, int64_t K, int64_t ldw, int hblock, int format,
+                       void* q, int64_t ldq, void* scale, int64_t ld_scale, void* zero, int64_t ld_zero,
+                       void* stream);
 
 /*
  * Load-time decode of comfy-kitchen's shipped asym_w4a8_int8 weight (tools/_formats.py:79-125:

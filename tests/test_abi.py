@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mq_abi_version() == 5
+    assert lib.mq_abi_version() == 6
 
 
 def _err(lib):
@@ -102,3 +102,25 @@ def test_gemm_validation_rejects_before_launch(lib):
     assert "wbits" in _err(lib)
     assert lib.mq_gemm_rowscale_acc(None, 64, None, 64, 8, None, 8, 8, 64, None) == -1
     assert "null" in _err(lib)
+
+
+def test_quantize_weight_validation_rejects_before_launch(lib):
+    # (w, dtype, N, K, ldw, hblock, format, q, ldq, scale, ld_scale, zero, ld_zero, stream)
+    assert lib.mq_quantize_weight(None, 3, 4, 256, 256, 256, 0, None, 128, None, 4, None, 2, None) == -1
+    assert "dtype" in _err(lib)
+    assert lib.mq_quantize_weight(None, 0, 4, 256, 256, 256, 4, None, 128, None, 4, None, 2, None) == -1
+    assert "format" in _err(lib)
+    assert lib.mq_quantize_weight(None, 0, 4, 96, 96, 0, 0, None, 48, None, 2, None, 1, None) == -1
+    assert "multiple of 64" in _err(lib)
+    assert lib.mq_quantize_weight(None, 0, 4, 200, 200, 0, 3, None, 200, None, 1, None, 0, None) == -1
+    assert "multiple of 16" in _err(lib)
+    assert lib.mq_quantize_weight(None, 0, 4, 320, 320, 256, 2, None, 160, None, 1, None, 0, None) == -1
+    assert "not a multiple of the group size" in _err(lib)
+    assert lib.mq_quantize_weight(None, 0, 4, 256, 256, 32, 1, None, 128, None, 4, None, 0, None) == -1
+    assert "convrot group size" in _err(lib)
+    assert lib.mq_quantize_weight(None, 0, 4, 65536, 65536, 256, 1, None, 32768, None, 1024, None, 0, None) == -1
+    assert "32768" in _err(lib)
+    assert lib.mq_quantize_weight(None, 0, 4, 256, 256, 256, 0, None, 128, None, 4, None, 2, None) == -1
+    assert "null" in _err(lib)
+    # N == 0 is a valid no-op
+    assert lib.mq_quantize_weight(None, 2, 0, 256, 256, 256, 3, None, 256, None, 1, None, 0, None) == 0
