@@ -30,8 +30,8 @@ key order (`_formats.py:279-293`). Formats (tensor names per layer `<l>`):
                       <l>.weight_zero U8 [N, ceil(K/G/2)] packed uint4 zero-points  (configs' W4A8)
     w4a4_sym_g64      <l>.weight I8 [N, K/2], <l>.weight_scale F16 [N, K/G]   (configs' W4A4)
 
-The weight math is kitchen_amd.weights (torch fp32 on the chosen device, bit-identical codes on
-CPU and GPU). comfy-kitchen's codebook `asym_w4a8_int8` fitter is not reproduced (it is not in
+The weight math is kitchen_amd.weights (the HIP quantizer for --device cuda, torch fp32 on the
+CPU otherwise; bit-identical codes either way). comfy-kitchen's codebook `asym_w4a8_int8` fitter is not reproduced (it is not in
 the reference tree); files in that format are read by w4a8_int8_linear, not written here.
 """
 from __future__ import annotations
