@@ -182,8 +182,9 @@ def measure_traffic(args) -> dict:
 def measure_stack(steps: int = 3) -> dict:
     """ms per pass over the config-4 linear stack (every linear: rotate + quantize + GEMM +
     epilogue, inputs resident, random-init quantized weights): eager (one Python call per linear,
-    as a loader runs it) and replayed from one captured HIP graph (the 840 linears' kernels,
-    workspaces and outputs from the graph's memory pool); 1 untimed pass each, then `steps`."""
+    as a loader runs it), replayed from one captured HIP graph (the 840 linears' kernels,
+    workspaces and outputs from the graph's memory pool), and replayed from a graph of the
+    dual-stream pass (synth.stack_pass with a side stream); 1 untimed pass each, then `steps`."""
     import torch
 
     from kitchen_amd import synth
@@ -219,6 +220,18 @@ def measure_stack(steps: int = 3) -> dict:
     with torch.cuda.graph(graph):
         one_pass()
     ms_graph = timed(graph.replay)
+    # the same pass with each block's text and image linears on two streams (joined at the
+    # block's attention and end), captured in one graph
+    graph2 = torch.cuda.CUDAGraph()
+    side2 = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        synth.stack_pass(layers, acts, side=side2)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph2):
+        synth.stack_pass(layers, acts, side=side2)
+    ms_dual = timed(graph2.replay)
     ops = synth.stack_ops(layers)
     w4 = sum(l["fmt"] == "w4a4" for l in layers)
     out = {"workload": "config 4: 60 dual-stream MMDiT blocks x 14 linears (q k v out mlp_up mlp_down mod), "
@@ -226,8 +239,10 @@ def measure_stack(steps: int = 3) -> dict:
                        "weights), rest W8A8 (H256, int8 per-token acts, int8 per-row weights)",
            "ms_per_step": round(ms_graph, 3), "tops": round(ops / (ms_graph * 1e-3) / 1e12, 1),
            "ms_per_step_eager": round(ms_eager, 3), "timing": "HIP graph replay of one pass (eager alongside)",
+           "ms_per_step_dual_stream": round(ms_dual, 3), "tops_dual_stream": round(ops / (ms_dual * 1e-3) / 1e12, 1),
+           "dual_stream": "each block's text linears on a second stream, joined after q/k/v and at the block end",
            "ops_per_step": ops, "linears": len(layers), "w4a4_linears": w4, "steps": steps}
-    del graph, layers, acts
+    del graph, graph2, layers, acts
     torch.cuda.empty_cache()
     return out
 

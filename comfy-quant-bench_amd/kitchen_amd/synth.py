@@ -103,6 +103,39 @@ def stack_activations(device="cuda", seed: int = 5) -> dict:
     return out
 
 
+def stack_pass(layers, acts, side=None):
+    """One pass over the stack; returns the outputs in layer order. side=None: every linear in
+    order on the current stream. With a side stream, the two token streams of each MMDiT block run
+    concurrently (text linears on `side`, image linears on the current stream), joined where a
+    block joins them: after mod / q / k / v (the joint attention reads both streams' q, k, v) and
+    after out / mlp_up / mlp_down (the block's end). The text linears are small (M = 256) and
+    latency-bound, so they fill compute units the image GEMMs leave between tiles."""
+    outs = [None] * len(layers)
+    if side is None:
+        for i, layer in enumerate(layers):
+            outs[i] = stack_layer(layer, acts[(layer["M"], layer["K"])])
+        return outs
+    main = torch.cuda.current_stream()
+    blocks: dict = {}
+    for i, layer in enumerate(layers):
+        blocks.setdefault(layer["name"].split(".")[1], []).append(i)
+    for idx in blocks.values():
+        for phase in (("mod", "q", "k", "v"), ("out", "mlp_up", "mlp_down")):
+            side.wait_stream(main)
+            for i in idx:
+                layer = layers[i]
+                if layer["name"].rsplit(".", 1)[1] not in phase:
+                    continue
+                x = acts[(layer["M"], layer["K"])]
+                if layer["stream"] == "text":
+                    with torch.cuda.stream(side):
+                        outs[i] = stack_layer(layer, x)
+                else:
+                    outs[i] = stack_layer(layer, x)
+            main.wait_stream(side)
+    return outs
+
+
 def stack_layer(layer, x):
     """One linear of the stack through the drop-in ops."""
     from . import ops

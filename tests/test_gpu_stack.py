@@ -70,3 +70,31 @@ def test_graph_replay_matches_eager(gpu_device):
             assert torch.equal(y, ref), (rep, l["name"])
         synth.stack_layer(layers[0], acts[(layers[0]["M"], layers[0]["K"])])   # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_dual_stream_graph_matches_single_stream(gpu_device):
+    # two blocks: text linears on a side stream (joined after q/k/v and at each block end),
+    # captured in one graph and replayed several times; outputs equal the single-stream pass
+    print("[stack] dual-stream graph of two blocks", flush=True)
+    layers = synth.mmdit_linear_stack(blocks=2, device=gpu_device)
+    acts = synth.stack_activations(gpu_device)
+    ref = [y.clone() for y in synth.stack_pass(layers, acts)]
+    side = torch.cuda.Stream()
+    warm = torch.cuda.Stream()
+    warm.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(warm):
+        eager2 = synth.stack_pass(layers, acts, side=side)
+    torch.cuda.current_stream().wait_stream(warm)
+    torch.cuda.synchronize()
+    for l, y, r in zip(layers, eager2, ref):
+        assert torch.equal(y, r), ("eager dual", l["name"])
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = synth.stack_pass(layers, acts, side=side)
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for l, y, r in zip(layers, outs, ref):
+            assert torch.equal(y, r), (rep, l["name"])
+        synth.stack_layer(layers[1], acts[(layers[1]["M"], layers[1]["K"])])   # eager work between replays
+        torch.cuda.synchronize()
