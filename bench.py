@@ -262,7 +262,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
-              "the W4A8 linear would shard over tokens or output channels with no exchange, see DESIGN.md.",
+              "the W4A8 linear would shard over tokens or output channels with no exchange between GPUs.",
               file=sys.stderr)
         return 2
     if args.kernels_child:
