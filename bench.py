@@ -247,6 +247,69 @@ def measure_stack(steps: int = 3) -> dict:
     return out
 
 
+def sweep() -> dict:
+    """Every BASELINE configuration's linear shapes, timed end to end (rotate + quantize + GEMM +
+    epilogue through the drop-in ops; median of 3 rounds of 10 calls, inputs resident) on
+    random-code quantized weights of each shape, plus the rotate+quantize kernel at config 3's
+    two activation widths. Returns {"linears": [...], "rotquant": [...]}."""
+    import torch
+
+    import kitchen_amd as ck
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(7)
+
+    def w4a8_weights(n, k):
+        qd = torch.randint(0, 256, (n, k // 2), generator=gen, device=dev, dtype=torch.uint8)
+        s16 = (torch.rand(n, k // 64, generator=gen, device=dev) * 0.004 + 0.004).to(torch.float16)
+        zp = torch.randint(0, 256, (n, (k // 64 + 1) // 2), generator=gen, device=dev, dtype=torch.uint8)
+        return qd, s16, zp
+
+    def w4a4_weights(n, k):
+        qw = torch.randint(-128, 128, (n, k // 2), generator=gen, device=dev, dtype=torch.int8)
+        s16 = (torch.rand(n, k // 64, generator=gen, device=dev) * 0.004 + 0.004).to(torch.float16)
+        return qw, s16
+
+    shapes = [("C0", "w4a8", 1024, 3072, 3072, 256)]
+    c1_kn = [(3072, 3072), (3072, 9216), (3072, 12288), (12288, 3072)]
+    shapes += [("C1", "w4a8", m, k, n, 256) for m in (4352, 8192) for k, n in c1_kn]
+    shapes += [("C1", "w4a8", 1, 3072, 18432, 256)]
+    shapes += [("C2", "w4a4", 4352, k, n, hb) for hb in (16, 64, 256) for k, n in c1_kn]
+    shapes += [("C3", "w4a8", 32760, k, n, 256) for k, n in ((3072, 9216), (3072, 14336), (14336, 3072))]
+    out = {"linears": [], "rotquant": []}
+    acts: dict = {}
+    for cfg, fmt, m, k, n, hb in shapes:
+        if (m, k) not in acts:
+            acts[(m, k)] = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
+        x = acts[(m, k)]
+        bias = (torch.randn(n, generator=gen, device=dev) * 0.1).to(torch.bfloat16)
+        if fmt == "w4a8":
+            qd, s16, zp = w4a8_weights(n, k)
+            fn = lambda: ck.w4a8_int8_linear(x, qd, s16, None, None, zp, bias, 64, hb, torch.bfloat16)  # noqa: E731
+        else:
+            qw, s16 = w4a4_weights(n, k)
+            fn = lambda: ck.convrot_w4a4_linear(x, qw, s16, bias, convrot_groupsize=hb, quant_group_size=64,  # noqa: E731
+                                                linear_dtype="int4")
+        ms = time_launches(fn, 10, rounds=3)
+        tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        out["linears"].append({"config": cfg, "format": fmt, "M": m, "K": k, "N": n, "hadamard_block": hb,
+                               "ms": round(ms, 5), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)})
+        print(json.dumps(out["linears"][-1]), file=sys.stderr, flush=True)
+        del fn
+    acts.clear()
+    for k in (3072, 14336):
+        x = torch.randn(RQ_M, k, generator=gen, device=dev).to(torch.bfloat16)
+        ms = time_launches(lambda: ck.quantize_int8_rowwise_convrot(x, 256), 10, rounds=3)
+        nbytes = RQ_M * k * 3 + 4 * RQ_M
+        out["rotquant"].append({"config": "C3", "M": RQ_M, "K": k, "ms": round(ms, 5),
+                                "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)})
+        print(json.dumps(out["rotquant"][-1]), file=sys.stderr, flush=True)
+        del x
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -258,6 +321,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 traffic counters")
     ap.add_argument("--no-stack", action="store_true", help="skip the config-4 linear stack")
+    ap.add_argument("--sweep", action="store_true",
+                    help="time every configuration's linear shapes instead (one JSON object, not the bench line)")
     ap.add_argument("--kernels-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -267,6 +332,9 @@ def main() -> int:
         return 2
     if args.kernels_child:
         return kernels_child(args)
+    if args.sweep:
+        print(json.dumps(sweep()))
+        return 0
 
     import torch
 
