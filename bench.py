@@ -6,7 +6,11 @@ quantize + uint4-asymmetric group-64 GEMM + scale/zero/bias epilogue to bf16, at
 N=12288, on seeded synthetic DiT-shaped data with every input resident in HBM. A step is one
 call of kitchen_amd.w4a8_int8_linear (two kernel launches on the current stream).
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--settle-ms 200]
+
+Before the W warmup steps the step runs untimed for settle_ms of wall time (and each kernel timed
+alone for half of that before its own measurement): the GPU clock ramps for tens of milliseconds
+after idle or after different work, and the figures are for the loaded steady state.
 
 Prints one JSON line: whole-linear int8 TOPS (2*M*N*K / step time), the GEMM kernel's roofline
 (average launch duration from HIP events on the launch stream, against the 5.0 POPS dense int8
@@ -54,11 +58,27 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def time_launches(fn, iters: int, rounds: int = 5, warm: int = 3) -> float:
-    """Median over `rounds` of the average milliseconds per call of fn (HIP events recorded on
-    torch's current stream, which is the stream the library launches on)."""
+def settle(fn, ms: float) -> None:
+    """Run fn untimed for `ms` milliseconds of wall time, so the GPU clock reaches its loaded
+    steady state for this work (it ramps over tens of milliseconds after idle or after other work)."""
+    import time
+
     import torch
 
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
+def time_launches(fn, iters: int, rounds: int = 5, warm: int = 3, settle_ms: float = 0.0) -> float:
+    """Median over `rounds` of the average milliseconds per call of fn (HIP events recorded on
+    torch's current stream, which is the stream the library launches on), after `settle_ms` of
+    untimed calls and `warm` more."""
+    import torch
+
+    settle(fn, settle_ms)
     for _ in range(warm):
         fn()
     torch.cuda.synchronize()
@@ -249,7 +269,8 @@ def measure_stack(steps: int = 3) -> dict:
 
 def sweep() -> dict:
     """Every BASELINE configuration's linear shapes, timed end to end (rotate + quantize + GEMM +
-    epilogue through the drop-in ops; median of 3 rounds of 10 calls, inputs resident) on
+    epilogue through the drop-in ops; median of 3 rounds of 10 calls after 50 ms of untimed calls,
+    inputs resident) on
     random-code quantized weights of each shape, plus the rotate+quantize kernel at config 3's
     two activation widths. Returns {"linears": [...], "rotquant": [...]}."""
     import torch
@@ -290,7 +311,7 @@ def sweep() -> dict:
             qw, s16 = w4a4_weights(n, k)
             fn = lambda: ck.convrot_w4a4_linear(x, qw, s16, bias, convrot_groupsize=hb, quant_group_size=64,  # noqa: E731
                                                 linear_dtype="int4")
-        ms = time_launches(fn, 10, rounds=3)
+        ms = time_launches(fn, 10, rounds=3, settle_ms=50.0)
         tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         out["linears"].append({"config": cfg, "format": fmt, "M": m, "K": k, "N": n, "hadamard_block": hb,
                                "ms": round(ms, 5), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)})
@@ -299,7 +320,7 @@ def sweep() -> dict:
     acts.clear()
     for k in (3072, 14336):
         x = torch.randn(RQ_M, k, generator=gen, device=dev).to(torch.bfloat16)
-        ms = time_launches(lambda: ck.quantize_int8_rowwise_convrot(x, 256), 10, rounds=3)
+        ms = time_launches(lambda: ck.quantize_int8_rowwise_convrot(x, 256), 10, rounds=3, settle_ms=50.0)
         nbytes = RQ_M * k * 3 + 4 * RQ_M
         out["rotquant"].append({"config": "C3", "M": RQ_M, "K": k, "ms": round(ms, 5),
                                 "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
@@ -315,6 +336,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--settle-ms", type=float, default=200.0,
+                    help="untimed steps for this long before the warmup steps (clock steady state)")
     ap.add_argument("--m", type=int, default=4096)
     ap.add_argument("--k", type=int, default=3072)
     ap.add_argument("--n", type=int, default=12288)
@@ -347,7 +370,8 @@ def main() -> int:
     def step():
         return ck.w4a8_int8_linear(x, qd, s16, None, None, zp, bias, 64, 256, torch.bfloat16)
 
-    # ---- whole linear: W untimed warmup steps, then exactly K timed steps
+    # ---- whole linear: untimed steps for settle_ms, W untimed warmup steps, then exactly K timed steps
+    settle(step, args.settle_ms)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -365,13 +389,13 @@ def main() -> int:
     # ---- dominant kernel (GEMM) alone, same stream, inputs resident
     qa, sa = ck.quantize_int8_rowwise_convrot(x, 256)
     qdu, zpu = qd.view(torch.uint8), zp.view(torch.uint8)
-    ms_gemm = time_launches(lambda: ck.gemm_w4_group(qa, sa, qdu, s16, zpu, bias, n), 20)
+    ms_gemm = time_launches(lambda: ck.gemm_w4_group(qa, sa, qdu, s16, zpu, bias, n), 20, settle_ms=args.settle_ms / 2)
     gemm_tops = ops / (ms_gemm * 1e-3) / 1e12
     ms_rq_ns = time_launches(lambda: ck.quantize_int8_rowwise_convrot(x, 256), 20)
 
     # ---- rotate+quantize kernel at the HBM-bound video-token shape (C3: 32760 x 3072, 302 MB)
     x3 = synth.to_bf16_tensor(synth.activations(RQ_M, k, seed=3), x.device)
-    ms_rq = time_launches(lambda: ck.quantize_int8_rowwise_convrot(x3, 256), 20)
+    ms_rq = time_launches(lambda: ck.quantize_int8_rowwise_convrot(x3, 256), 20, settle_ms=args.settle_ms / 2)
     rq_bytes = RQ_M * k * 2 + RQ_M * k + 4 * RQ_M
     rq_gbps = rq_bytes / (ms_rq * 1e-3) / 1e9
     del x3
@@ -390,6 +414,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": args.settle_ms,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
