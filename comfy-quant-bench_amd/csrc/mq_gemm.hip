@@ -275,8 +275,26 @@ int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     if (a.M > 128 && fits32 && zs_aligned && a.act_mode != 1) {
         GemmArgs w = a;
         w.ksplit = 1;
-        if (a.work && (epi == Epi::GroupScale || epi == Epi::RowScale))
+        if (a.work && (epi == Epi::GroupScale || epi == Epi::RowScale)) {
+            // a last, nearly empty wave of whole tile rows: those rows split along K, the rest not
+            const int64_t tail = split_tail_rows(a.M, a.N, a.K);
+            if (tail > 0) {
+                GemmArgs t = a;
+                t.M = tail;
+                t.qa = a.qa + (a.M - tail) * a.lda;
+                t.sa = a.sa + (a.M - tail);
+                t.y = a.y + (a.M - tail) * a.ldy;
+                t.ksplit = choose_ksplit(t.M, t.N, t.K, t.work_bytes, &t.kgroups);
+                if (t.ksplit > 1) {
+                    w.M = a.M - tail;
+                    w.work = nullptr;
+                    w.work_bytes = 0;
+                    const int rc = launch_gemm_wide(w, wk, epi, stream);
+                    return rc ? rc : launch_gemm_wide(t, wk, epi, stream);
+                }
+            }
             w.ksplit = choose_ksplit(a.M, a.N, a.K, a.work_bytes, &w.kgroups);
+        }
         return launch_gemm_wide(w, wk, epi, stream);
     }
     switch (wk) {

@@ -767,6 +767,20 @@ int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgro
     return static_cast<int>(s);
 }
 
+int64_t split_tail_rows(int64_t M, int64_t N, int64_t K) {
+    if (M <= TM || K % TK) return 0;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return 0;
+    const int64_t tiles_m = (M + TM - 1) / TM, tiles_n = (N + TN - 1) / TN;
+    const int64_t r = (tiles_m * tiles_n) % cus;   // tiles of the last, partial wave
+    if (tiles_m * tiles_n <= cus || r == 0 || r % tiles_n || 4 * r > cus) return 0;
+    const int64_t tail = M - (tiles_m - r / tiles_n) * TM;
+    int kgroups = 0;
+    return choose_ksplit(tail, N, K, INT64_MAX, &kgroups) > 1 ? tail : 0;
+}
+
 int launch_gemm_wide(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     switch (wk) {
         case WKind::U4Asym: return launch_wk<WKind::U4Asym>(a, epi, stream);

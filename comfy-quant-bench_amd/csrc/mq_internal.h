@@ -68,6 +68,12 @@ struct GemmArgs {
 // 256 x 256 tiles leave most compute units idle (small M).
 int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups);
 
+// Rows at the end of an M x N product that run as a separate split-K GEMM (0: none): when the
+// 256 x 256 tiles leave a last wave of whole tile rows that would occupy at most a quarter of the
+// compute units (M = 4352 = 4096 + 256 tokens against N = 12288: 816 tiles on 256 units), those
+// rows are split along K instead, so they take a fraction of a tile's time.
+int64_t split_tail_rows(int64_t M, int64_t N, int64_t K);
+
 // Power-of-two factor by which a group GEMM's MFMA result exceeds the true partial, per
 // activation layout and weight kind (see mq_gemm_wide.hip).
 __host__ __device__ inline int group_shift(int act_mode, WKind wk) {

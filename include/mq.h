@@ -190,9 +190,12 @@ int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8
  * most compute units idle (small M: the text-token linears, the adaLN-sized outputs) the K groups
  * are split into slices, each slice's workgroups write fp32 partial outputs [slices][M][N] into
  * the workspace, and a reduction kernel sums them in slice order (deterministic) and applies
- * sa, bias and the bf16 rounding. mq_gemm_workspace_bytes(M, N, K) gives the size that enables
- * the split on the current device (0: no split for this shape); a smaller or NULL workspace
- * runs without it. No reference counterpart: comfy-kitchen's GEMMs allocate internally.
+ * sa, bias and the bf16 rounding. For large M whose tiles would leave a last wave of whole tile
+ * rows occupying at most a quarter of the compute units (M = 4352 against N = 12288 on 256 units),
+ * only those trailing rows are split that way, after the others run unsplit.
+ * mq_gemm_workspace_bytes(M, N, K) gives the size that enables the split on the current device
+ * (0: no split for this shape); a smaller or NULL workspace runs without it. No reference
+ * counterpart: comfy-kitchen's GEMMs allocate internally.
  *   workspace  device memory, 16-byte aligned, workspace_bytes long (or NULL)
  */
 int mq_gemm_w4_group_ws(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
@@ -201,7 +204,7 @@ int mq_gemm_w4_group_ws(const int8_t* qa, int64_t lda, const float* sa, const ui
                         void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Workspace bytes mq_gemm_w4_group_ws / mq_gemm_rowscale_ws use for an M x N x K product on the
- * current device (0 when the shape fills the device without splitting K). */
+ * current device (0 when the shape fills the device without splitting K, whole or in part). */
 int64_t mq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /*

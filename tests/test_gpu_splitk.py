@@ -69,3 +69,51 @@ def test_group_split_matches_oracle(gpu_device, m, n, k):
     print(f"[splitk] rel L2 split {e_split:.2e} plain {e_plain:.2e}", flush=True)
     assert e_split < 4e-3 and e_plain < 4e-3
     assert gemm.rel_l2(y_plain.float().cpu().numpy(), y_split.float().cpu().numpy()) < 4e-3
+
+
+def test_tail_rows_split(gpu_device):
+    # M = 4352 against N = 12288: 17 x 48 = 816 tiles, a last wave of one tile row on 256 units;
+    # that row runs split along K after the first 4096 rows run unsplit
+    m, n, k = 4352, 12288, 3072
+    print(f"[splitk] tail rows M={m} N={n} K={k}", flush=True)
+    lib = _lib.load()
+    ws_bytes = lib.mq_gemm_workspace_bytes(m, n, k)
+    assert ws_bytes > 0 and ws_bytes % (256 * n * 4) == 0 and ws_bytes // (256 * n * 4) >= 2
+    assert lib.mq_gemm_workspace_bytes(4096, n, k) == 0
+    rng = np.random.default_rng(11)
+    qa = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    sa = rng.uniform(0.001, 0.01, m).astype(np.float32)
+    rows = np.r_[0:32, 4064:4128, m - 32:m]                      # both sides of the boundary
+    bias = torch.randn(n, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(gpu_device)
+    qa_d, sa_d = _t(qa, gpu_device), _t(sa, gpu_device)
+    # int8 row scale: exact int32 sums, so the split output equals the unsplit one bit for bit
+    qw = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    ws = rng.uniform(0.001, 0.01, n).astype(np.float32)
+    qw_d, ws_d = _t(qw, gpu_device), _t(ws, gpu_device)
+    y_split = ops.gemm_rowscale(qa_d, sa_d, qw_d, ws_d, bias, n, 8)
+    y_plain = torch.empty_like(y_split)
+    _lib.call("mq_gemm_rowscale", qa_d.data_ptr(), k, sa_d.data_ptr(), qw_d.data_ptr(), k, 8, ws_d.data_ptr(),
+              bias.data_ptr(), y_plain.data_ptr(), n, m, n, k, _lib.stream_of(qa_d))
+    torch.cuda.synchronize()
+    assert torch.equal(y_split, y_plain)
+    acc = qa[rows].astype(np.float64) @ qw.astype(np.float64).T          # exact in float64
+    ref = acc * sa[rows].astype(np.float64)[:, None] * ws.astype(np.float64)[None, :] + \
+        bias.float().cpu().numpy()[None, :]
+    assert gemm.rel_l2(ref, y_split.float().cpu().numpy()[rows]) < 4e-3
+    # uint4 group scale: fp32 slice sums, close to the unsplit kernel and to the oracle
+    q = rng.integers(0, 16, (n, k)).astype(np.uint8)
+    z = rng.integers(0, 16, (n, k // 64)).astype(np.uint8)
+    s16 = rng.uniform(1e-3, 4e-3, (n, k // 64)).astype(np.float16)
+    qw_d, z_d, s_d = _t(quant.pack_u4(q), gpu_device), _t(quant.pack_u4(z), gpu_device), _t(s16, gpu_device)
+    y_split = ops.gemm_w4_group(qa_d, sa_d, qw_d, s_d, z_d, bias, n)
+    y_plain = torch.empty_like(y_split)
+    _lib.call("mq_gemm_w4_group", qa_d.data_ptr(), k, sa_d.data_ptr(), qw_d.data_ptr(), k // 2, s_d.data_ptr(),
+              k // 64, z_d.data_ptr(), z_d.stride(0), 64, 0, bias.data_ptr(), y_plain.data_ptr(), n, m, n, k,
+              _lib.stream_of(qa_d))
+    torch.cuda.synchronize()
+    assert gemm.rel_l2(y_plain.float().cpu().numpy(), y_split.float().cpu().numpy()) < 4e-3
+    assert torch.equal(y_split[:4096], y_plain[:4096])                  # the unsplit rows are the same kernel
+    wdq = ((q.reshape(n, -1, 64).astype(np.float64) - z.astype(np.float64)[..., None]) *
+           s16.astype(np.float64)[..., None]).reshape(n, k)
+    ref = (qa[rows].astype(np.float64) * sa[rows].astype(np.float64)[:, None]) @ wdq.T + bias.float().cpu().numpy()
+    assert gemm.rel_l2(ref, y_split.float().cpu().numpy()[rows]) < 4e-3
