@@ -359,6 +359,12 @@ template <int BLK, int OUT, int ACT>
 int dispatch_nch(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, void* q, int64_t ldq,
                  float* scale, hipStream_t stream) {
     const int chunks = static_cast<int>((K + 1023) / 1024);
+    // few rows (the text-token and single-token calls): four waves per row, so the launch has
+    // four times the waves and each wave a quarter of the row's latency-bound chain
+    if (M <= 512 && chunks <= 8) {
+        if (chunks <= 4) return launch_rq<BLK, OUT, 1, ACT, 4>(x, M, K, ldx, q, ldq, scale, stream);
+        return launch_rq<BLK, OUT, 2, ACT, 4>(x, M, K, ldx, q, ldq, scale, stream);
+    }
     switch (chunks) {
         case 1: return launch_rq<BLK, OUT, 1, ACT, 1>(x, M, K, ldx, q, ldq, scale, stream);
         case 2: return launch_rq<BLK, OUT, 2, ACT, 1>(x, M, K, ldx, q, ldq, scale, stream);
