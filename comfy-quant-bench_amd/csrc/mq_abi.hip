@@ -43,12 +43,15 @@ namespace {
         }                            \
     } while (0)
 
+constexpr int kEmpty = 1;   // check_gemm_common: valid shape with nothing to compute
+
 int check_gemm_common(const int8_t* qa, int64_t lda, const void* qw, int64_t ldw, int64_t M, int64_t N,
                       int64_t K, int64_t wbytes_per_row) {
     MQ_REQUIRE(M >= 0 && N >= 0 && K > 0, "gemm: bad shape M=%lld N=%lld K=%lld", (long long)M,
                (long long)N, (long long)K);
     MQ_REQUIRE(K % 64 == 0, "gemm: K=%lld must be a multiple of 64", (long long)K);
     MQ_REQUIRE(M <= (int64_t(1) << 31) - 256 && N <= (int64_t(1) << 31) - 256, "gemm: M or N too large");
+    if (M == 0 || N == 0) return kEmpty;   // a valid no-op: no operand is read or written
     MQ_REQUIRE(qa && qw, "gemm: null operand");
     MQ_REQUIRE(lda >= K && lda % 16 == 0 && aligned(qa, 16), "gemm: qa needs lda >= K, lda %% 16 == 0 and a 16-byte aligned base");
     MQ_REQUIRE(ldw >= wbytes_per_row && ldw % 16 == 0 && aligned(qw, 16),
@@ -192,7 +195,7 @@ int mq_gemm_w4_group_ws(const int8_t* qa, int64_t lda, const float* sa, const ui
     MQ_REQUIRE(group == 64, "gemm_w4_group: quant group size must be 64 (got %d)", group);
     MQ_REQUIRE(act_mode >= MQ_ACT_I8 && act_mode <= MQ_ACT_X16ALT, "gemm_w4_group: unknown act_mode %d", act_mode);
     int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, K / 2);
-    if (rc) return rc;
+    if (rc) return rc == kEmpty ? MQ_OK : rc;
     MQ_REQUIRE(sa && ws && y, "gemm_w4_group: null pointer");
     MQ_REQUIRE(ldws >= K / group, "gemm_w4_group: ldws < K/group");
     MQ_REQUIRE(!wz || ldwz >= (K / group + 1) / 2, "gemm_w4_group: ldwz < ceil(K/group/2)");
@@ -223,7 +226,7 @@ int mq_gemm_w4_group_partials(const int8_t* qa, int64_t lda, const uint8_t* qw, 
     MQ_REQUIRE(act_mode >= MQ_ACT_I8 && act_mode <= MQ_ACT_X16ALT, "gemm_w4_group_partials: unknown act_mode %d",
                act_mode);
     int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, K / 2);
-    if (rc) return rc;
+    if (rc) return rc == kEmpty ? MQ_OK : rc;
     MQ_REQUIRE(part, "gemm_w4_group_partials: null pointer");
     MQ_REQUIRE(!wz || ldwz >= (K / group + 1) / 2, "gemm_w4_group_partials: ldwz < ceil(K/group/2)");
     GemmArgs a{};
@@ -238,7 +241,7 @@ int mq_gemm_rowscale_ws(const int8_t* qa, int64_t lda, const float* sa, const vo
     clear_error();
     MQ_REQUIRE(wbits == 4 || wbits == 8, "gemm_rowscale: wbits must be 4 or 8 (got %d)", wbits);
     int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, wbits == 4 ? K / 2 : K);
-    if (rc) return rc;
+    if (rc) return rc == kEmpty ? MQ_OK : rc;
     MQ_REQUIRE(sa && ws && y, "gemm_rowscale: null pointer");
     MQ_REQUIRE(ldy >= N, "gemm_rowscale: ldy < N");
     MQ_REQUIRE(workspace_bytes >= 0 && (!workspace || aligned(workspace, 16)),
@@ -273,7 +276,7 @@ int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t 
     clear_error();
     MQ_REQUIRE(wbits == 4 || wbits == 8, "gemm_rowscale_acc: wbits must be 4 or 8 (got %d)", wbits);
     int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, wbits == 4 ? K / 2 : K);
-    if (rc) return rc;
+    if (rc) return rc == kEmpty ? MQ_OK : rc;
     MQ_REQUIRE(acc, "gemm_rowscale_acc: null pointer");
     GemmArgs a{};
     a.qa = qa; a.lda = lda; a.qw = static_cast<const uint8_t*>(qw); a.ldw = ldw; a.part = acc;

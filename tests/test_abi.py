@@ -124,3 +124,14 @@ def test_quantize_weight_validation_rejects_before_launch(lib):
     assert "null" in _err(lib)
     # N == 0 is a valid no-op
     assert lib.mq_quantize_weight(None, 2, 0, 256, 256, 256, 3, None, 256, None, 1, None, 0, None) == 0
+
+
+def test_gemm_empty_shapes_are_noops(lib):
+    # M == 0 or N == 0 passes the shape checks and touches nothing (null pointers are fine)
+    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 64, 0, None, None, 8, 0, 8, 64, None) == 0
+    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 64, 0, None, None, 8, 8, 0, 64, None) == 0
+    assert lib.mq_gemm_rowscale(None, 64, None, None, 64, 8, None, None, None, 8, 0, 8, 64, None) == 0
+    assert lib.mq_gemm_rowscale_acc(None, 64, None, 64, 8, None, 0, 8, 64, None) == 0
+    assert lib.mq_gemm_w4_group_partials(None, 64, None, 32, None, 1, 64, 0, None, 0, 8, 64, None) == 0
+    # shape checks still apply to empty products
+    assert lib.mq_gemm_w4_group(None, 96, None, None, 48, None, 1, None, 1, 64, 0, None, None, 8, 0, 8, 96, None) == -1

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 import kitchen_amd as ck
-from kitchen_amd import synth
+from kitchen_amd import synth, weights
 from oracle import gemm, linear, quant
 
 pytestmark = pytest.mark.gpu
@@ -104,3 +104,19 @@ def test_leading_dims_and_m1(gpu_device):
     q0, s0, z0 = quant.quant_weight_u4_asym(linear.rotate_weight(w, 256), 64)
     ref = linear.w4a8_asym_linear(synth.bf16_bits_to_f32(xb), q0, s0, z0, None, 256, 64)
     assert gemm.rel_l2(ref.y, y.reshape(2, n).float().cpu().numpy()) < 1e-2
+
+
+def test_empty_batch(gpu_device):
+    # zero tokens (a leading dimension of 0) give an empty output of the right shape on every op
+    print("[linear] empty batch", flush=True)
+    n, k = 384, 512
+    w = torch.from_numpy(synth.weight(n, k, seed=9)).to(gpu_device)
+    qd, s16, zp = ck.quantize_w4a8_asym_weight(w, 64, 256)
+    qw, ws = ck.quantize_convrot_w4a4_weight(w, 256, 64)
+    q8, s8 = weights.quantize_int8_convrot_weight(w, 256)
+    for shape in ((0, k), (2, 0, k)):
+        x = torch.empty(shape, dtype=torch.bfloat16, device=gpu_device)
+        out = (*shape[:-1], n)
+        assert ck.w4a8_int8_linear(x, qd, s16, None, None, zp, None, 64, 256, torch.bfloat16).shape == out
+        assert ck.convrot_w4a4_linear(x, qw, ws, None).shape == out
+        assert ck.int8_linear(x, q8, s8, None, torch.bfloat16, True, 256).shape == out
