@@ -133,8 +133,9 @@ __device__ __forceinline__ void map_tile(int pid, int tiles_m, int tiles_n, int&
     tn = (pid % in_group) / gsize;
 }
 
-// Buffer resource over [base, base + bytes): loads outside the range return 0. Invalid rows are
-// given the offset kOob, which is out of range whatever the scalar offset adds to it.
+// Buffer resource over [base, base + bytes): loads whose vector offset lies outside the range
+// return 0 (the scalar offset is added to the address but is not part of that check, so it must
+// keep every in-range access inside the buffer). Invalid rows are given the vector offset kOob.
 constexpr int kOob = static_cast<int>(0x80000000u);
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
@@ -281,23 +282,29 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     asm volatile("" : "+v"(a_rd), "+v"(b_rd), "+v"(s_rd), "+v"(b_st0), "+v"(b_st1), "+v"(s_st));
 
     // Groups past the last one ("dead" groups, which pad the loop to a multiple of the unroll) load
-    // with a scalar offset beyond every buffer range: their codes, zero-points and scales are all
-    // zero, so they add nothing to any accumulator.
-    constexpr int kDead = 0x7fffffff;   // voffset + kDead never wraps and is never in range
-    auto soff = [&](int g, int per_group) { return g < G ? g * per_group : kDead; };
+    // through resources of zero bytes, so every such access is out of range and returns 0: their
+    // codes, zero-points and scales are all zero and add nothing to any accumulator. (A scalar
+    // offset past the range would not do: the range check does not include it.)
+    const auto ra_none = rsrc(a.qa, 0);
+    const auto rb_none = rsrc(a.qw, 0);
+    const u4v d_none = sdesc(a.qw, 0);
+    auto soff = [&](int g, int per_group) { return g < G ? g * per_group : 0; };
     // DMA of group g's A (and int8 B) tile into stage st
     auto dma_group = [&](int g, int st) {
+        const bool live = g < G;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            dma16(ra_rs, smem, A_LDS + st * TILE_BYTES + dma_lds + h * 16 * TK, dma_a[h], soff(g, TK));
+            dma16(live ? ra_rs : ra_none, smem, A_LDS + st * TILE_BYTES + dma_lds + h * 16 * TK, dma_a[h],
+                  soff(g, TK));
             if constexpr (!kPacked)
-                dma16(rb_rs, smem, B_LDS + st * TILE_BYTES + dma_lds + h * 16 * TK, dma_b[h], soff(g, TK));
+                dma16(live ? rb_rs : rb_none, smem, B_LDS + st * TILE_BYTES + dma_lds + h * 16 * TK, dma_b[h],
+                      soff(g, TK));
         }
     };
     // Two register sets carry packed B groups from their global load to their LDS store.
     u4v rb[2] = {u4v{0u, 0u, 0u, 0u}, u4v{0u, 0u, 0u, 0u}};
     auto gload_b = [&](int g, int set) {
-        if constexpr (kPacked) rb[set] = asm_ld128(db, b_off, soff(g, TK / 2));
+        if constexpr (kPacked) rb[set] = asm_ld128(g < G ? db : d_none, b_off, soff(g, TK / 2));
     };
     // Zero-points and scales of a block of four K groups b4 .. b4 + 3 (b4 % 4 == 0), one load each
     // per block instead of one per group: zq holds the four zero-point nibbles (group b4 + u in
@@ -306,8 +313,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // and their activations are zero.
     uint32_t zq = 0u, sq = 0u;
     auto gload_zs = [&](int b4) {
-        if constexpr (WK == WKind::U4Asym) zq = asm_ld16(dz, z_off, b4 < G ? b4 >> 1 : kDead);
-        if constexpr (EPI == Epi::GroupScale) sq = asm_ld32(ds, s_off, soff(b4, 2));
+        if constexpr (WK == WKind::U4Asym) zq = asm_ld16(b4 < G ? dz : d_none, z_off, b4 < G ? b4 >> 1 : 0);
+        if constexpr (EPI == Epi::GroupScale) sq = asm_ld32(b4 < G ? ds : d_none, s_off, soff(b4, 2));
     };
     // Wait until at most N VMEM operations are outstanding; register set SET counts as written by
     // the wait, so no use of it moves above it.
