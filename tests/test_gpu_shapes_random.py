@@ -1,13 +1,14 @@
-"""Seeded random shapes through every GEMM entry point (few-row, 128-tile, 256-tile and split-K
-kernels are all reached) against the oracle: exact int32 partials / accumulators where the entry
-point exposes them, and the bf16 outputs (with and without the split-K workspace) against a float64
-product of the same codes. Sizes are drawn so the oracle finishes in seconds."""
+"""Seeded random shapes against the oracle. GEMM: every entry point (few-row, 128-tile, 256-tile and
+split-K kernels are all reached), exact int32 partials / accumulators where the entry point exposes
+them, and the bf16 outputs (with and without the split-K workspace) against a float64 product of the
+same codes. Rotate + quantize, plain and with the SwiGLU prologue: codes and scales bit-exact. Sizes
+are drawn so the oracle finishes in seconds."""
 import numpy as np
 import pytest
 import torch
 
-from kitchen_amd import _lib, ops
-from oracle import gemm, quant
+from kitchen_amd import _lib, ops, synth
+from oracle import gemm, quant, swiglu
 
 pytestmark = pytest.mark.gpu
 
@@ -95,3 +96,56 @@ def test_rowscale(gpu_device, wbits, case, m, n, k):
     assert np.array_equal(acc.cpu().numpy().astype(np.int64), p)
     ref = p.astype(np.float64) * sa.astype(np.float64)[:, None] * ws.astype(np.float64)[None, :]
     assert gemm.rel_l2(ref, y.float().cpu().numpy()) < 4e-3
+
+
+# Rotate + quantize (plain and SwiGLU prologue): seeded random M (both sides of the 512-row switch
+# between four waves per row and one), K, Hadamard block and code layout; codes and scales bit-exact.
+RQ_MODES = [(8, _lib.Q_BYTES), (4, _lib.Q_BYTES), (4, _lib.Q_PACKED), (4, _lib.Q_X16ALT)]
+RQ_CASES = []
+for i in range(12):
+    hb = int(RNG.choice([0, 16, 64, 256]))
+    bits, layout = RQ_MODES[int(RNG.integers(0, 4))]
+    unit = max(hb, 64)                                   # K: whole Hadamard blocks and 64-column groups
+    k = unit * int(RNG.choice([1, 3, 5, 12, 47, 48, 129, 256])) % 16384 or 16384
+    m = int(RNG.choice([1, 7, 64, 300, 512, 513, 1100]))
+    RQ_CASES.append((i, m, k, hb, bits, layout))
+
+
+def _check_codes(q, s, q0, s0, layout):
+    assert np.array_equal(s.view(np.uint32), s0.view(np.uint32)), "scales differ"
+    if layout == _lib.Q_X16ALT:
+        sign = np.where((np.arange(q0.shape[1]) // 64) % 2 == 1, -1, 1).astype(np.int16)
+        assert np.array_equal(q.astype(np.int16), 16 * q0.astype(np.int16) * sign[None, :]), "x16alt codes differ"
+    elif layout == _lib.Q_PACKED:
+        assert np.array_equal(q, quant.pack_i4(q0)), "packed codes differ"
+    else:
+        assert np.array_equal(q, q0), "codes differ"
+
+
+@pytest.mark.parametrize("case,m,k,hb,bits,layout", RQ_CASES)
+def test_rotquant(gpu_device, case, m, k, hb, bits, layout):
+    print(f"[random] rotquant case {case} M={m} K={k} hblock={hb} bits={bits} layout={layout}", flush=True)
+    xb = synth.activations(m, k, seed=400 + case)
+    q, s = ops.rotate_quantize(synth.to_bf16_tensor(xb, gpu_device), hb, bits, layout)
+    torch.cuda.synchronize()
+    xf = synth.bf16_bits_to_f32(xb)
+    q0, s0 = quant.rotquant(xf, hb, bits) if hb else quant.quant_per_token(xf, 127 if bits == 8 else 7)
+    _check_codes(q.cpu().numpy(), s.cpu().numpy(), q0, s0, layout)
+
+
+@pytest.mark.parametrize("case,m,k,hb,bits,layout", RQ_CASES[:8])
+def test_swiglu_rotquant(gpu_device, case, m, k, hb, bits, layout):
+    m = min(m, 300)
+    print(f"[random] swiglu rotquant case {case} M={m} K={k} hblock={hb} bits={bits} layout={layout}", flush=True)
+    rng = np.random.default_rng(500 + case)
+    g = rng.standard_normal((m, k)).astype(np.float32) * 3.0
+    u = synth.bf16_bits_to_f32(synth.activations(m, k, seed=600 + case))
+    hb_bits = synth.f32_to_bf16_bits(np.concatenate([g, u], axis=1))
+    q, s = ops.rotate_quantize(synth.to_bf16_tensor(hb_bits, gpu_device), hb, bits, layout, swiglu=True)
+    torch.cuda.synchronize()
+    hf = synth.bf16_bits_to_f32(hb_bits)
+    if hb:
+        q0, s0 = swiglu.swiglu_rotquant(hf, hb, bits)
+    else:
+        q0, s0 = quant.quant_per_token(swiglu.swiglu_bf16(*np.split(hf, 2, axis=1)), 127 if bits == 8 else 7)
+    _check_codes(q.cpu().numpy(), s.cpu().numpy(), q0, s0, layout)
