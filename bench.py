@@ -44,6 +44,9 @@ RQ_M = 32760                 # video-token shape of the rotate+quantize roofline
 COPY_BYTES = 256 << 20       # calibration copy for the traffic counters
 GEMM_KERNEL = "gemm_wide_kernel"
 RQ_KERNEL = "rotquant_kernel"
+GEMV_KERNEL = "gemv_kernel"
+GEMV_N = 18432               # config 1's adaLN linear at M = 1: K = 3072 -> N = 18432
+GEMV_COPIES = 10             # weight copies cycled over the calls: 305 MB, above the 256 MB MALL
 COPY_KERNEL = "copyBuffer"
 
 
@@ -115,6 +118,70 @@ def make_inputs(m: int, k: int, n: int):
     return xb, bias_f, x, qd, s16, zp, bias
 
 
+def gemv_inputs(x, k: int):
+    """The M = 1 GEMM's operands: the quantized first activation row and GEMV_COPIES random-code
+    uint4-asymmetric g64 weight sets [GEMV_N, k] (packed codes, fp16 scales, packed zero-points)."""
+    import torch
+
+    import kitchen_amd as ck
+
+    dev = x.device
+    gen = torch.Generator(device=dev).manual_seed(5)
+    qa, sa = ck.quantize_int8_rowwise_convrot(x[:1], 256)
+    g = k // 64
+    copies = [(torch.randint(0, 256, (GEMV_N, k // 2), generator=gen, device=dev, dtype=torch.uint8),
+               (torch.rand(GEMV_N, g, generator=gen, device=dev) * 0.004 + 0.004).to(torch.float16),
+               torch.randint(0, 256, (GEMV_N, (g + 1) // 2), generator=gen, device=dev, dtype=torch.uint8))
+              for _ in range(GEMV_COPIES)]
+    bias = torch.zeros(GEMV_N, dtype=torch.bfloat16, device=dev)
+    return qa, sa, copies, bias
+
+
+def gemv_bytes(k: int) -> int:
+    """Algorithmic bytes of one M = 1 call: packed weights, fp16 scales, packed zero-points, the
+    int8 activation row and its scale, bias and bf16 output."""
+    g = k // 64
+    return GEMV_N * k // 2 + GEMV_N * g * 2 + GEMV_N * ((g + 1) // 2) + k + 4 + 2 * GEMV_N + 2 * GEMV_N
+
+
+def measure_gemv(x, settle_ms: float, launches: int = 40) -> dict:
+    """The M = 1 W4A8 GEMM (the few-row GEMV kernel) at config 1's adaLN shape, HBM-bound on the
+    packed weights. Consecutive calls read different weight copies (GEMV_COPIES of them, more than
+    the MALL holds), so each call's weights come from HBM. `launches` calls are captured in one HIP
+    graph and replayed, so the host's launch cost (longer than the kernel) stays out of the timing;
+    the time per launch still includes the graph's gap between consecutive kernels."""
+    import torch
+
+    import kitchen_amd as ck
+
+    k = x.shape[1]
+    qa, sa, copies, bias = gemv_inputs(x, k)
+
+    def calls():
+        for i in range(launches):
+            qd, s16, zp = copies[i % GEMV_COPIES]
+            ck.gemm_w4_group(qa, sa, qd, s16, zp, bias, GEMV_N)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        calls()                                      # warm the allocator on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        calls()
+    ms = time_launches(graph.replay, 5, settle_ms=settle_ms) / launches
+    nbytes = gemv_bytes(k)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    del graph, copies
+    torch.cuda.empty_cache()
+    return {"bound": "hbm", "kernel": "gemv_kernel<U4Asym,GroupScale,0,1>", "M": 1, "K": k, "N": GEMV_N,
+            "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "bytes_per_launch": nbytes, "avg_launch_ms": round(ms, 5), "weight_copies": GEMV_COPIES,
+            "timing": f"HIP graph of {launches} launches over {GEMV_COPIES} weight copies, per launch"}
+
+
 def kernels_child(args) -> int:
     """Launch each measured kernel a few times and exit (run under rocprofv3 by measure_traffic)."""
     import torch
@@ -130,6 +197,11 @@ def kernels_child(args) -> int:
     x3 = synth.to_bf16_tensor(synth.activations(RQ_M, k, seed=3), x.device)
     for _ in range(3):
         ck.quantize_int8_rowwise_convrot(x3, 256)
+    del x3
+    gqa, gsa, copies, gbias = gemv_inputs(x, k)
+    for qdc, s16c, zpc in copies[:3]:
+        ck.gemm_w4_group(gqa, gsa, qdc, s16c, zpc, gbias, GEMV_N)
+    del copies
     src = torch.empty(COPY_BYTES // 4, dtype=torch.int32, device=x.device)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -147,7 +219,7 @@ def _counter_means(csv_path: str, counter: str) -> dict:
         if row.get("Counter_Name") != counter:
             continue
         name = row["Kernel_Name"]
-        for key in (GEMM_KERNEL, RQ_KERNEL, COPY_KERNEL):
+        for key in (GEMM_KERNEL, RQ_KERNEL, GEMV_KERNEL, COPY_KERNEL):
             if key in name:
                 sums.setdefault(key, []).append((int(row.get("Grid_Size") or 0), float(row["Counter_Value"])))
     out = {}
@@ -191,7 +263,7 @@ def measure_traffic(args) -> dict:
     f_fetch = COPY_BYTES / (out["FETCH_SIZE"][COPY_KERNEL] * 1024.0)
     f_write = COPY_BYTES / (out["WRITE_SIZE"][COPY_KERNEL] * 1024.0)
     res = {"fetch_scale": round(f_fetch, 4), "write_scale": round(f_write, 4)}
-    for key in (GEMM_KERNEL, RQ_KERNEL):
+    for key in (GEMM_KERNEL, RQ_KERNEL, GEMV_KERNEL):
         if key in out["FETCH_SIZE"] and key in out["WRITE_SIZE"]:
             fetch = out["FETCH_SIZE"][key] * 1024.0 * f_fetch
             write = out["WRITE_SIZE"][key] * 1024.0 * f_write
@@ -400,12 +472,16 @@ def main() -> int:
     rq_gbps = rq_bytes / (ms_rq * 1e-3) / 1e9
     del x3
 
+    # ---- M = 1 GEMV (config 1's adaLN shape), weights cycled past the MALL
+    gemv = measure_gemv(x, args.settle_ms / 2)
+
     # ---- the mixed W4A4 / W8A8 MMDiT linear stack (60 blocks x 14 linears)
     stack = None if args.no_stack else measure_stack()
 
     traffic = None if args.no_traffic else measure_traffic(args)
     gemm_traffic = traffic.get(GEMM_KERNEL, {}).get("bytes") if traffic else None
     rq_traffic = traffic.get(RQ_KERNEL, {}).get("bytes") if traffic else None
+    gemv["traffic"] = traffic.get(GEMV_KERNEL, {}).get("bytes") if traffic else None
 
     result = {
         "metric": METRIC,
@@ -432,6 +508,7 @@ def main() -> int:
                               "frac": round(rq_gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": rq_bytes,
                               "traffic": rq_traffic, "avg_launch_ms": round(ms_rq, 5),
                               "north_star_M_launch_ms": round(ms_rq_ns, 5)},
+        "gemv_roofline": gemv,
     }
     if stack is not None:
         result["c4_linear_stack"] = stack

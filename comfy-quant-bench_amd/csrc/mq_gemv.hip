@@ -33,6 +33,31 @@ __global__ void __launch_bounds__(64 * kWaves) gemv_kernel(GemmArgs a) {
     const int nchunks = K / kChunkK;
     uint32_t* act = gv_smem;                            // [MR][K / 4] dwords
     int* asum = reinterpret_cast<int*>(gv_smem + MR * (K / 4));   // [MR][nchunks] (uint4 asym)
+    const int64_t n_base = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * kCols;
+
+    // Raw weight chunk, zero-point byte and fp16 scale of chunk ch for the wave's kCols columns
+    // (zero past the row's end or past N). Decoding waits for the loads, so it happens at the use:
+    // the first chunk is loaded before the activation staging and every later one an iteration
+    // ahead, and the loads' latency overlaps the staging and the previous chunk's arithmetic.
+    struct Chunk {
+        uint4 w[kCols];
+        uint32_t z[kCols], s[kCols];
+    };
+    auto load_chunk = [&](int ch, Chunk& t) {
+        const int g = ch * kChunkK / 64;
+#pragma unroll
+        for (int c = 0; c < kCols; ++c) {
+            const int64_t n = n_base + c;
+            const bool ok = ch < nchunks && n < a.N;
+            t.w[c] = ok ? *reinterpret_cast<const uint4*>(a.qw + n * a.ldw + ch * 16) : uint4{0u, 0u, 0u, 0u};
+            t.z[c] = 0u;
+            t.s[c] = 0u;
+            if constexpr (WK == WKind::U4Asym) t.z[c] = ok ? a.wz[n * a.ldwz + (g >> 1)] : 0u;
+            if constexpr (EPI == Epi::GroupScale) t.s[c] = ok ? a.ws16[n * a.ldws + g] : 0u;
+        }
+    };
+    Chunk cur, next;
+    load_chunk(lane, cur);
 
     // stage the activation rows (de-interleaved per 8 values for 4-bit weights)
     for (int i = tid; i < MR * (K / 8); i += 64 * kWaves) {
@@ -61,7 +86,6 @@ __global__ void __launch_bounds__(64 * kWaves) gemv_kernel(GemmArgs a) {
     }
     __syncthreads();
 
-    const int64_t n_base = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * kCols;
     float accf[kCols][MR];
     int acci[kCols][MR];
 #pragma unroll
@@ -72,23 +96,16 @@ __global__ void __launch_bounds__(64 * kWaves) gemv_kernel(GemmArgs a) {
             acci[c][m] = 0;
         }
     for (int ch = lane; ch < nchunks; ch += 64) {
-        uint4 w[kCols];
-#pragma unroll
-        for (int c = 0; c < kCols; ++c) {
-            const int64_t n = n_base + c;
-            w[c] = n < a.N ? *reinterpret_cast<const uint4*>(a.qw + n * a.ldw + ch * 16) : uint4{0u, 0u, 0u, 0u};
-        }
+        load_chunk(ch + 64, next);
         const int g = ch * kChunkK / 64;
 #pragma unroll
         for (int c = 0; c < kCols; ++c) {
-            const int64_t n = n_base + c;
-            const bool ok = n < a.N;
-            const uint32_t wd[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+            const uint32_t wd[4] = {cur.w[c].x, cur.w[c].y, cur.w[c].z, cur.w[c].w};
             int z = 0;
-            if constexpr (WK == WKind::U4Asym) z = ok ? (a.wz[n * a.ldwz + (g >> 1)] >> (4 * (g & 1))) & 0xf : 0;
+            if constexpr (WK == WKind::U4Asym) z = (cur.z[c] >> (4 * (g & 1))) & 0xf;
             float s = 0.0f;
             if constexpr (EPI == Epi::GroupScale) {
-                s = ok ? f16_bits_to_f32(a.ws16[n * a.ldws + g]) : 0.0f;
+                s = f16_bits_to_f32(static_cast<uint16_t>(cur.s[c]));
                 if constexpr (WK == WKind::I4Sym) s *= 0.0625f;
                 if constexpr (AM == 2) s *= (g & 1) ? -0.0625f : 0.0625f;
             }
@@ -114,6 +131,7 @@ __global__ void __launch_bounds__(64 * kWaves) gemv_kernel(GemmArgs a) {
                 else acci[c][m] += d;
             }
         }
+        cur = next;
     }
     // wavefront reductions and the epilogue (lane 0 writes)
 #pragma unroll
