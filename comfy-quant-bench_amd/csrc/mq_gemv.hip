@@ -23,8 +23,11 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kCols = 4;        // output columns per wavefront step
 
+// One row (the adaLN modulation linear, M = 1) is built for five waves per SIMD: 1280 resident
+// workgroups, so config 1's N = 18432 (1152 workgroups) runs in one wave of workgroups instead of
+// a full second wave for its last 128 (the uint4 kernel then keeps 12 bytes of values in scratch).
 template <WKind WK, Epi EPI, int AM, int MR>
-__global__ void __launch_bounds__(64 * kWaves) gemv_kernel(GemmArgs a) {
+__global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(GemmArgs a) {
     constexpr bool kPacked = WK != WKind::I8;
     constexpr int kChunkK = kPacked ? 32 : 16;          // K values per 16-byte weight chunk
     extern __shared__ __attribute__((aligned(16))) uint32_t gv_smem[];
