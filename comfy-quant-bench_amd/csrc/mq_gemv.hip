@@ -63,28 +63,32 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
     load_chunk(lane, cur);
 
     // stage the activation rows (de-interleaved per 8 values for 4-bit weights)
-    for (int i = tid; i < MR * (K / 8); i += 64 * kWaves) {
-        const int m = i / (K / 8), b = i % (K / 8);
-        const uint2 x = m < a.M ? *reinterpret_cast<const uint2*>(a.qa + m * a.lda + 8 * b) : uint2{0u, 0u};
-        uint2 o = x;
-        if constexpr (kPacked) {
-            o.x = __builtin_amdgcn_perm(x.y, x.x, 0x06040200u);   // values 0, 2, 4, 6
-            o.y = __builtin_amdgcn_perm(x.y, x.x, 0x07050301u);   // values 1, 3, 5, 7
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        for (int b = tid; b < K / 8; b += 64 * kWaves) {
+            const uint2 x = m < a.M ? *reinterpret_cast<const uint2*>(a.qa + m * a.lda + 8 * b) : uint2{0u, 0u};
+            uint2 o = x;
+            if constexpr (kPacked) {
+                o.x = __builtin_amdgcn_perm(x.y, x.x, 0x06040200u);   // values 0, 2, 4, 6
+                o.y = __builtin_amdgcn_perm(x.y, x.x, 0x07050301u);   // values 1, 3, 5, 7
+            }
+            *reinterpret_cast<uint2*>(act + m * (K / 4) + 2 * b) = o;
         }
-        *reinterpret_cast<uint2*>(act + m * (K / 4) + 2 * b) = o;
     }
     if constexpr (WK == WKind::U4Asym) {
-        for (int i = tid; i < MR * nchunks; i += 64 * kWaves) {
-            const int m = i / nchunks, c = i % nchunks;
-            int s = 0;
-            if (m < a.M) {
-                const uint4 x0 = *reinterpret_cast<const uint4*>(a.qa + m * a.lda + c * kChunkK);
-                const uint4 x1 = *reinterpret_cast<const uint4*>(a.qa + m * a.lda + c * kChunkK + 16);
-                const uint32_t w[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-                for (int j = 0; j < 8; ++j) s = __builtin_amdgcn_sdot4(static_cast<int>(w[j]), 0x01010101, s, false);
+        for (int m = 0; m < MR; ++m) {
+            for (int c = tid; c < nchunks; c += 64 * kWaves) {
+                int s = 0;
+                if (m < a.M) {
+                    const uint4 x0 = *reinterpret_cast<const uint4*>(a.qa + m * a.lda + c * kChunkK);
+                    const uint4 x1 = *reinterpret_cast<const uint4*>(a.qa + m * a.lda + c * kChunkK + 16);
+                    const uint32_t w[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) s = __builtin_amdgcn_sdot4(static_cast<int>(w[j]), 0x01010101, s, false);
+                }
+                asum[m * nchunks + c] = s;
             }
-            asum[m * nchunks + c] = s;
         }
     }
     __syncthreads();
