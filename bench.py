@@ -182,6 +182,15 @@ def measure_gemv(x, settle_ms: float, launches: int = 40) -> dict:
             "timing": f"HIP graph of {launches} launches over {GEMV_COPIES} weight copies, per launch"}
 
 
+def _aux(fn) -> dict:
+    """An auxiliary measurement of the bench line: its result, or {"error": ...} if it raised, so
+    that the headline figures are still printed (the error names what to look at)."""
+    try:
+        return fn()
+    except Exception as e:  # noqa: BLE001 - reported in the JSON line instead of ending the run
+        return {"error": f"{type(e).__name__}: {e}"[:300]}
+
+
 def kernels_child(args) -> int:
     """Launch each measured kernel a few times and exit (run under rocprofv3 by measure_traffic)."""
     import torch
@@ -473,15 +482,16 @@ def main() -> int:
     del x3
 
     # ---- M = 1 GEMV (config 1's adaLN shape), weights cycled past the MALL
-    gemv = measure_gemv(x, args.settle_ms / 2)
+    gemv = _aux(lambda: measure_gemv(x, args.settle_ms / 2))
 
     # ---- the mixed W4A4 / W8A8 MMDiT linear stack (60 blocks x 14 linears)
-    stack = None if args.no_stack else measure_stack()
+    stack = None if args.no_stack else _aux(measure_stack)
 
     traffic = None if args.no_traffic else measure_traffic(args)
     gemm_traffic = traffic.get(GEMM_KERNEL, {}).get("bytes") if traffic else None
     rq_traffic = traffic.get(RQ_KERNEL, {}).get("bytes") if traffic else None
-    gemv["traffic"] = traffic.get(GEMV_KERNEL, {}).get("bytes") if traffic else None
+    if "error" not in gemv:
+        gemv["traffic"] = traffic.get(GEMV_KERNEL, {}).get("bytes") if traffic else None
 
     result = {
         "metric": METRIC,

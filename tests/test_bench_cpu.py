@@ -59,3 +59,9 @@ def test_more_than_one_gpu_is_refused():
                          text=True, timeout=120)
     assert res.returncode == 2
     assert "one GPU" in res.stderr and res.stdout == ""
+
+
+def test_auxiliary_measurement_errors_are_reported_not_raised():
+    assert bench._aux(lambda: {"ms": 1.0}) == {"ms": 1.0}
+    err = bench._aux(lambda: 1 / 0)
+    assert set(err) == {"error"} and err["error"].startswith("ZeroDivisionError")
