@@ -50,15 +50,36 @@ GEMV_COPIES = 10             # weight copies cycled over the calls: 305 MB, abov
 COPY_KERNEL = "copyBuffer"
 
 
-def cpu_model() -> str:
+def cpu_info() -> dict:
+    """The host CPU as lscpu reports it (model name, sockets, cores per socket, threads per core,
+    logical CPUs) plus /proc/cpuinfo's model name where lscpu's is shorter."""
+    info: dict = {}
+    keys = {"Model name": "model", "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+            "Thread(s) per core": "threads_per_core", "CPU(s)": "logical_cpus", "Vendor ID": "vendor"}
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
         for line in out.splitlines():
-            if line.startswith("Model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            if key.strip() in keys and keys[key.strip()] not in info:
+                info[keys[key.strip()]] = val.strip()
     except OSError:
         pass
-    return platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    full = line.split(":", 1)[1].strip()
+                    if len(full) > len(info.get("model", "")):
+                        info["model"] = full
+                    break
+    except OSError:
+        pass
+    info.setdefault("model", platform.processor() or "unknown")
+    try:
+        info["physical_cores"] = int(info["sockets"]) * int(info["cores_per_socket"])
+    except (KeyError, ValueError):
+        pass
+    return info
 
 
 def settle(fn, ms: float) -> None:
@@ -376,7 +397,8 @@ def sweep() -> dict:
     c1_kn = [(3072, 3072), (3072, 9216), (3072, 12288), (12288, 3072)]
     shapes += [("C1", "w4a8", m, k, n, 256) for m in (4352, 8192) for k, n in c1_kn]
     shapes += [("C1", "w4a8", 1, 3072, 18432, 256)]
-    shapes += [("C2", "w4a4", 4352, k, n, hb) for hb in (16, 64, 256) for k, n in c1_kn]
+    shapes += [("C2", "w4a4", m, k, n, hb) for hb in (16, 64, 256) for m in (4352, 8192) for k, n in c1_kn]
+    shapes += [("C2", "w4a4", 1, 3072, 18432, hb) for hb in (16, 64, 256)]
     shapes += [("C3", "w4a8", 32760, k, n, 256) for k, n in ((3072, 9216), (3072, 14336), (14336, 3072))]
     out = {"linears": [], "rotquant": []}
     acts: dict = {}
@@ -529,18 +551,28 @@ def main() -> int:
         from oracle import quant
         from oracle.torch_path import W4A8CpuLinear, time_cpu
 
-        ms = 512
+        ms = m   # the whole workload's rows: the sample is one full step, repeated for ~10 s
         q_codes = quant.unpack_u4(qd.cpu().numpy())
         z_codes = quant.unpack_u4(zp.cpu().numpy())[:, : k // 64]
         lin = W4A8CpuLinear(q_codes, s16.cpu().numpy(), z_codes, bias_f, 256, 64)
         xs = torch.from_numpy(synth.bf16_bits_to_f32(xb[:ms]))
-        t = time_cpu(lin, xs, runs=5)
+        # every CPU this process may use, capped by the host's CPU share for this job
+        # (OMP_NUM_THREADS, which torch's default thread count already follows)
+        usable = len(os.sched_getaffinity(0))
+        share = int(os.environ.get("OMP_NUM_THREADS", usable) or usable)
+        threads = max(1, min(usable, share))
+        torch.set_num_threads(threads)
+        t, calls = time_cpu(lin, xs, runs=5, min_seconds=10.0)
+        cpu = cpu_info()
         result["cpu_baseline"] = {
-            "value": round(2.0 * ms * n * k / t / 1e12, 4), "unit": "TOPS", "cores": torch.get_num_threads(),
-            "kind": "port", "cpu": cpu_model(),
-            "sample": f"M={ms} rows of the same linear (K={k}, N={n}): torch fp32 rotate-by-matmul, int8 "
-                      "per-token quant, dequantized-weight matmul, bias; median of 5 after 1 warm-up",
-            "seconds_per_sample": round(t, 4)}
+            "value": round(2.0 * ms * n * k / t / 1e12, 4), "unit": "TOPS", "cores": threads,
+            "threads": threads, "kind": "port", "cpu": cpu.get("model"), "lscpu": cpu,
+            "threads_rule": "threads = CPUs in this process's affinity mask, capped by OMP_NUM_THREADS "
+                            "(the job's CPU share on the GPU host); cores = those threads",
+            "sample": f"the whole step, M={ms} rows of the same linear (K={k}, N={n}): torch fp32 "
+                      f"rotate-by-matmul, int8 per-token quant, dequantized-weight matmul, bias; median of "
+                      f"{calls} calls (at least 5, and at least 10 s of timed work) after 1 warm-up",
+            "seconds_per_sample": round(t, 4), "calls": calls}
     print(json.dumps(result), flush=True)
     return 0
 

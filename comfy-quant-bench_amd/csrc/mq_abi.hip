@@ -2,6 +2,7 @@
 // reporting and dispatch to the kernel launchers. Nothing here allocates device memory.
 #include "../../include/mq.h"
 
+#include <atomic>
 #include <cstdarg>
 #include <cstring>
 
@@ -23,6 +24,22 @@ void set_error(const char* fmt, ...) {
 }
 
 void clear_error() { g_err[0] = '\0'; }
+
+int device_cu_count() {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cache[kMaxDevices];   // 0 = not queried yet
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    const bool cached = dev >= 0 && dev < kMaxDevices;
+    if (cached) {
+        const int v = cache[dev].load(std::memory_order_relaxed);
+        if (v > 0) return v;
+    }
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+    if (cached) cache[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
 
 int launch_status(const char* what) {
     const hipError_t e = hipGetLastError();

@@ -259,8 +259,10 @@ int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
 
 int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     if (a.M == 0 || a.N == 0) return 0;
-    // a few rows: HBM-bound, served by the dot4 kernel (activation rows staged in LDS)
-    if (a.M <= 4 && a.M * a.K <= 131072 && (epi == Epi::GroupScale || epi == Epi::RowScale))
+    // a few rows: HBM-bound, served by the dot4 kernel (activation rows staged in LDS); its parity
+    // entries (exact group partials, full-K sums) run the same kernel
+    if (a.M <= 4 && a.M * a.K <= 131072 && !(wk == WKind::I8 && epi == Epi::GroupPartials) &&
+        !(wk == WKind::U4Asym && epi == Epi::RowAcc))
         return launch_gemv(a, wk, epi, stream);
     // The 256 x 256-tile kernel addresses each operand with 32-bit buffer offsets.
     const int64_t wbytes = wk == WKind::I8 ? a.K : a.K / 2;

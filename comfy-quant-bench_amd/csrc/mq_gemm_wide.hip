@@ -758,10 +758,8 @@ int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
 int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups) {
     *kgroups = 0;
     if (M <= 128 || K % TK) return 1;                           // the 128-tile kernel has no split
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        return 1;
+    const int cus = device_cu_count();
+    if (cus <= 0) return 1;
     const int64_t tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
     const int64_t blocks = (K / TK + 3) / 4;                    // blocks of four K groups
     if (2 * tiles > cus || blocks < 4) return 1;
@@ -776,10 +774,8 @@ int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgro
 
 int64_t split_tail_rows(int64_t M, int64_t N, int64_t K) {
     if (M <= TM || K % TK) return 0;
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        return 0;
+    const int cus = device_cu_count();
+    if (cus <= 0) return 0;
     const int64_t tiles_m = (M + TM - 1) / TM, tiles_n = (N + TN - 1) / TN;
     const int64_t r = (tiles_m * tiles_n) % cus;   // tiles of the last, partial wave
     if (tiles_m * tiles_n <= cus || r == 0 || r % tiles_n || 4 * r > cus) return 0;

@@ -14,6 +14,9 @@
 //                activation layout 16 q negated in odd groups: every factor a power of two;
 //                y = bf16(acc * sa[m] + bias[n]) after a wavefront reduction
 //   RowScale     an int32 sum over all of K (exact), y = bf16(P * sa[m] * ws[n] + bias[n])
+//   GroupPartials / RowAcc (parity entries) write the exact int32 group partials P[g, m, n] (the
+//                two half-group chunk sums of adjacent lanes added, the x16 / sign factors of the
+//                int4 layouts undone by exact shifts) or the full-K int32 sums
 #include "mq_device.h"
 #include "mq_internal.h"
 
@@ -110,7 +113,7 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
             const uint32_t wd[4] = {cur.w[c].x, cur.w[c].y, cur.w[c].z, cur.w[c].w};
             int z = 0;
             if constexpr (WK == WKind::U4Asym) z = (cur.z[c] >> (4 * (g & 1))) & 0xf;
-            float s = 0.0f;
+            [[maybe_unused]] float s = 0.0f;
             if constexpr (EPI == Epi::GroupScale) {
                 s = f16_bits_to_f32(static_cast<uint16_t>(cur.s[c]));
                 if constexpr (WK == WKind::I4Sym) s *= 0.0625f;
@@ -134,12 +137,27 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
                     }
                 }
                 if constexpr (WK == WKind::U4Asym) d -= z * asum[m * nchunks + ch];
-                if constexpr (EPI == Epi::GroupScale) accf[c][m] = __builtin_fmaf(static_cast<float>(d), s, accf[c][m]);
-                else acci[c][m] += d;
+                if constexpr (EPI == Epi::GroupScale) {
+                    accf[c][m] = __builtin_fmaf(static_cast<float>(d), s, accf[c][m]);
+                } else if constexpr (EPI == Epi::GroupPartials) {
+                    // chunks 2g and 2g + 1 (the two halves of group g) sit in lanes 2j and 2j + 1 of
+                    // the same iteration; both lanes of a pair are active or inactive together
+                    // (the chunk count is even), so the exchange reads a live lane
+                    static_assert(kPacked, "group partials are defined for 4-bit weights");
+                    constexpr int shift = (WK == WKind::I4Sym ? 4 : 0) + (AM == 2 ? 4 : 0);
+                    int pv = (d + __shfl_xor(d, 1, 64)) >> shift;   // exact: a multiple of 2^shift
+                    if (AM == 2 && (g & 1)) pv = -pv;
+                    const int64_t n = n_base + c;
+                    if ((lane & 1) == 0 && m < a.M && n < a.N)
+                        a.part[(static_cast<int64_t>(g) * a.M + m) * a.N + n] = pv;
+                } else {
+                    acci[c][m] += d;
+                }
             }
         }
         cur = next;
     }
+    if constexpr (EPI == Epi::GroupPartials) return;
     // wavefront reductions and the epilogue (lane 0 writes)
 #pragma unroll
     for (int c = 0; c < kCols; ++c) {
@@ -157,6 +175,10 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
 #pragma unroll
                 for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
                 if constexpr (WK == WKind::I4Sym) v >>= 4;   // exact: a multiple of 16
+                if constexpr (EPI == Epi::RowAcc) {
+                    if (lane == 0 && m < a.M && n < a.N) a.part[m * a.N + n] = v;
+                    continue;
+                }
                 t = m < a.M && n < a.N ? static_cast<float>(v) * a.sa[m] * a.ws32[n] : 0.0f;
             }
             if (lane == 0 && m < a.M && n < a.N) {
@@ -205,9 +227,15 @@ int launch_gemv(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     if (epi == Epi::GroupScale) {
         if (wk == WKind::U4Asym) return launch_am<WKind::U4Asym, Epi::GroupScale>(a, stream);
         if (wk == WKind::I4Sym) return launch_am<WKind::I4Sym, Epi::GroupScale>(a, stream);
+    } else if (epi == Epi::GroupPartials) {
+        if (wk == WKind::U4Asym) return launch_am<WKind::U4Asym, Epi::GroupPartials>(a, stream);
+        if (wk == WKind::I4Sym) return launch_am<WKind::I4Sym, Epi::GroupPartials>(a, stream);
     } else if (epi == Epi::RowScale) {
         if (wk == WKind::I4Sym) return launch_rows<WKind::I4Sym, Epi::RowScale, 0>(a, stream);
         if (wk == WKind::I8) return launch_rows<WKind::I8, Epi::RowScale, 0>(a, stream);
+    } else if (epi == Epi::RowAcc) {
+        if (wk == WKind::I4Sym) return launch_rows<WKind::I4Sym, Epi::RowAcc, 0>(a, stream);
+        if (wk == WKind::I8) return launch_rows<WKind::I8, Epi::RowAcc, 0>(a, stream);
     }
     set_error("gemv: unsupported weight kind / epilogue combination");
     return -2;

@@ -16,6 +16,11 @@ void clear_error();
 // Translates the HIP launch status into the ABI status and message.
 int launch_status(const char* what);
 
+// Compute units of the current device (0 if the runtime cannot say). The attribute query runs
+// once per device; later calls read the cached value, so the launchers can size their grids on
+// every call without a runtime query.
+int device_cu_count();
+
 // --- rotate + quantize (mq_rotquant.hip)
 int launch_rotquant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits,
                     int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);

@@ -33,6 +33,7 @@
 #pragma once
 
 #include <algorithm>
+#include <atomic>
 
 #include "mq_device.h"
 #include "mq_silu_table.h"
@@ -321,15 +322,6 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
     }
 }
 
-// Compute units of the current device.
-inline int device_cu_count() {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-        return 256;
-    return n;
-}
-
 template <int BLK, int OUT, int NCH, int ACT, int W>
 int launch_rq(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, void* q, int64_t ldq, float* scale,
               hipStream_t stream) {
@@ -340,13 +332,21 @@ int launch_rq(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, void* q, int
     if constexpr (ACT == 1) {
         // as many workgroups as are resident at once (the same number on every CU), each
         // striding over the row groups
-        int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &per_cu, reinterpret_cast<const void*>(&rotquant_kernel<BLK, OUT, NCH, ACT, W>), 64 * kWaves, 0) !=
-                hipSuccess ||
-            per_cu <= 0)
-            per_cu = 1;
-        wgs = std::min<int64_t>(groups, static_cast<int64_t>(device_cu_count()) * per_cu);
+        // resident workgroups per CU of this instantiation: queried once (every device this
+        // library runs on is a gfx950 with the same per-CU resources)
+        static std::atomic<int> per_cu_cache{0};
+        int per_cu = per_cu_cache.load(std::memory_order_relaxed);
+        if (per_cu <= 0) {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                    &per_cu, reinterpret_cast<const void*>(&rotquant_kernel<BLK, OUT, NCH, ACT, W>), 64 * kWaves,
+                    0) != hipSuccess ||
+                per_cu <= 0)
+                per_cu = 1;
+            else
+                per_cu_cache.store(per_cu, std::memory_order_relaxed);
+        }
+        const int cus = device_cu_count();
+        wgs = std::min<int64_t>(groups, static_cast<int64_t>(cus > 0 ? cus : 256) * per_cu);
     }
     if (wgs == 0) return 0;
     hipLaunchKernelGGL((rotquant_kernel<BLK, OUT, NCH, ACT, W>), dim3(static_cast<unsigned>(wgs)),

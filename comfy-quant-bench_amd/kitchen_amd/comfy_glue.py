@@ -141,7 +141,10 @@ def layer_linear(tensors: dict, layer: str, config: dict, compile_safe: bool = F
         return lambda x, bias=None, out_dtype=torch.bfloat16: lin["w4a8_int8_linear"](
             x, w, s_rel, s_ch, cb, None, bias, group_size=gs, convrot_groupsize=cg, out_dtype=out_dtype)
     if fmt == "int8_tensorwise":
-        convrot = bool(config.get("convrot", cg > 0))
+        # a missing "convrot" key means no rotation: quant_int8.py --no-convrot writes neither key
+        # (tools/_formats.py:150-152) and the loader reads layer_conf.get("convrot", False)
+        # (tools/verify_w4a4.py:313-315,338)
+        convrot = bool(config.get("convrot", False))
         return lambda x, bias=None, out_dtype=torch.bfloat16, input_act=None: lin["int8_linear"](
             x, w, scale, bias, out_dtype, convrot, cg if cg else 256, input_act)
     raise NotImplementedError(f"{layer}: format {fmt!r} is not on this path")

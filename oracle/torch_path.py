@@ -40,13 +40,16 @@ class W4A8CpuLinear:
         return y.to(torch.bfloat16)
 
 
-def time_cpu(fn, x, runs: int = 5) -> float:
-    """Median seconds of `runs` calls after one warm-up."""
+def time_cpu(fn, x, runs: int = 5, min_seconds: float = 0.0) -> tuple[float, int]:
+    """(median seconds per call, calls timed): at least `runs` calls after one warm-up, and more
+    until `min_seconds` of timed work have run."""
     fn(x)
     ts = []
-    for _ in range(runs):
+    total = 0.0
+    while len(ts) < runs or total < min_seconds:
         t0 = time.perf_counter()
         fn(x)
         ts.append(time.perf_counter() - t0)
+        total += ts[-1]
     ts.sort()
-    return ts[len(ts) // 2]
+    return ts[len(ts) // 2], len(ts)

@@ -73,6 +73,17 @@ def test_layer_linear_maps_each_format(record):
     G.layer_linear(i8, "l", {"format": "int8_tensorwise", "convrot": False, "convrot_groupsize": 0})(x)
     name, a, k = record[-1]
     assert name == "int8_linear" and a[5] is False
+    # quant_int8.py --no-convrot writes neither "convrot" nor "convrot_groupsize"
+    # (tools/_formats.py:148-152): absence means no rotation (tools/verify_w4a4.py:313-315,338)
+    G.layer_linear(i8, "l", {"format": "int8_tensorwise"})(x)
+    name, a, k = record[-1]
+    assert name == "int8_linear" and a[5] is False
+    G.layer_linear(i8, "l", {"format": "int8_tensorwise", "convrot": True})(x)
+    name, a, k = record[-1]
+    assert a[5] is True and a[6] == 256
+    G.layer_linear(i8, "l", {"format": "int8_tensorwise", "convrot": True, "convrot_groupsize": 64})(x)
+    name, a, k = record[-1]
+    assert a[5] is True and a[6] == 64
     with pytest.raises(NotImplementedError):
         G.layer_linear(i8, "l", {"format": "nvfp4"})
     with pytest.raises(KeyError):

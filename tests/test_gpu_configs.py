@@ -75,19 +75,39 @@ def test_config1_adaln_m1(gpu_device):
 @pytest.mark.parametrize("hb", [16, 64, 256])
 @pytest.mark.parametrize("k,n", C1_KN)
 def test_config2_w4a4_shapes(gpu_device, k, n, hb):
-    m = 4352
-    print(f"[config2] w4a4 H{hb} M={m} K={k} N={n}", flush=True)
     qw, s16 = ck.quantize_w4a4_group_weight(torch.from_numpy(synth.weight(n, k, seed=k + n + hb)).to(gpu_device),
                                             64, hb)
-    xb = synth.activations(m, k, seed=m + hb, spike_frac=0.001)
     bias = _bias(n, hb)
+    for m in (4352, 8192):
+        print(f"[config2] w4a4 H{hb} M={m} K={k} N={n}", flush=True)
+        xb = synth.activations(m, k, seed=m + hb, spike_frac=0.001)
+        y = ck.convrot_w4a4_linear(synth.to_bf16_tensor(xb, gpu_device), qw, s16,
+                                   torch.from_numpy(bias).to(gpu_device), convrot_groupsize=hb)
+        torch.cuda.synchronize()
+        assert torch.isfinite(y).all()
+        rows = _rows(m)
+        ref = _ref_w4a4(synth.bf16_bits_to_f32(xb[rows]), qw, s16, bias, hb)
+        err = gemm.rel_l2(ref, y.float().cpu().numpy()[rows])
+        print(f"[config2] rel L2 {err:.2e}", flush=True)
+        assert err < 4e-3
+        del y
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("hb", [16, 64, 256])
+def test_config2_adaln_m1(gpu_device, hb):
+    """Config 2 on config 1's M = 1 adaLN shape (3072 -> 18432): the few-row kernel with int4
+    activations in the group GEMM's x16 layout."""
+    k, n = 3072, 18432
+    print(f"[config2] w4a4 adaLN H{hb} M=1 K={k} N={n}", flush=True)
+    qw, s16 = ck.quantize_w4a4_group_weight(torch.from_numpy(synth.weight(n, k, seed=12 + hb)).to(gpu_device), 64, hb)
+    xb = synth.activations(1, k, seed=13 + hb)
+    bias = _bias(n, 14 + hb)
     y = ck.convrot_w4a4_linear(synth.to_bf16_tensor(xb, gpu_device), qw, s16, torch.from_numpy(bias).to(gpu_device),
                                convrot_groupsize=hb)
     torch.cuda.synchronize()
-    assert torch.isfinite(y).all()
-    rows = _rows(m)
-    ref = _ref_w4a4(synth.bf16_bits_to_f32(xb[rows]), qw, s16, bias, hb)
-    err = gemm.rel_l2(ref, y.float().cpu().numpy()[rows])
+    ref = _ref_w4a4(synth.bf16_bits_to_f32(xb), qw, s16, bias, hb)
+    err = gemm.rel_l2(ref, y.float().cpu().numpy())
     print(f"[config2] rel L2 {err:.2e}", flush=True)
     assert err < 4e-3
 
