@@ -18,7 +18,9 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "kitchen_amd", "libmq.so")
-SOURCES = ["mq_abi.hip", "mq_rotquant.hip", "mq_swiglu.hip", "mq_codebook.hip", "mq_wquant.hip", "mq_gemv.hip", "mq_gemm.hip", "mq_gemm_wide.hip"]
+SOURCES = ["mq_abi.hip", "mq_rotquant.hip", "mq_rotquant_f16.hip", "mq_rotquant_f32.hip", "mq_swiglu.hip",
+           "mq_swiglu_f16.hip",
+           "mq_codebook.hip", "mq_wquant.hip", "mq_gemv.hip", "mq_gemm.hip", "mq_gemm_wide.hip"]
 ARCH = "gfx950"
 
 
@@ -64,9 +66,10 @@ def build(verbose: bool = False) -> str:
     """Compile every source (in parallel) and link libmq.so; returns its path. Always recompiles."""
     build_dir = os.path.join(HERE, "_build")
     os.makedirs(os.path.join(build_dir, "gen"), exist_ok=True)
-    # generated constant table: correctly rounded fp32 silu of the bf16 gates (SwiGLU prologue)
+    # generated constant tables: correctly rounded fp32 silu of the bf16 and fp16 gates (SwiGLU prologue)
     subprocess.run([sys.executable, os.path.join(CSRC, "gen_silu_table.py"),
-                    os.path.join(build_dir, "gen", "mq_silu_table.h")], check=True)
+                    os.path.join(build_dir, "gen", "mq_silu_table.h"),
+                    os.path.join(build_dir, "gen", "mq_silu_f16_table.h")], check=True)
     workers = max(1, min(len(SOURCES), os.cpu_count() or 1))
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
         objs = list(pool.map(lambda src: _compile(src, build_dir, verbose), SOURCES))

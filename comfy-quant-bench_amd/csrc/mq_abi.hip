@@ -62,6 +62,20 @@ namespace {
 
 constexpr int kEmpty = 1;   // check_gemm_common: valid shape with nothing to compute
 
+int dtype_bytes(int dt) { return dt == MQ_DT_F32 ? 4 : 2; }
+
+// Output and bias checks shared by the GEMM entry points: types, alignment and the row stride.
+int check_gemm_out(const char* what, const void* bias, int bias_dtype, const void* y, int y_dtype, int64_t ldy,
+                   int64_t N) {
+    MQ_REQUIRE(y_dtype >= MQ_DT_BF16 && y_dtype <= MQ_DT_F32, "%s: unknown output type %d", what, y_dtype);
+    MQ_REQUIRE(!bias || (bias_dtype >= MQ_DT_BF16 && bias_dtype <= MQ_DT_F32), "%s: unknown bias type %d", what,
+               bias_dtype);
+    MQ_REQUIRE(y && aligned(y, dtype_bytes(y_dtype)), "%s: y must be non-null and aligned to its element size", what);
+    MQ_REQUIRE(!bias || aligned(bias, dtype_bytes(bias_dtype)), "%s: bias must be aligned to its element size", what);
+    MQ_REQUIRE(ldy >= N, "%s: ldy < N", what);
+    return MQ_OK;
+}
+
 int check_gemm_common(const int8_t* qa, int64_t lda, const void* qw, int64_t ldw, int64_t M, int64_t N,
                       int64_t K, int64_t wbytes_per_row) {
     MQ_REQUIRE(M >= 0 && N >= 0 && K > 0, "gemm: bad shape M=%lld N=%lld K=%lld", (long long)M,
@@ -91,10 +105,13 @@ const char* mq_last_error(void) { return g_err; }
 
 namespace {
 
-// Argument checks shared by mq_rotquant and mq_swiglu_rotquant; x holds `cols` bf16 values per
+// Argument checks shared by mq_rotquant and mq_swiglu_rotquant; x holds `cols` 16-bit values per
 // row (K, or 2K for gate | up).
-int check_rotquant(const char* what, const void* x, int64_t M, int64_t K, int64_t cols, int64_t ldx, int hblock,
-                   int bits, int packed, const void* q, int64_t ldq, const float* scale) {
+int check_rotquant(const char* what, const void* x, int x_dtype, bool f32_ok, int64_t M, int64_t K, int64_t cols,
+                   int64_t ldx, int hblock, int bits, int packed, const void* q, int64_t ldq, const float* scale) {
+    MQ_REQUIRE(x_dtype == MQ_DT_BF16 || x_dtype == MQ_DT_F16 || (f32_ok && x_dtype == MQ_DT_F32),
+               "%s: input type must be bf16 (%d), fp16 (%d)%s, got %d", what, MQ_DT_BF16, MQ_DT_F16,
+               f32_ok ? " or fp32 (2)" : "", x_dtype);
     MQ_REQUIRE(M >= 0 && K > 0, "%s: bad shape M=%lld K=%lld", what, (long long)M, (long long)K);
     MQ_REQUIRE(M < (int64_t(1) << 31), "%s: M too large", what);
     MQ_REQUIRE(bits == 8 || bits == 4, "%s: bits must be 8 or 4 (got %d)", what, bits);
@@ -111,8 +128,10 @@ int check_rotquant(const char* what, const void* x, int64_t M, int64_t K, int64_
     }
     if (M == 0) return MQ_OK;
     MQ_REQUIRE(x && q && scale, "%s: null pointer", what);
-    MQ_REQUIRE(ldx >= cols && ldx % 8 == 0 && aligned(x, 16),
-               "%s: x needs ldx >= %lld, ldx %% 8 == 0, 16-byte aligned base", what, (long long)cols);
+    const int64_t per16 = x_dtype == MQ_DT_F32 ? 4 : 8;   // elements per 16 bytes
+    MQ_REQUIRE(ldx >= cols && ldx % per16 == 0 && aligned(x, 16),
+               "%s: x needs ldx >= %lld, ldx %% %lld == 0, 16-byte aligned base", what, (long long)cols,
+               (long long)per16);
     const int64_t row_bytes = packed == MQ_Q_PACKED ? K / 2 : K;
     const int64_t qalign = packed == MQ_Q_PACKED ? 8 : 16;
     MQ_REQUIRE(ldq >= row_bytes && ldq % qalign == 0 && aligned(q, qalign),
@@ -126,22 +145,30 @@ int check_rotquant(const char* what, const void* x, int64_t M, int64_t K, int64_
 
 extern "C" {
 
-int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits, int packed, void* q,
-                int64_t ldq, float* scale, void* stream) {
+int mq_rotquant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int hblock, int bits, int packed,
+                void* q, int64_t ldq, float* scale, void* stream) {
     clear_error();
-    const int rc = check_rotquant("rotquant", x, M, K, K, ldx, hblock, bits, packed, q, ldq, scale);
+    const int rc = check_rotquant("rotquant", x, x_dtype, true, M, K, K, ldx, hblock, bits, packed, q, ldq, scale);
     if (rc != MQ_OK || M == 0) return rc;
-    return launch_rotquant(static_cast<const uint16_t*>(x), M, K, ldx, hblock, bits, packed, q, ldq, scale,
-                           static_cast<hipStream_t>(stream));
+    auto* xs = static_cast<const uint16_t*>(x);
+    auto* st = static_cast<hipStream_t>(stream);
+    if (x_dtype == MQ_DT_F32)
+        return launch_rotquant_f32(static_cast<const float*>(x), M, K, ldx, hblock, bits, packed, q, ldq, scale, st);
+    return x_dtype == MQ_DT_F16 ? launch_rotquant_f16(xs, M, K, ldx, hblock, bits, packed, q, ldq, scale, st)
+                                : launch_rotquant_bf16(xs, M, K, ldx, hblock, bits, packed, q, ldq, scale, st);
 }
 
-int mq_swiglu_rotquant(const void* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits, int packed,
-                       void* q, int64_t ldq, float* scale, void* stream) {
+int mq_swiglu_rotquant(const void* h, int h_dtype, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
+                       int packed, void* q, int64_t ldq, float* scale, void* stream) {
     clear_error();
-    const int rc = check_rotquant("swiglu_rotquant", h, M, K, 2 * K, ldh, hblock, bits, packed, q, ldq, scale);
+    const int rc =
+        check_rotquant("swiglu_rotquant", h, h_dtype, false, M, K, 2 * K, ldh, hblock, bits, packed, q, ldq, scale);
     if (rc != MQ_OK || M == 0) return rc;
-    return launch_swiglu_rotquant(static_cast<const uint16_t*>(h), M, K, ldh, hblock, bits, packed, q, ldq, scale,
-                                  static_cast<hipStream_t>(stream));
+    auto* hs = static_cast<const uint16_t*>(h);
+    auto* st = static_cast<hipStream_t>(stream);
+    return h_dtype == MQ_DT_F16
+               ? launch_swiglu_rotquant_f16(hs, M, K, ldh, hblock, bits, packed, q, ldq, scale, st)
+               : launch_swiglu_rotquant_bf16(hs, M, K, ldh, hblock, bits, packed, q, ldq, scale, st);
 }
 
 int mq_decode_w4a8_codebook(const void* qdata, int64_t ldq, const void* s_rel, int64_t lds, const float* s_channel,
@@ -206,22 +233,24 @@ int mq_quantize_weight(const void* w, int dtype, int64_t N, int64_t K, int64_t l
 
 int mq_gemm_w4_group_ws(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
                         const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
-                        const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
-                        void* workspace, int64_t workspace_bytes, void* stream) {
+                        const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy, int64_t M, int64_t N,
+                        int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
     clear_error();
     MQ_REQUIRE(group == 64, "gemm_w4_group: quant group size must be 64 (got %d)", group);
     MQ_REQUIRE(act_mode >= MQ_ACT_I8 && act_mode <= MQ_ACT_X16ALT, "gemm_w4_group: unknown act_mode %d", act_mode);
     int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, K / 2);
     if (rc) return rc == kEmpty ? MQ_OK : rc;
-    MQ_REQUIRE(sa && ws && y, "gemm_w4_group: null pointer");
+    MQ_REQUIRE(sa && ws, "gemm_w4_group: null pointer");
+    rc = check_gemm_out("gemm_w4_group", bias, bias_dtype, y, y_dtype, ldy, N);
+    if (rc) return rc;
     MQ_REQUIRE(ldws >= K / group, "gemm_w4_group: ldws < K/group");
     MQ_REQUIRE(!wz || ldwz >= (K / group + 1) / 2, "gemm_w4_group: ldwz < ceil(K/group/2)");
-    MQ_REQUIRE(ldy >= N, "gemm_w4_group: ldy < N");
     MQ_REQUIRE(workspace_bytes >= 0 && (!workspace || aligned(workspace, 16)),
                "gemm_w4_group: workspace must be 16-byte aligned");
     GemmArgs a{};
     a.qa = qa; a.lda = lda; a.sa = sa; a.qw = qw; a.ldw = ldw; a.ws16 = ws; a.ldws = ldws;
-    a.wz = wz; a.ldwz = ldwz; a.bias = bias; a.y = y; a.ldy = ldy; a.M = M; a.N = N; a.K = K;
+    a.wz = wz; a.ldwz = ldwz; a.bias = bias; a.bias_dtype = bias_dtype; a.y = y; a.y_dtype = y_dtype; a.ldy = ldy;
+    a.M = M; a.N = N; a.K = K;
     a.act_mode = act_mode;
     a.work = workspace; a.work_bytes = workspace ? workspace_bytes : 0;
     return launch_gemm(a, wz ? WKind::U4Asym : WKind::I4Sym, Epi::GroupScale, static_cast<hipStream_t>(stream));
@@ -229,10 +258,10 @@ int mq_gemm_w4_group_ws(const int8_t* qa, int64_t lda, const float* sa, const ui
 
 int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
                      const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
-                     const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
-                     void* stream) {
-    return mq_gemm_w4_group_ws(qa, lda, sa, qw, ldw, ws, ldws, wz, ldwz, group, act_mode, bias, y, ldy, M, N, K,
-                               nullptr, 0, stream);
+                     const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy, int64_t M, int64_t N,
+                     int64_t K, void* stream) {
+    return mq_gemm_w4_group_ws(qa, lda, sa, qw, ldw, ws, ldws, wz, ldwz, group, act_mode, bias, bias_dtype, y,
+                               y_dtype, ldy, M, N, K, nullptr, 0, stream);
 }
 
 int mq_gemm_w4_group_partials(const int8_t* qa, int64_t lda, const uint8_t* qw, int64_t ldw, const uint8_t* wz,
@@ -253,27 +282,29 @@ int mq_gemm_w4_group_partials(const int8_t* qa, int64_t lda, const uint8_t* qw, 
 }
 
 int mq_gemm_rowscale_ws(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw, int wbits,
-                        const float* ws, const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N,
-                        int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
+                        const float* ws, const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy,
+                        int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
     clear_error();
     MQ_REQUIRE(wbits == 4 || wbits == 8, "gemm_rowscale: wbits must be 4 or 8 (got %d)", wbits);
     int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, wbits == 4 ? K / 2 : K);
     if (rc) return rc == kEmpty ? MQ_OK : rc;
-    MQ_REQUIRE(sa && ws && y, "gemm_rowscale: null pointer");
-    MQ_REQUIRE(ldy >= N, "gemm_rowscale: ldy < N");
+    MQ_REQUIRE(sa && ws, "gemm_rowscale: null pointer");
+    rc = check_gemm_out("gemm_rowscale", bias, bias_dtype, y, y_dtype, ldy, N);
+    if (rc) return rc;
     MQ_REQUIRE(workspace_bytes >= 0 && (!workspace || aligned(workspace, 16)),
                "gemm_rowscale: workspace must be 16-byte aligned");
     GemmArgs a{};
     a.qa = qa; a.lda = lda; a.sa = sa; a.qw = static_cast<const uint8_t*>(qw); a.ldw = ldw; a.ws32 = ws;
-    a.bias = bias; a.y = y; a.ldy = ldy; a.M = M; a.N = N; a.K = K;
+    a.bias = bias; a.bias_dtype = bias_dtype; a.y = y; a.y_dtype = y_dtype; a.ldy = ldy; a.M = M; a.N = N; a.K = K;
     a.work = workspace; a.work_bytes = workspace ? workspace_bytes : 0;
     return launch_gemm(a, wbits == 4 ? WKind::I4Sym : WKind::I8, Epi::RowScale, static_cast<hipStream_t>(stream));
 }
 
 int mq_gemm_rowscale(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw, int wbits,
-                     const float* ws, const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N,
-                     int64_t K, void* stream) {
-    return mq_gemm_rowscale_ws(qa, lda, sa, qw, ldw, wbits, ws, bias, y, ldy, M, N, K, nullptr, 0, stream);
+                     const float* ws, const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy,
+                     int64_t M, int64_t N, int64_t K, void* stream) {
+    return mq_gemm_rowscale_ws(qa, lda, sa, qw, ldw, wbits, ws, bias, bias_dtype, y, y_dtype, ldy, M, N, K, nullptr,
+                               0, stream);
 }
 
 int64_t mq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {

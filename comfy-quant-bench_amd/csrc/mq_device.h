@@ -24,6 +24,37 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
 
+// Floating-point operand types chosen by the caller (MQ_DT_* of include/mq.h).
+constexpr int kDtBf16 = 0, kDtF16 = 1, kDtF32 = 2;
+
+// Element i of a vector of type dt, as fp32 (exact for every type).
+__device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
+    if (dt == kDtF32) return static_cast<const float*>(p)[i];
+    const uint16_t h = static_cast<const uint16_t*>(p)[i];
+    return dt == kDtF16 ? f16_bits_to_f32(h) : __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+typedef float mq_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 mq_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 mq_f16x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 values rounded (to nearest, ties to even) to the 16-bit type dt (bf16 or fp16) and
+// packed: v0 in bits 0-15, v1 in bits 16-31.
+__device__ __forceinline__ uint32_t pack_16x2(float v0, float v1, int dt) {
+    const mq_f32x2 v = {v0, v1};
+    if (dt == kDtF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, mq_f16x2));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, mq_bf16x2));
+}
+
+// Store v rounded to type dt at element i of p.
+__device__ __forceinline__ void store_from_f32(void* p, int dt, int64_t i, float v) {
+    if (dt == kDtF32) {
+        static_cast<float*>(p)[i] = v;
+        return;
+    }
+    static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(pack_16x2(v, 0.0f, dt) & 0xffffu);
+}
+
 // v_mov_b32 with a DPP source: every lane reads `src` from the lane the control selects.
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float src) {

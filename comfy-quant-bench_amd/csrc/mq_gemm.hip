@@ -13,10 +13,11 @@
 //
 // Epilogues:
 //   GroupScale    acc[m,n] += float(P_g[m,n]) * ws[n,g] after every group; at the end
-//                 y = bf16(acc * sa[m] + bias[n])      (g64_bench6.py:50-68 order of scales).
+//                 y = T(acc * sa[m] + bias[n])      (g64_bench6.py:50-68 order of scales; T is
+//                 the output type, bf16, fp16 or fp32).
 //                 Activation layout 2 (16 * q, negated in odd groups) is undone through the scale.
 //   GroupPartials writes P_g[m,n] (int32) for every group (parity entry)
-//   RowScale      one int32 accumulator over all of K; y = bf16(P * sa[m] * ws[n] + bias[n])
+//   RowScale      one int32 accumulator over all of K; y = T(P * sa[m] * ws[n] + bias[n])
 //                 (policy 0 of experiments/qwen21-kernel/kernels/g64_gemm6.cu:5)
 //   RowAcc        writes the full-K int32 accumulator (parity entry)
 #include "mq_device.h"
@@ -217,7 +218,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
                     if (row < M) a.part[row * N + col] = p[i][j][r];
                 }
             } else {
-                const float bias = a.bias ? __uint_as_float(static_cast<uint32_t>(a.bias[col]) << 16) : 0.0f;
+                const float bias = a.bias ? load_as_f32(a.bias, a.bias_dtype, col) : 0.0f;
                 const float wsc = EPI == Epi::RowScale ? a.ws32[col] : 1.0f;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
@@ -228,7 +229,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
                         v = static_cast<float>(p[i][j][r]) * a.sa[row] * wsc + bias;
                     else
                         v = acc[i][j][r] * a.sa[row] + bias;
-                    a.y[row * a.ldy + col] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+                    store_from_f32(a.y, a.y_dtype, row * a.ldy + col, v);
                 }
             }
         }
@@ -285,7 +286,7 @@ int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
                 t.M = tail;
                 t.qa = a.qa + (a.M - tail) * a.lda;
                 t.sa = a.sa + (a.M - tail);
-                t.y = a.y + (a.M - tail) * a.ldy;
+                t.y = static_cast<char*>(a.y) + (a.M - tail) * a.ldy * (a.y_dtype == kDtF32 ? 4 : 2);
                 t.ksplit = choose_ksplit(t.M, t.N, t.K, t.work_bytes, &t.kgroups);
                 if (t.ksplit > 1) {
                     w.M = a.M - tail;

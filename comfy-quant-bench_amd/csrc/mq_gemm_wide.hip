@@ -56,7 +56,6 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float f2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 
 constexpr int TM = 256, TN = 256, TK = 64;
 constexpr int NT = 512;                   // threads per workgroup
@@ -71,7 +70,7 @@ constexpr int A_LDS = 0;
 constexpr int B_LDS = A_LDS + NSTAGE * TILE_BYTES;        // 65536
 constexpr int S_LDS = B_LDS + NSTAGE * TILE_BYTES;        // 131072: fp32 scales, 1 KB per stage
 constexpr int PIPE_END = S_LDS + NSTAGE * TN * 4;         // 135168
-constexpr int OROW = 136;                                 // bf16 pitch of the output staging rows
+constexpr int OROW = 136;                                 // 16-bit pitch of the output staging rows
 constexpr int OUT_END = 8 * 64 * OROW * 2;                // 139264
 constexpr int C_LDS = PIPE_END > OUT_END ? PIPE_END : OUT_END;   // per-column offset correction
 constexpr int SMEM_BYTES = C_LDS + TN * 4;
@@ -556,7 +555,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         return;
     }
 
-    // ---- output epilogue: scale, bias, bf16, staged through LDS for 16-byte row stores
+    // ---- output epilogue: scale, bias, rounding to the output type; 16-bit types are staged through
+    // LDS for 16-byte row stores
     __syncthreads();   // every wave is done with the pipeline stages the staging area reuses
     if constexpr (EPI == Epi::GroupScale) {
         const float cs_row = cs + __shfl_xor(cs, 1, 64);   // the two threads of the row
@@ -595,7 +595,30 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         const bool ok = col < N;
         if constexpr (EPI == Epi::GroupScale) colv[j] = lds<float>(smem, C_LDS + 4 * lc);
         else colv[j] = ok ? a.ws32[col] : 0.0f;
-        biasv[j] = (ok && a.bias) ? __uint_as_float(static_cast<uint32_t>(a.bias[col]) << 16) : 0.0f;
+        biasv[j] = (ok && a.bias) ? load_as_f32(a.bias, a.bias_dtype, col) : 0.0f;
+    }
+    // y[m, n] in fp32 before the rounding to the output type
+    auto out_value = [&](int i, int j, int r, float sa_r) {
+        if constexpr (EPI == Epi::GroupScale) return __builtin_fmaf(acc[i][j][r] - colv[j], sa_r, biasv[j]);
+        else return static_cast<float>(acci[i][j][r]) * sa_r * colv[j] + biasv[j];
+    };
+    if (a.y_dtype == kDtF32) {
+        // fp32 outputs straight from the registers: the 16 lanes of a row segment write 64
+        // consecutive bytes
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
+                if (row >= M) continue;
+                const float sa_r = a.sa[row];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int64_t col = n0 + wn * 128 + j * 16 + fr;
+                    if (col < N) static_cast<float*>(a.y)[row * a.ldy + col] = out_value(i, j, r, sa_r);
+                }
+            }
+        return;
     }
     uint16_t* stage = reinterpret_cast<uint16_t*>(smem) + wave * 64 * OROW;
 #pragma unroll
@@ -610,18 +633,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             const int lc = j * 16 + fr;
 #pragma unroll
             for (int r = 0; r < 4; r += 2) {
-                f2 v;
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    float t;
-                    if constexpr (EPI == Epi::GroupScale)
-                        t = __builtin_fmaf(acc[i][j][r + e] - colv[j], sav[r + e], biasv[j]);
-                    else
-                        t = static_cast<float>(acci[i][j][r + e]) * sav[r + e] * colv[j] + biasv[j];
-                    v[e] = t;
-                }
-                const bf2 h = __builtin_convertvector(v, bf2);
-                const uint32_t hb = __builtin_bit_cast(uint32_t, h);
+                const uint32_t hb = pack_16x2(out_value(i, j, r, sav[r]), out_value(i, j, r + 1, sav[r + 1]), a.y_dtype);
                 stage[(lr0 + r) * OROW + lc] = static_cast<uint16_t>(hb & 0xffffu);
                 stage[(lr0 + r + 1) * OROW + lc] = static_cast<uint16_t>(hb >> 16);
             }
@@ -629,7 +641,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     }
     __syncthreads();
     const int64_t col0 = n0 + wn * 128;
-    const bool vec_ok = (a.ldy % 8) == 0;
+    const bool vec_ok = (a.ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
 #pragma unroll 4
     for (int it = 0; it < 16; ++it) {
         const int c = it * 64 + lane;
@@ -638,7 +650,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         const int64_t col = col0 + ch * 8;
         if (row >= M || col >= N) continue;
         const uint4 v = *reinterpret_cast<const uint4*>(&stage[lr * OROW + ch * 8]);
-        uint16_t* dst = a.y + row * a.ldy + col;
+        uint16_t* dst = static_cast<uint16_t*>(a.y) + row * a.ldy + col;
         if (vec_ok && col + 8 <= N) {
             *reinterpret_cast<uint4*>(dst) = v;
         } else {
@@ -650,8 +662,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     }
 }
 
-// y[m, n] = bf16(sum_s part[s][m][n] * sa[m] + bias[n]) (GroupScale: fp32 partials) or
-// bf16(float(sum_s part[s][m][n]) * sa[m] * ws[n] + bias[n]) (RowScale: int32 partials, the
+// y[m, n] = T(sum_s part[s][m][n] * sa[m] + bias[n]) (GroupScale: fp32 partials) or
+// T(float(sum_s part[s][m][n]) * sa[m] * ws[n] + bias[n]) (RowScale: int32 partials, the
 // non-split epilogue's arithmetic on the exact full-K sum). 8 consecutive columns per thread.
 template <bool INT>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a) {
@@ -691,16 +703,25 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) t[e] = sum[e] * a.sa[row];
     }
-    uint32_t out[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        if (col0 + e >= N) break;
-        float v = t[e];
-        if (a.bias) v += __uint_as_float(static_cast<uint32_t>(a.bias[col0 + e]) << 16);
-        out[e >> 1] |= f32_to_bf16_bits(v) << (16 * (e & 1));
+    for (int e = 0; e < 8; ++e)
+        if (a.bias && col0 + e < N) t[e] += load_as_f32(a.bias, a.bias_dtype, col0 + e);
+    const bool vec = col0 + 8 <= N;
+    if (a.y_dtype == kDtF32) {
+        float* dst = static_cast<float*>(a.y) + row * a.ldy + col0;
+        if (vec && a.ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0) {
+            *reinterpret_cast<float4*>(dst) = float4{t[0], t[1], t[2], t[3]};
+            *reinterpret_cast<float4*>(dst + 4) = float4{t[4], t[5], t[6], t[7]};
+        } else {
+            for (int e = 0; e < 8 && col0 + e < N; ++e) dst[e] = t[e];
+        }
+        return;
     }
-    uint16_t* dst = a.y + row * a.ldy + col0;
-    if (col0 + 8 <= N && a.ldy % 8 == 0) {
+    uint32_t out[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = pack_16x2(t[2 * e], t[2 * e + 1], a.y_dtype);
+    uint16_t* dst = static_cast<uint16_t*>(a.y) + row * a.ldy + col0;
+    if (vec && a.ldy % 8 == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0) {
         *reinterpret_cast<uint4*>(dst) = uint4{out[0], out[1], out[2], out[3]};
     } else {
         for (int e = 0; e < 8 && col0 + e < N; ++e) dst[e] = static_cast<uint16_t>(out[e >> 1] >> (16 * (e & 1)));

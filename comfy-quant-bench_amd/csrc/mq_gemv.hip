@@ -12,8 +12,8 @@
 //   int4 sym     the nibble is moved to the top of its byte (16 v), so D = 16 sum a v
 //   GroupScale   acc += s[n, g] * D * f in fp32, f = 1/16 (int4 sym) times (-1)^g / 16 for the
 //                activation layout 16 q negated in odd groups: every factor a power of two;
-//                y = bf16(acc * sa[m] + bias[n]) after a wavefront reduction
-//   RowScale     an int32 sum over all of K (exact), y = bf16(P * sa[m] * ws[n] + bias[n])
+//                y = T(acc * sa[m] + bias[n]) after a wavefront reduction (T: the output type)
+//   RowScale     an int32 sum over all of K (exact), y = T(P * sa[m] * ws[n] + bias[n])
 //   GroupPartials / RowAcc (parity entries) write the exact int32 group partials P[g, m, n] (the
 //                two half-group chunk sums of adjacent lanes added, the x16 / sign factors of the
 //                int4 layouts undone by exact shifts) or the full-K int32 sums
@@ -182,8 +182,8 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
                 t = m < a.M && n < a.N ? static_cast<float>(v) * a.sa[m] * a.ws32[n] : 0.0f;
             }
             if (lane == 0 && m < a.M && n < a.N) {
-                if (a.bias) t += __uint_as_float(static_cast<uint32_t>(a.bias[n]) << 16);
-                a.y[m * a.ldy + n] = static_cast<uint16_t>(f32_to_bf16_bits(t));
+                if (a.bias) t += load_as_f32(a.bias, a.bias_dtype, n);
+                store_from_f32(a.y, a.y_dtype, m * a.ldy + n, t);
             }
         }
     }

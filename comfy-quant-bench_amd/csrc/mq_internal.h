@@ -21,13 +21,19 @@ int launch_status(const char* what);
 // every call without a runtime query.
 int device_cu_count();
 
-// --- rotate + quantize (mq_rotquant.hip)
-int launch_rotquant(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits,
-                    int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
+// --- rotate + quantize (mq_rotquant*.hip), one launcher per input type
+int launch_rotquant_bf16(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits,
+                         int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
+int launch_rotquant_f16(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits,
+                        int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
+int launch_rotquant_f32(const float* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits,
+                        int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
 
-// --- SwiGLU prologue + rotate + quantize (mq_swiglu.hip); h holds gate | up, K columns each
-int launch_swiglu_rotquant(const uint16_t* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
-                           int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
+// --- SwiGLU prologue + rotate + quantize (mq_swiglu*.hip); h holds gate | up, K columns each
+int launch_swiglu_rotquant_bf16(const uint16_t* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
+                                int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
+int launch_swiglu_rotquant_f16(const uint16_t* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
+                               int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
 
 // --- load-time decode of the shipped asym_w4a8_int8 codebook weights (mq_codebook.hip)
 int launch_decode_w4a8_codebook(const uint8_t* qdata, int64_t ldq, const uint8_t* s_rel, int64_t lds,
@@ -54,9 +60,11 @@ struct GemmArgs {
     const float* ws32;      // per-row fp32 scales [N]
     const uint8_t* wz;      // packed u4 zero-points [N, ldwz]
     int64_t ldwz;
-    const uint16_t* bias;   // bf16 [N] or null
-    uint16_t* y;            // bf16 [M, ldy]
+    const void* bias;       // [N] of type bias_dtype, or null
+    void* y;                // [M, ldy] of type y_dtype
     int64_t ldy;
+    int bias_dtype;         // MQ_DT_BF16 / MQ_DT_F16 / MQ_DT_F32
+    int y_dtype;
     int32_t* part;          // int32 partials / accumulators
     int64_t M, N, K;
     int act_mode;           // group-scale GEMMs: MQ_ACT_* layout of qa (include/mq.h)

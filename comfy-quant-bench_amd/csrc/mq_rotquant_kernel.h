@@ -48,13 +48,20 @@ constexpr int kWaves = 4;                 // wavefronts per workgroup
 constexpr float kTieWindow = 0.5f - 0x1p-15f;
 
 // --- SwiGLU prologue (tools/ck_swiglu/swiglu_quant.cu:56-66): a = silu(g) * u in fp32, rounded
-// once to bf16, formed from the gate | up halves while loading. silu(g) = g / (1 + exp(-g)) is
-// taken correctly rounded to fp32: the gate is a bf16 value, so every result that is not a closed
-// form comes from a 32 KB table (mq_silu_table.h, generated with exact decimal arithmetic) that
-// each workgroup stages in LDS. Closed forms: |g| < 2^-25 gives g / 2, g >= 128 gives g and
-// g <= -128 gives -0. Then a = bf16(fp32(silu(g) * u)).
+// once to the input type, formed from the gate | up halves while loading. silu(g) = g / (1 +
+// exp(-g)) is taken correctly rounded to fp32, from tables generated with exact decimal arithmetic
+// (mq_silu_table.h). bf16 gates: every result that is not a closed form comes from a 32 KB table
+// that each workgroup stages in LDS; closed forms: |g| < 2^-25 gives g / 2, g >= 128 gives g and
+// g <= -128 gives -0. fp16 gates: a 256 KB table over all 65536 bit patterns, read from global
+// memory (cached), provided by the translation unit that instantiates the fp16 SwiGLU kernels
+// through SiluF16Table. Then a = T(fp32(silu(g) * u)) with T the input type.
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// fp32 bits of silu(g) for every fp16 bit pattern g; specialized where the table is compiled in.
+template <int IN>
+struct SiluF16Table;
 
 __device__ __forceinline__ float silu_f32(uint32_t b, float g, const float* tab) {
     const uint32_t t = b & 0x7fffu;
@@ -72,6 +79,18 @@ __device__ __forceinline__ void swiglu_pair(uint32_t wg, uint32_t wu, const floa
     const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{p0, p1}, bf16x2));
     a0 = __uint_as_float(h << 16);
     a1 = __uint_as_float(h & 0xffff0000u);
+}
+
+__device__ __forceinline__ float f16lo(uint32_t w) { return f16_bits_to_f32(static_cast<uint16_t>(w & 0xffffu)); }
+__device__ __forceinline__ float f16hi(uint32_t w) { return f16_bits_to_f32(static_cast<uint16_t>(w >> 16)); }
+
+// fp16 inputs: silu of both gates from the global fp16 table, the products rounded to fp16.
+__device__ __forceinline__ void swiglu_pair_f16(uint32_t wg, uint32_t wu, const uint32_t* tab, float& a0, float& a1) {
+    const float p0 = __uint_as_float(tab[wg & 0xffffu]) * f16lo(wu);
+    const float p1 = __uint_as_float(tab[wg >> 16]) * f16hi(wu);
+    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{p0, p1}, f16x2));
+    a0 = f16lo(h);
+    a1 = f16hi(h);
 }
 
 // Radix-4 butterflies over register bits J, J+1 (element stride 4^d mapped to register stride 2^J).
@@ -183,8 +202,9 @@ __device__ __forceinline__ void quant16(const float (&v)[16], float sg, float r,
 //          the group-scale GEMM takes for int4 activations: exact, and 16x finer in its fp32 step).
 // ACT: 0 = x is the activation itself; 1 = x holds gate | up halves of K columns each (the up
 // half starts K elements into the row) and the activation is swiglu_pair(gate, up).
+// IN: 0 = bf16 input, 1 = fp16 input (either converts exactly to fp32), 2 = fp32 input.
 // NCH: chunks per wave; W: waves per row (NCH * W * 1024 >= K).
-template <int BLK, int OUT, int NCH, int ACT, int W>
+template <int BLK, int OUT, int NCH, int ACT, int W, int IN>
 __global__ void __launch_bounds__(64 * kWaves)
 rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
                 uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale) {
@@ -194,7 +214,9 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
     const int wave = threadIdx.x >> 6;
     const int wr = wave % W;                             // this wave's share of its row
     [[maybe_unused]] const float* tab = nullptr;
-    if constexpr (ACT == 1) {
+    [[maybe_unused]] const uint32_t* tab16 = nullptr;
+    if constexpr (ACT == 1 && IN == 1) tab16 = SiluF16Table<IN>::get();
+    if constexpr (ACT == 1 && IN == 0) {
         __shared__ __attribute__((aligned(16))) uint32_t silu_lds[2 * kSiluEntries];
         for (uint32_t i = threadIdx.x; i < 2 * kSiluEntries / 4; i += 64 * kWaves)
             reinterpret_cast<uint4*>(silu_lds)[i] = reinterpret_cast<const uint4*>(kSiluTable)[i];
@@ -224,7 +246,9 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
         // row's start or from row M - 1 instead, and their values are left out of the absmax; their
         // codes are not stored. A Hadamard block lies wholly inside or outside the row (K is a
         // multiple of the block), so the rotation never mixes such values into stored ones.
-        const uint16_t* xr = x + (live ? row : static_cast<int64_t>(M) - 1) * ldx;
+        // (fp32 inputs: x and ldx count 16-bit units of the row buffer, two per element)
+        constexpr int kU = IN == 2 ? 2 : 1;
+        const uint16_t* xr = x + (live ? row : static_cast<int64_t>(M) - 1) * ldx * kU;
 
         float v[NCH][16];
         bool in[NCH];
@@ -233,6 +257,18 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
             const int e0 = (c * W + wr) * 1024 + seg_ld * 16;
             in[c] = e0 < K;
             const int e = in[c] ? e0 : 0;
+            if constexpr (IN == 2) {
+                static_assert(ACT == 0, "the SwiGLU prologue takes bf16 or fp16 inputs");
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float4 f = *reinterpret_cast<const float4*>(xr + 2 * e + 8 * j);
+                    v[c][4 * j] = f.x;
+                    v[c][4 * j + 1] = f.y;
+                    v[c][4 * j + 2] = f.z;
+                    v[c][4 * j + 3] = f.w;
+                }
+                continue;
+            }
             const uint4 a = *reinterpret_cast<const uint4*>(xr + e);
             const uint4 b = *reinterpret_cast<const uint4*>(xr + e + 8);
             const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
@@ -241,12 +277,15 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
                 const uint4 ub = *reinterpret_cast<const uint4*>(xr + K + e + 8);
                 const uint32_t wu[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
 #pragma unroll
-                for (int j = 0; j < 8; ++j) swiglu_pair(w[j], wu[j], tab, v[c][2 * j], v[c][2 * j + 1]);
+                for (int j = 0; j < 8; ++j) {
+                    if constexpr (IN == 1) swiglu_pair_f16(w[j], wu[j], tab16, v[c][2 * j], v[c][2 * j + 1]);
+                    else swiglu_pair(w[j], wu[j], tab, v[c][2 * j], v[c][2 * j + 1]);
+                }
             } else {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    v[c][2 * j] = bf16lo(w[j]);
-                    v[c][2 * j + 1] = bf16hi(w[j]);
+                    v[c][2 * j] = IN == 1 ? f16lo(w[j]) : bf16lo(w[j]);
+                    v[c][2 * j + 1] = IN == 1 ? f16hi(w[j]) : bf16hi(w[j]);
                 }
             }
         }
@@ -322,14 +361,14 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
     }
 }
 
-template <int BLK, int OUT, int NCH, int ACT, int W>
+template <int BLK, int OUT, int NCH, int ACT, int W, int IN>
 int launch_rq(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, void* q, int64_t ldq, float* scale,
               hipStream_t stream) {
     const int64_t groups = (M + kWaves / W - 1) / (kWaves / W);
     // plain inputs: one workgroup per row group; SwiGLU: a grid-stride loop over the row groups,
     // so each workgroup stages the LDS table once for many rows
     int64_t wgs = groups;
-    if constexpr (ACT == 1) {
+    if constexpr (ACT == 1 && IN == 0) {
         // as many workgroups as are resident at once (the same number on every CU), each
         // striding over the row groups
         // resident workgroups per CU of this instantiation: queried once (every device this
@@ -338,7 +377,7 @@ int launch_rq(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, void* q, int
         int per_cu = per_cu_cache.load(std::memory_order_relaxed);
         if (per_cu <= 0) {
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &per_cu, reinterpret_cast<const void*>(&rotquant_kernel<BLK, OUT, NCH, ACT, W>), 64 * kWaves,
+                    &per_cu, reinterpret_cast<const void*>(&rotquant_kernel<BLK, OUT, NCH, ACT, W, IN>), 64 * kWaves,
                     0) != hipSuccess ||
                 per_cu <= 0)
                 per_cu = 1;
@@ -349,54 +388,54 @@ int launch_rq(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, void* q, int
         wgs = std::min<int64_t>(groups, static_cast<int64_t>(cus > 0 ? cus : 256) * per_cu);
     }
     if (wgs == 0) return 0;
-    hipLaunchKernelGGL((rotquant_kernel<BLK, OUT, NCH, ACT, W>), dim3(static_cast<unsigned>(wgs)),
+    hipLaunchKernelGGL((rotquant_kernel<BLK, OUT, NCH, ACT, W, IN>), dim3(static_cast<unsigned>(wgs)),
                        dim3(64 * kWaves), 0, stream, x, ldx, static_cast<int>(M), static_cast<int>(K),
                        static_cast<uint8_t*>(q), ldq, scale);
     return launch_status("rotquant");
 }
 
-template <int BLK, int OUT, int ACT>
+template <int BLK, int OUT, int ACT, int IN>
 int dispatch_nch(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, void* q, int64_t ldq,
                  float* scale, hipStream_t stream) {
     const int chunks = static_cast<int>((K + 1023) / 1024);
     // few rows (the text-token and single-token calls): four waves per row, so the launch has
     // four times the waves and each wave a quarter of the row's latency-bound chain
     if (M <= 512 && chunks <= 8) {
-        if (chunks <= 4) return launch_rq<BLK, OUT, 1, ACT, 4>(x, M, K, ldx, q, ldq, scale, stream);
-        return launch_rq<BLK, OUT, 2, ACT, 4>(x, M, K, ldx, q, ldq, scale, stream);
+        if (chunks <= 4) return launch_rq<BLK, OUT, 1, ACT, 4, IN>(x, M, K, ldx, q, ldq, scale, stream);
+        return launch_rq<BLK, OUT, 2, ACT, 4, IN>(x, M, K, ldx, q, ldq, scale, stream);
     }
     switch (chunks) {
-        case 1: return launch_rq<BLK, OUT, 1, ACT, 1>(x, M, K, ldx, q, ldq, scale, stream);
-        case 2: return launch_rq<BLK, OUT, 2, ACT, 1>(x, M, K, ldx, q, ldq, scale, stream);
-        case 3: return launch_rq<BLK, OUT, 3, ACT, 1>(x, M, K, ldx, q, ldq, scale, stream);
-        case 4: return launch_rq<BLK, OUT, 4, ACT, 1>(x, M, K, ldx, q, ldq, scale, stream);
-        case 5: case 6: return launch_rq<BLK, OUT, 3, ACT, 2>(x, M, K, ldx, q, ldq, scale, stream);
-        case 7: case 8: return launch_rq<BLK, OUT, 4, ACT, 2>(x, M, K, ldx, q, ldq, scale, stream);
-        case 9: case 10: case 11: case 12: return launch_rq<BLK, OUT, 3, ACT, 4>(x, M, K, ldx, q, ldq, scale, stream);
-        case 13: case 14: case 15: case 16: return launch_rq<BLK, OUT, 4, ACT, 4>(x, M, K, ldx, q, ldq, scale, stream);
+        case 1: return launch_rq<BLK, OUT, 1, ACT, 1, IN>(x, M, K, ldx, q, ldq, scale, stream);
+        case 2: return launch_rq<BLK, OUT, 2, ACT, 1, IN>(x, M, K, ldx, q, ldq, scale, stream);
+        case 3: return launch_rq<BLK, OUT, 3, ACT, 1, IN>(x, M, K, ldx, q, ldq, scale, stream);
+        case 4: return launch_rq<BLK, OUT, 4, ACT, 1, IN>(x, M, K, ldx, q, ldq, scale, stream);
+        case 5: case 6: return launch_rq<BLK, OUT, 3, ACT, 2, IN>(x, M, K, ldx, q, ldq, scale, stream);
+        case 7: case 8: return launch_rq<BLK, OUT, 4, ACT, 2, IN>(x, M, K, ldx, q, ldq, scale, stream);
+        case 9: case 10: case 11: case 12: return launch_rq<BLK, OUT, 3, ACT, 4, IN>(x, M, K, ldx, q, ldq, scale, stream);
+        case 13: case 14: case 15: case 16: return launch_rq<BLK, OUT, 4, ACT, 4, IN>(x, M, K, ldx, q, ldq, scale, stream);
         default: break;
     }
     set_error("rotquant: K=%lld exceeds 16384", static_cast<long long>(K));
     return -2;
 }
 
-template <int BLK, int ACT>
+template <int BLK, int ACT, int IN>
 int dispatch_out(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int bits, int packed, void* q,
                  int64_t ldq, float* scale, hipStream_t stream) {
-    if (bits == 8) return dispatch_nch<BLK, 0, ACT>(x, M, K, ldx, q, ldq, scale, stream);
-    if (packed == 1) return dispatch_nch<BLK, 2, ACT>(x, M, K, ldx, q, ldq, scale, stream);
-    if (packed == 2) return dispatch_nch<BLK, 3, ACT>(x, M, K, ldx, q, ldq, scale, stream);
-    return dispatch_nch<BLK, 1, ACT>(x, M, K, ldx, q, ldq, scale, stream);
+    if (bits == 8) return dispatch_nch<BLK, 0, ACT, IN>(x, M, K, ldx, q, ldq, scale, stream);
+    if (packed == 1) return dispatch_nch<BLK, 2, ACT, IN>(x, M, K, ldx, q, ldq, scale, stream);
+    if (packed == 2) return dispatch_nch<BLK, 3, ACT, IN>(x, M, K, ldx, q, ldq, scale, stream);
+    return dispatch_nch<BLK, 1, ACT, IN>(x, M, K, ldx, q, ldq, scale, stream);
 }
 
-template <int ACT>
+template <int ACT, int IN>
 int launch_rotquant_impl(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits,
                          int packed, void* q, int64_t ldq, float* scale, hipStream_t stream) {
     switch (hblock) {
-        case 0: return dispatch_out<1, ACT>(x, M, K, ldx, bits, packed, q, ldq, scale, stream);
-        case 16: return dispatch_out<16, ACT>(x, M, K, ldx, bits, packed, q, ldq, scale, stream);
-        case 64: return dispatch_out<64, ACT>(x, M, K, ldx, bits, packed, q, ldq, scale, stream);
-        case 256: return dispatch_out<256, ACT>(x, M, K, ldx, bits, packed, q, ldq, scale, stream);
+        case 0: return dispatch_out<1, ACT, IN>(x, M, K, ldx, bits, packed, q, ldq, scale, stream);
+        case 16: return dispatch_out<16, ACT, IN>(x, M, K, ldx, bits, packed, q, ldq, scale, stream);
+        case 64: return dispatch_out<64, ACT, IN>(x, M, K, ldx, bits, packed, q, ldq, scale, stream);
+        case 256: return dispatch_out<256, ACT, IN>(x, M, K, ldx, bits, packed, q, ldq, scale, stream);
         default: break;
     }
     set_error("rotquant: hblock must be 0, 16, 64 or 256 (got %d)", hblock);

@@ -11,7 +11,7 @@ import os
 
 import torch  # noqa: F401  (must be imported before the library is loaded)
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmq.so")
 
@@ -24,23 +24,23 @@ c_vp = ctypes.c_void_p
 _SIGNATURES = {
     "mq_abi_version": ([], c_int),
     "mq_last_error": ([], ctypes.c_char_p),
-    "mq_rotquant": ([c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_vp], c_int),
-    "mq_swiglu_rotquant": ([c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_vp], c_int),
+    "mq_rotquant": ([c_vp, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_vp], c_int),
+    "mq_swiglu_rotquant": ([c_vp, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_vp], c_int),
     "mq_decode_w4a8_codebook": ([c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_int, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp],
                                 c_int),
     "mq_quantize_weight": ([c_vp, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp],
                            c_int),
-    "mq_gemm_w4_group": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_vp,
-                          c_i64, c_i64, c_i64, c_i64, c_vp], c_int),
-    "mq_gemm_w4_group_ws": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_vp,
-                             c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp], c_int),
+    "mq_gemm_w4_group": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_int, c_vp,
+                          c_int, c_i64, c_i64, c_i64, c_i64, c_vp], c_int),
+    "mq_gemm_w4_group_ws": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_int, c_vp,
+                             c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp], c_int),
     "mq_gemm_workspace_bytes": ([c_i64, c_i64, c_i64], c_i64),
     "mq_gemm_w4_group_partials": ([c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_int, c_int, c_vp, c_i64, c_i64, c_i64,
                                    c_vp], c_int),
-    "mq_gemm_rowscale": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp],
-                         c_int),
-    "mq_gemm_rowscale_ws": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64,
-                             c_vp, c_i64, c_vp], c_int),
+    "mq_gemm_rowscale": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_int, c_vp, c_int, c_i64, c_i64, c_i64,
+                          c_i64, c_vp], c_int),
+    "mq_gemm_rowscale_ws": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_int, c_vp, c_int, c_i64, c_i64,
+                             c_i64, c_i64, c_vp, c_i64, c_vp], c_int),
     "mq_gemm_rowscale_acc": ([c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_vp], c_int),
 }
 
@@ -50,6 +50,15 @@ EXPORTED = tuple(_SIGNATURES)
 Q_BYTES, Q_PACKED, Q_X16ALT = 0, 1, 2
 ACT_I8, ACT_I4, ACT_X16ALT = 0, 1, 2
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
+DTYPE_CODE = {torch.bfloat16: DT_BF16, torch.float16: DT_F16, torch.float32: DT_F32}
+
+
+def dtype_code(dt) -> int:
+    """MQ_DT_* code of a torch floating-point dtype (bf16, fp16, fp32)."""
+    try:
+        return DTYPE_CODE[dt]
+    except KeyError:
+        raise ValueError(f"unsupported floating-point type {dt}: expected bfloat16, float16 or float32") from None
 WFMT_U4_ASYM_G64, WFMT_I4_SYM_G64, WFMT_I4_ROW, WFMT_I8_ROW = 0, 1, 2, 3
 
 

@@ -138,6 +138,10 @@ def layer_linear(tensors: dict, layer: str, config: dict, compile_safe: bool = F
         s_ch = _t(tensors, f"{layer}.weight_s_channel")
         cb = _t(tensors, f"{layer}.weight_codebook", required=False)
         gs = int(config["group_size"])
+        if not compile_safe and w.is_cuda:
+            # decoded once here, at load: a forward runs only rotate + quantize and the int8 GEMM
+            prepared = ops.PreparedW4A8(w, s_rel, s_ch, cb, gs, cg)
+            return lambda x, bias=None, out_dtype=torch.bfloat16: prepared(x, bias, out_dtype)
         return lambda x, bias=None, out_dtype=torch.bfloat16: lin["w4a8_int8_linear"](
             x, w, s_rel, s_ch, cb, None, bias, group_size=gs, convrot_groupsize=cg, out_dtype=out_dtype)
     if fmt == "int8_tensorwise":

@@ -16,11 +16,19 @@ Names, keyword arguments and error messages follow the reference's contract:
 input_act="swiglu" takes x as the [gate | up] pair and folds silu(gate) * up into the activation
 quantizer (patches/comfy_kitchen_swiglu_w4a4_fused.patch:17-33,60-63;
 patches/comfyui_swiglu_triton_env.patch:65-97), for every convrot group size and both activation
-widths.
+widths; other activations of ComfyUI's INPUT_ACT_EAGER table ("gelu_tanh",
+patches/comfyui_swiglu_triton_env.patch:54-56) are applied eagerly first, as comfy-kitchen's
+fallback `x = _apply_input_act(x, input_act)` does (patches/comfy_kitchen_swiglu_w4a4_fused.patch:60-64).
+Activations are taken in their own type (bf16, fp16 or fp32: the rotation runs in fp32 from the
+exact value) and outputs are written by the GEMM epilogue directly in the requested type, with the
+bias in its own type; the reference writes out_dtype=x.dtype from its GEMM
+(patches/comfy_kitchen_swiglu_w4a4_fused.patch:37-38).
 Every op is a thin host wrapper: the caller's tensors are validated, outputs are allocated with
 torch on the input's device, and the HIP kernels run asynchronously on the current stream.
 """
 from __future__ import annotations
+
+import weakref
 
 import torch
 
@@ -28,64 +36,89 @@ from . import _lib
 
 INT4_GROUP_SIZE = 64
 CONVROT_GROUPSIZES = (16, 64, 256)
+FLOAT_TYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 
-def _as_bf16_2d(x: torch.Tensor, k: int) -> torch.Tensor:
+def _as_2d(x: torch.Tensor, k: int) -> torch.Tensor:
     if not x.is_cuda:
         raise ValueError("kitchen_amd ops run on the GPU: x must be a device tensor")
-    x2 = x.reshape(-1, k)
-    if x2.dtype != torch.bfloat16:
-        x2 = x2.to(torch.bfloat16)
-    return x2.contiguous()
+    if x.dtype not in FLOAT_TYPES:
+        raise ValueError(f"x must be bfloat16, float16 or float32, got {x.dtype}")
+    return x.reshape(-1, k).contiguous()
 
 
-def _bias_bf16(bias, n: int, device):
+def _bias(bias, n: int, device):
+    """The bias on the device in its own floating-point type (bf16, fp16 or fp32), or None."""
     if bias is None:
         return None
     if bias.numel() != n:
         raise ValueError(f"bias has {bias.numel()} elements, expected {n}")
-    return bias.to(device=device, dtype=torch.bfloat16).contiguous()
+    if bias.dtype not in FLOAT_TYPES:
+        bias = bias.float()
+    return bias.reshape(-1).to(device=device).contiguous()
 
 
-def _finish(y: torch.Tensor, x: torch.Tensor, n: int, out_dtype) -> torch.Tensor:
-    y = y.reshape(*x.shape[:-1], n)
-    if out_dtype is not None and out_dtype != torch.bfloat16:
-        y = y.to(out_dtype)
-    return y
+def _out_dtype(out_dtype, x: torch.Tensor):
+    dt = x.dtype if out_dtype is None else out_dtype
+    if dt not in FLOAT_TYPES:
+        raise ValueError(f"out_dtype must be bfloat16, float16 or float32, got {dt}")
+    return dt
+
+
+def _finish(y: torch.Tensor, x: torch.Tensor, n: int) -> torch.Tensor:
+    return y.reshape(*x.shape[:-1], n)
 
 
 # --------------------------------------------------------------------------- activation quantizers
+
+def _swiglu_eager(h: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up in h's own type (ComfyUI's _swiglu_eager, patches/comfyui_swiglu_triton_env.patch:16-19)."""
+    gate, up = h.chunk(2, dim=-1)
+    return torch.nn.functional.silu(gate).mul_(up)
+
 
 def rotate_quantize(x: torch.Tensor, convrot_groupsize: int | None, bits: int, packed: bool | int = False,
                     swiglu: bool = False):
     """Rotate x [.., K] by H_cg per block and quantize per token to int8 (bits 8) or int4 (bits 4).
 
+    x: bfloat16, float16 or float32 (rotated in fp32 from its exact value).
     packed: False / Q_BYTES one code per byte, True / Q_PACKED packed int4 [M, K/2], Q_X16ALT the
     group GEMM's int4 operand layout (16 * q, negated in odd 64-column groups).
-    swiglu: x is [.., 2K] = gate | up and the quantized activation is bf16(silu(gate) * up).
+    swiglu: x is [.., 2K] = gate | up and the quantized activation is silu(gate) * up rounded to x's
+    type (fused for bf16 / fp16; fp32 gate | up pairs are formed eagerly in fp32 first, as the
+    reference's quantizer takes bf16 or fp16 only).
     Returns (q, scale): q int8 [M, K] or [M, K/2], scale float32 [M]."""
     layout = int(packed)
     width = x.shape[-1]
     if swiglu and width % 2:
         raise ValueError("h must hold gate | up halves")
+    if swiglu and x.dtype == torch.float32:
+        x, swiglu, width = _swiglu_eager(x), False, width // 2
     k = width // 2 if swiglu else width
-    x2 = _as_bf16_2d(x, width)
+    x2 = _as_2d(x, width)
     m = x2.shape[0]
     q = torch.empty((m, k // 2 if layout == _lib.Q_PACKED else k), dtype=torch.int8, device=x2.device)
     s = torch.empty((m,), dtype=torch.float32, device=x2.device)
-    _lib.call("mq_swiglu_rotquant" if swiglu else "mq_rotquant", x2.data_ptr(), m, k, width,
-              int(convrot_groupsize or 0), int(bits), layout, q.data_ptr(), q.stride(0), s.data_ptr(),
+    _lib.call("mq_swiglu_rotquant" if swiglu else "mq_rotquant", x2.data_ptr(), _lib.dtype_code(x2.dtype), m, k,
+              width, int(convrot_groupsize or 0), int(bits), layout, q.data_ptr(), q.stride(0), s.data_ptr(),
               _lib.stream_of(x2))
     return q, s
 
 
-def _input_act_swiglu(input_act: str | None) -> bool:
-    """True for the fused SwiGLU prologue; the reference's other eager activations are not built."""
+INPUT_ACTS = ("swiglu", "gelu_tanh")
+
+
+def _input_act(x: torch.Tensor, input_act: str | None):
+    """(x for the quantizer, fused SwiGLU?): "swiglu" folds into the quantizer; "gelu_tanh" is applied
+    eagerly in x's type (ComfyUI's INPUT_ACT_EAGER entry, patches/comfyui_swiglu_triton_env.patch:54-56)
+    before quantizing, the way comfy-kitchen falls back for activations it does not fuse."""
     if input_act is None:
-        return False
+        return x, False
     if input_act == "swiglu":
-        return True
-    raise NotImplementedError(f"input_act={input_act!r} is not fused in this build (only 'swiglu')")
+        return x, True
+    if input_act == "gelu_tanh":
+        return torch.nn.functional.gelu(x, approximate="tanh"), False
+    raise ValueError(f"unknown input_act {input_act!r}: expected one of {INPUT_ACTS} or None")
 
 
 def quantize_int4_rowwise_convrot64(x: torch.Tensor, convrot_groupsize: int = 256):
@@ -160,27 +193,40 @@ def _check_w4_group(qa, qweight, wscales, wzeros, n, group_size):
         raise ValueError(f"zero-points must be packed uint4 [{n}, {(groups + 1) // 2}]")
 
 
+_WS_BYTES: dict = {}
+
+
 def _workspace(m: int, n: int, k: int, device):
-    """Split-K workspace for an M x N x K product when the library wants one (small M), else None."""
-    nbytes = _lib.load().mq_gemm_workspace_bytes(m, n, k)
+    """Split-K workspace for an M x N x K product when the library wants one (small M), else None.
+    The size is asked of the library once per shape and device."""
+    key = (device.index, m, n, k)
+    nbytes = _WS_BYTES.get(key)
+    if nbytes is None:
+        with torch.cuda.device(device):
+            nbytes = _WS_BYTES[key] = int(_lib.load().mq_gemm_workspace_bytes(m, n, k))
     return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes > 0 else None
 
 
+def _bias_args(bias):
+    return (_lib.ptr(bias), _lib.DT_BF16 if bias is None else _lib.dtype_code(bias.dtype))
+
+
 def gemm_w4_group(qa, sa, qweight, wscales, wzeros, bias, n: int, group_size: int = INT4_GROUP_SIZE,
-                  act_mode: int = _lib.ACT_I8):
-    """y bf16 [M, N] = sa * sum_g wscales[:, g] * P_g + bias with P_g exact int32 group partials.
+                  act_mode: int = _lib.ACT_I8, out_dtype=torch.bfloat16):
+    """y [M, N] = sa * sum_g wscales[:, g] * P_g + bias with P_g exact int32 group partials, written
+    in out_dtype (bf16, fp16 or fp32); bias in its own floating-point type or None.
 
     act_mode: ACT_I8 int8 codes, ACT_I4 int4 codes one per byte, ACT_X16ALT the layout written by
     rotate_quantize(..., packed=Q_X16ALT). Small M splits K over a torch-allocated workspace."""
     m, k = qa.shape
     _check_w4_group(qa, qweight, wscales, wzeros, n, group_size)
-    y = torch.empty((m, n), dtype=torch.bfloat16, device=qa.device)
+    y = torch.empty((m, n), dtype=out_dtype, device=qa.device)
     ldwz = wzeros.stride(0) if wzeros is not None else 0
     work = _workspace(m, n, k, qa.device)
     _lib.call("mq_gemm_w4_group_ws", qa.data_ptr(), qa.stride(0), sa.data_ptr(), qweight.data_ptr(),
               qweight.stride(0), wscales.data_ptr(), wscales.stride(0), _lib.ptr(wzeros), ldwz, int(group_size),
-              int(act_mode), _lib.ptr(bias), y.data_ptr(), y.stride(0), m, n, k, _lib.ptr(work),
-              0 if work is None else work.numel(), _lib.stream_of(qa))
+              int(act_mode), *_bias_args(bias), y.data_ptr(), _lib.dtype_code(out_dtype), y.stride(0), m, n, k,
+              _lib.ptr(work), 0 if work is None else work.numel(), _lib.stream_of(qa))
     return y
 
 
@@ -197,15 +243,16 @@ def gemm_w4_group_partials(qa, qweight, wzeros, n: int, group_size: int = INT4_G
     return part
 
 
-def gemm_rowscale(qa, sa, qweight, wscales, bias, n: int, wbits: int):
-    """y bf16 [M, N] = (qa . w^T) * sa[m] * wscales[n] + bias, full-K int32 accumulator (split over
-    K into int32 partial sums for small M, summed exactly)."""
+def gemm_rowscale(qa, sa, qweight, wscales, bias, n: int, wbits: int, out_dtype=torch.bfloat16):
+    """y [M, N] = (qa . w^T) * sa[m] * wscales[n] + bias in out_dtype, full-K int32 accumulator (split
+    over K into int32 partial sums for small M, summed exactly)."""
     m, k = qa.shape
-    y = torch.empty((m, n), dtype=torch.bfloat16, device=qa.device)
+    y = torch.empty((m, n), dtype=out_dtype, device=qa.device)
     work = _workspace(m, n, k, qa.device)
     _lib.call("mq_gemm_rowscale_ws", qa.data_ptr(), qa.stride(0), sa.data_ptr(), qweight.data_ptr(),
-              qweight.stride(0), int(wbits), wscales.data_ptr(), _lib.ptr(bias), y.data_ptr(), y.stride(0),
-              m, n, k, _lib.ptr(work), 0 if work is None else work.numel(), _lib.stream_of(qa))
+              qweight.stride(0), int(wbits), wscales.data_ptr(), *_bias_args(bias), y.data_ptr(),
+              _lib.dtype_code(out_dtype), y.stride(0), m, n, k, _lib.ptr(work), 0 if work is None else work.numel(),
+              _lib.stream_of(qa))
     return y
 
 
@@ -223,7 +270,7 @@ def gemm_rowscale_acc(qa, qweight, n: int, wbits: int):
 def convrot_w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.Tensor, bias=None,
                         convrot_groupsize: int = 256, quant_group_size: int = INT4_GROUP_SIZE,
                         linear_dtype: str = "int4", input_act: str | None = None) -> torch.Tensor:
-    """``act(x) @ W.T + bias`` with ConvRot W4A4 weights.
+    """``act(x) @ W.T + bias`` with ConvRot W4A4 weights, written in x's type.
 
     qweight int8 [N, K/2] holds signed int4 (low nibble = even k). wscales is either the shipped
     per-row F32 [N] scale (full-K int32 accumulation) or the configs' per-group fp16 [N, K/64]
@@ -232,7 +279,8 @@ def convrot_w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.T
         raise ValueError(f"ConvRot W4A4 linear_dtype must be 'int4' or 'int8', got {linear_dtype!r}")
     if quant_group_size != INT4_GROUP_SIZE:
         raise ValueError(f"int4 MMA kernel requires quant_group_size {INT4_GROUP_SIZE}")
-    swiglu = _input_act_swiglu(input_act)
+    x_out = x
+    x, swiglu = _input_act(x, input_act)
     k = x.shape[-1] // 2 if swiglu else x.shape[-1]
     if k != qweight.shape[-1] * 2:
         raise ValueError(f"Input K={k} does not match qweight K={qweight.shape[-1] * 2}")
@@ -240,24 +288,76 @@ def convrot_w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.T
         raise ValueError(f"Input K={k} is not divisible by convrot_groupsize={convrot_groupsize}")
     n = qweight.shape[0]
     bits = 4 if linear_dtype == "int4" else 8
+    out_dtype = _out_dtype(None, x_out)
     if wscales.dim() == 2 and wscales.shape[1] > 1:
         if wscales.shape != (n, k // quant_group_size):
             raise ValueError(f"per-group wscales must be [{n}, {k // quant_group_size}], got {list(wscales.shape)}")
         # int4 activations go to the group GEMM in its x16 operand layout
         layout = _lib.Q_X16ALT if bits == 4 else _lib.Q_BYTES
         qa, sa = rotate_quantize(x, convrot_groupsize, bits, layout, swiglu)
-        b = _bias_bf16(bias, n, qa.device)
         ws = wscales.to(torch.float16).contiguous()
         act = _lib.ACT_X16ALT if bits == 4 else _lib.ACT_I8
-        y = gemm_w4_group(qa, sa, qweight.contiguous(), ws, None, b, n, quant_group_size, act)
+        y = gemm_w4_group(qa, sa, qweight.contiguous(), ws, None, _bias(bias, n, qa.device), n, quant_group_size, act,
+                          out_dtype)
     else:
         ws = wscales.reshape(-1).to(torch.float32).contiguous()
         if ws.numel() != n:
             raise ValueError(f"per-row wscales must have {n} elements, got {ws.numel()}")
         qa, sa = rotate_quantize(x, convrot_groupsize, bits, swiglu=swiglu)
-        b = _bias_bf16(bias, n, qa.device)
-        y = gemm_rowscale(qa, sa, qweight.contiguous(), ws, b, n, 4)
-    return _finish(y, x, n, x.dtype if x.dtype in (torch.float16, torch.float32) else None)
+        y = gemm_rowscale(qa, sa, qweight.contiguous(), ws, _bias(bias, n, qa.device), n, 4, out_dtype)
+    return _finish(y, x_out, n)
+
+
+# Shipped asym_w4a8_int8 weights decoded to (int8 [N, K], row scale [N]) once per weight: one entry
+# per packed-weight tensor object, valid while the operands' storage and versions are unchanged,
+# dropped when that tensor is freed.
+_DECODED: dict = {}
+
+
+def _decoded_w4a8(qdata, s_rel, s_channel, codebook, group_size):
+    sig = (qdata.data_ptr(), qdata._version, s_rel.data_ptr(), s_rel._version, s_channel.data_ptr(),
+           s_channel._version, 0 if codebook is None else codebook.data_ptr(),
+           0 if codebook is None else codebook._version, int(group_size))
+    qid = id(qdata)
+    hit = _DECODED.get(qid)
+    if hit is not None and hit[0] == sig:
+        return hit[1]
+    dec = decode_w4a8_codebook_weight(qdata, s_rel, s_channel, codebook, group_size)
+    if hit is None:
+        weakref.finalize(qdata, _DECODED.pop, qid, None)
+    _DECODED[qid] = (sig, dec)
+    return dec
+
+
+class PreparedW4A8:
+    """A shipped asym_w4a8_int8 weight decoded once (at load) to the int8 weight and per-row scale
+    the row-scale GEMM takes; calling it runs only rotate + quantize and the int8 GEMM."""
+
+    def __init__(self, qdata, s_rel, s_channel, codebook=None, group_size: int = 16, convrot_groupsize: int = 256):
+        self.q8, self.row_scale = decode_w4a8_codebook_weight(qdata, s_rel, s_channel, codebook, group_size)
+        self.n, self.k = self.q8.shape
+        self.convrot_groupsize = convrot_groupsize
+
+    def __call__(self, x, bias=None, out_dtype=None):
+        return int8_rowscale_linear(x, self.q8, self.row_scale, bias, out_dtype, self.convrot_groupsize)
+
+
+def int8_rowscale_linear(x, q8, row_scale, bias=None, out_dtype=None, convrot_groupsize: int | None = 256,
+                         input_act: str | None = None):
+    """The W8A8 linear the decoded W4A8 weights and int8_tensorwise share: rotate + int8 per-token
+    quantize, then the int8 row-scale GEMM."""
+    x_out = x
+    x, swiglu = _input_act(x, input_act)
+    k = x.shape[-1] // 2 if swiglu else x.shape[-1]
+    n = q8.shape[0]
+    if q8.shape[1] != k:
+        raise ValueError(f"Input K={k} does not match weight K={q8.shape[1]}")
+    if convrot_groupsize and k % convrot_groupsize:
+        raise ValueError(f"Input K={k} is not divisible by convrot_groupsize={convrot_groupsize}")
+    qa, sa = rotate_quantize(x, convrot_groupsize, 8, swiglu=swiglu)
+    ws = row_scale.reshape(-1).to(torch.float32).contiguous()
+    y = gemm_rowscale(qa, sa, q8.contiguous(), ws, _bias(bias, n, qa.device), n, 8, _out_dtype(out_dtype, x_out))
+    return _finish(y, x_out, n)
 
 
 def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, s_channel=None, codebook=None,
@@ -270,8 +370,8 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
       zero-points (None = signed int4 weights), s_channel and codebook None; group GEMM.
     * comfy-kitchen's shipped asym_w4a8_int8 (tools/_formats.py:79-125): qdata I8 [N, K/2] codes,
       s_rel fp8 e4m3fn (or its U8 bytes) [N, K/group], s_channel F32 [N], codebook F32 [16] or
-      None, no correction; the weight is decoded to int8 with a per-row scale on each call
-      (decode_w4a8_codebook_weight) and runs on the int8 row-scale GEMM."""
+      None, no correction; the weight is decoded to int8 with a per-row scale once (cached per
+      weight tensor; PreparedW4A8 holds it explicitly) and runs on the int8 row-scale GEMM."""
     k = x.shape[-1]
     if k != qdata.shape[-1] * 2:
         raise ValueError(f"Input K={k} does not match qdata K={qdata.shape[-1] * 2}")
@@ -284,11 +384,8 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
                                       "the reference's loader drops it as well")
         if s_channel is None:
             raise ValueError("the shipped asym_w4a8_int8 layout needs s_channel")
-        q8, rs = decode_w4a8_codebook_weight(qdata, s_rel, s_channel, codebook, group_size)
-        qa, sa = rotate_quantize(x, convrot_groupsize, 8)
-        b = _bias_bf16(bias, n, qa.device)
-        y = gemm_rowscale(qa, sa, q8, rs, b, n, 8)
-        return _finish(y, x, n, out_dtype)
+        q8, rs = _decoded_w4a8(qdata, s_rel, s_channel, codebook, group_size)
+        return int8_rowscale_linear(x, q8, rs, bias, out_dtype, convrot_groupsize)
     if s_rel.dtype != torch.float16:
         raise ValueError(f"per-group s_rel must be float16 (configs' scheme) or fp8 bytes, got {s_rel.dtype}")
     if group_size != INT4_GROUP_SIZE:
@@ -298,11 +395,11 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
     if correction is not None and correction.shape != (n, (k // group_size + 1) // 2):
         raise ValueError(f"correction (zero-points) must be [{n}, {(k // group_size + 1) // 2}]")
     qa, sa = rotate_quantize(x, convrot_groupsize, 8)
-    b = _bias_bf16(bias, n, qa.device)
     qw = qdata.view(torch.uint8).contiguous()
     zz = correction.view(torch.uint8).contiguous() if correction is not None else None
-    y = gemm_w4_group(qa, sa, qw, s_rel.contiguous(), zz, b, n, group_size)
-    return _finish(y, x, n, out_dtype)
+    y = gemm_w4_group(qa, sa, qw, s_rel.contiguous(), zz, _bias(bias, n, qa.device), n, group_size,
+                      out_dtype=_out_dtype(out_dtype, x))
+    return _finish(y, x, n)
 
 
 def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, bias=None,
@@ -310,15 +407,5 @@ def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tenso
                 input_act: str | None = None) -> torch.Tensor:
     """int8_tensorwise linear: int8 per-row weights [N, K] + F32 scale [N, 1], int8 per-token
     activations (after H_cg when convrot), full-K int32 accumulation."""
-    swiglu = _input_act_swiglu(input_act)
-    k = x.shape[-1] // 2 if swiglu else x.shape[-1]
-    n = weight.shape[0]
-    if weight.shape[1] != k:
-        raise ValueError(f"Input K={k} does not match weight K={weight.shape[1]}")
-    if convrot and k % convrot_groupsize:
-        raise ValueError(f"Input K={k} is not divisible by convrot_groupsize={convrot_groupsize}")
-    qa, sa = rotate_quantize(x, convrot_groupsize if convrot else None, 8, swiglu=swiglu)
-    b = _bias_bf16(bias, n, qa.device)
-    ws = weight_scale.reshape(-1).to(torch.float32).contiguous()
-    y = gemm_rowscale(qa, sa, weight.contiguous(), ws, b, n, 8)
-    return _finish(y, x, n, out_dtype)
+    return int8_rowscale_linear(x, weight, weight_scale, bias, out_dtype, convrot_groupsize if convrot else None,
+                                input_act)

@@ -8,7 +8,9 @@
  * of the last failure on the calling thread is returned by mq_last_error().
  *
  * Layout conventions (all row-major, strides in elements of the stated type):
- *   bf16 / fp16 values are passed as uint16_t bit patterns.
+ *   floating-point operands whose type the caller chooses (activations, bias, outputs, weights to
+ *   quantize) are passed as void pointers with an MQ_DT_* type code; bf16 / fp16 are their bit
+ *   patterns. Scales keep fixed types (fp32 per token / per row, fp16 per weight group).
  *   int4 packing: byte j of a row holds k = 2j in bits 0-3 and k = 2j + 1 in bits 4-7
  *   (experiments/qwen21-kernel/node/__init__.py:82-86; custom_nodes/comfy-lowbit-loader/
  *   kernel.py:75-81 for the unsigned form). Signed nibbles decode as v >= 8 -> v - 16.
@@ -25,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MQ_ABI_VERSION 6
+#define MQ_ABI_VERSION 7
 
 enum {
     MQ_OK = 0,
@@ -33,6 +35,11 @@ enum {
     MQ_EUNSUPPORTED = -2, /* valid request outside what this build implements */
     MQ_ELAUNCH = -3,      /* the HIP runtime refused a launch */
 };
+
+/* Element types of the floating-point operands (the *_dtype arguments). */
+#define MQ_DT_BF16 0
+#define MQ_DT_F16 1
+#define MQ_DT_F32 2
 
 /* Layouts of the activation codes written by mq_rotquant (its `packed` argument). */
 enum {
@@ -65,7 +72,9 @@ const char* mq_last_error(void);
  *   s[m] = max(max_k |xr[m,k]| / L, 1e-10f), q[m,k] = clamp(rne(xr[m,k] / s[m]), -L, L),
  * with L = 127 for bits = 8 and L = 7 for bits = 4. The division is IEEE fp32.
  *
- *   x      bf16 [M, K], row stride ldx elements (ldx % 8 == 0, 16-byte aligned base)
+ *   x      [M, K] of type x_dtype (MQ_DT_BF16, MQ_DT_F16 or MQ_DT_F32; the 16-bit types convert
+ *          exactly to fp32, the type the rotation runs in), row stride ldx elements (a multiple of
+ *          16 bytes, 16-byte aligned base)
  *   bits   8 or 4
  *   packed MQ_Q_BYTES: q is int8 [M, K] (one code per byte, stride ldq bytes)
  *          MQ_Q_PACKED: q is int8 [M, K/2] packed int4 (bits must be 4, stride ldq bytes)
@@ -73,35 +82,31 @@ const char* mq_last_error(void);
  *   scale  fp32 [M]
  * Requires K % 16 == 0, K <= 16384, K % hblock == 0.
  */
-int mq_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits, int packed,
+int mq_rotquant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int hblock, int bits, int packed,
                 void* q, int64_t ldq, float* scale, void* stream);
 
 /*
  * SwiGLU prologue fused into rotate + quantize: the activation is
- *   a[m,k] = bf16( silu(h[m,k]) * h[m,K+k] )      (fp32 arithmetic, one rounding to bf16)
+ *   a[m,k] = T( silu(h[m,k]) * h[m,K+k] )      (fp32 arithmetic, one rounding to T = h_dtype)
  * formed while loading the gate | up row, then rotated and quantized exactly as mq_rotquant does
- * with x = a. The bf16 intermediate never touches memory.
+ * with x = a. The intermediate never touches memory; like the reference, the product is rounded to
+ * the input's own type (bf16 or fp16, tools/ck_swiglu/swiglu_quant.cu:63-70,124-132).
  *
  * Replaces swiglu_quantize_int4_rowwise_convrot64(h) (tools/ck_swiglu/swiglu_quant.cu:23-97 and
  * :111-120, dispatched by convrot_w4a4_linear(..., input_act="swiglu") at
  * patches/comfy_kitchen_swiglu_w4a4_fused.patch:17-33) and generalises it to every Hadamard block,
  * int8 codes and the group GEMM's code layouts. silu(g) = g / (1 + exp(-g)) is taken correctly
- * rounded to fp32 (the reference uses a hardware exp approximation and an fp32 division): a table of
- * the exact results for every bf16 gate outside the closed forms |g| < 2^-25 -> g / 2,
- * g >= 128 -> g, g <= -128 -> -0.
+ * rounded to fp32 (the reference uses a hardware exp approximation and an fp32 division): tables of
+ * the exact results, for every bf16 gate outside the closed forms |g| < 2^-25 -> g / 2,
+ * g >= 128 -> g, g <= -128 -> -0, and for every fp16 gate.
  *
- *   h      bf16 [M, 2K]: gate in columns [0, K), up in [K, 2K); row stride ldh >= 2K elements
- *          (ldh % 8 == 0, 16-byte aligned base)
+ *   h      [M, 2K] of type h_dtype (MQ_DT_BF16 or MQ_DT_F16): gate in columns [0, K), up in
+ *          [K, 2K); row stride ldh >= 2K elements (ldh % 8 == 0, 16-byte aligned base)
  *   other arguments as mq_rotquant (K is the width of the activation, half of h's).
  * Requires K % 16 == 0, K <= 16384, K % hblock == 0.
  */
-int mq_swiglu_rotquant(const void* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits, int packed,
-                       void* q, int64_t ldq, float* scale, void* stream);
-
-/* Element types of mq_quantize_weight's input. */
-#define MQ_DT_BF16 0
-#define MQ_DT_F16 1
-#define MQ_DT_F32 2
+int mq_swiglu_rotquant(const void* h, int h_dtype, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
+                       int packed, void* q, int64_t ldq, float* scale, void* stream);
 
 /* Weight formats written by mq_quantize_weight. */
 #define MQ_WFMT_U4_ASYM_G64 0   /* configs' W4A8: uint4 asymmetric per 64, fp16 scale, uint4 zero   */
@@ -162,7 +167,7 @@ int mq_decode_w4a8_codebook(const void* qdata, int64_t ldq, const void* s_rel, i
 /*
  * Quantized GEMM with per-group weight scales (W4A8 asym / W4A4 sym, configs' scheme):
  *   P[g,m,n] = sum_{k in group g} qa[m,k] * (w[n,k] - z[n,g])            (exact int32)
- *   y[m,n]   = bf16( sa[m] * sum_g ws[n,g] * P[g,m,n] + bias[n] )
+ *   y[m,n]   = T( sa[m] * sum_g ws[n,g] * P[g,m,n] + bias[n] )      (fp32, one rounding to T)
  *
  * Replaces the GEMM half of w4a8_int8_linear / convrot_w4a4_linear (the int4_linear call at
  * patches/comfy_kitchen_swiglu_w4a4_fused.patch:37-38) for per-group fp16 weight scales; the
@@ -176,14 +181,15 @@ int mq_decode_w4a8_codebook(const void* qdata, int64_t ldq, const void* s_rel, i
  *   wz    packed uint4 zero-points [N, ceil(K/group/2)], stride ldwz bytes; NULL = signed
  *         symmetric int4 weights (no zero-point)
  *   group 64
- *   bias  bf16 [N] or NULL
- *   y     bf16 [M, N], stride ldy elements
+ *   bias  [N] of type bias_dtype (MQ_DT_BF16, MQ_DT_F16 or MQ_DT_F32), or NULL
+ *   y     [M, N] of type y_dtype (MQ_DT_BF16, MQ_DT_F16 or MQ_DT_F32: the caller's out_dtype,
+ *         written directly), stride ldy elements
  * Requires K % 64 == 0. The partials are exact; the sum over groups is accumulated in fp32.
  */
 int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
                      const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
-                     const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
-                     void* stream);
+                     const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy, int64_t M, int64_t N,
+                     int64_t K, void* stream);
 
 /*
  * mq_gemm_w4_group with a caller-provided workspace. When the 256 x 256 output tiles would leave
@@ -200,8 +206,8 @@ int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8
  */
 int mq_gemm_w4_group_ws(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
                         const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
-                        const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
-                        void* workspace, int64_t workspace_bytes, void* stream);
+                        const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy, int64_t M, int64_t N,
+                        int64_t K, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Workspace bytes mq_gemm_w4_group_ws / mq_gemm_rowscale_ws use for an M x N x K product on the
  * current device (0 when the shape fills the device without splitting K, whole or in part). */
@@ -219,7 +225,7 @@ int mq_gemm_w4_group_partials(const int8_t* qa, int64_t lda, const uint8_t* qw, 
 /*
  * Quantized GEMM with per-row weight scales and a full-K int32 accumulator (policy 0 of
  * experiments/qwen21-kernel/kernels/g64_gemm6.cu:5):
- *   y[m,n] = bf16( (sum_k qa[m,k] * w[n,k]) * sa[m] * ws[n] + bias[n] )
+ *   y[m,n] = T( (sum_k qa[m,k] * w[n,k]) * sa[m] * ws[n] + bias[n] )
  * Replaces int4_linear(qact, qweight, x_scale, wscales, bias, out_dtype) of the shipped ConvRot
  * W4A4 format (patches/comfy_kitchen_swiglu_w4a4_fused.patch:37-38) when wbits = 4, and the
  * int8 x int8 GEMM of int8_linear (tools/verify_w4a4.py:342-370) when wbits = 8.
@@ -227,17 +233,18 @@ int mq_gemm_w4_group_partials(const int8_t* qa, int64_t lda, const uint8_t* qw, 
  *   qa    int8 activation codes [M, K], stride lda bytes
  *   qw    wbits 4: signed int4 packed [N, K/2]; wbits 8: int8 [N, K]; stride ldw bytes
  *   ws    fp32 [N]
+ *   bias, y as mq_gemm_w4_group
  * Requires K % 64 == 0.
  */
 int mq_gemm_rowscale(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw,
-                     int wbits, const float* ws, const uint16_t* bias, uint16_t* y, int64_t ldy,
-                     int64_t M, int64_t N, int64_t K, void* stream);
+                     int wbits, const float* ws, const void* bias, int bias_dtype, void* y, int y_dtype,
+                     int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* mq_gemm_rowscale with a caller-provided workspace (int32 partial sums per K slice, summed
  * exactly before the epilogue: the same result as without the split). */
 int mq_gemm_rowscale_ws(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw, int wbits,
-                        const float* ws, const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N,
-                        int64_t K, void* workspace, int64_t workspace_bytes, void* stream);
+                        const float* ws, const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy,
+                        int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Debug / parity entry: the full-K int32 accumulator of mq_gemm_rowscale, acc int32 [M, N]. */
 int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t ldw, int wbits,

@@ -17,10 +17,15 @@ reference approximates:
     silu32(g) = RN_fp32(g / (1 + exp(-g)))            (exact real arithmetic, one rounding)
     swiglu_bf16(g, u) = RN_bf16(RN_fp32(silu32(g) * u))
 
-Here silu32 is evaluated in float64 and rounded to fp32. For the bf16 gate values this path sees,
-that equals the correctly rounded value; tests/test_oracle_swiglu.py checks all 65536 bf16
-patterns against exact decimal arithmetic. Closed forms it reproduces: |g| < 2^-25 gives g / 2,
-g >= 128 gives g and g <= -128 gives -0.
+Here silu32 is evaluated in float64 and rounded to fp32. For the bf16 and fp16 gate values this
+path sees, that equals the correctly rounded value; tests/test_oracle_swiglu.py checks every finite
+bf16 and fp16 pattern against exact decimal arithmetic. Closed forms it reproduces for bf16 gates:
+|g| < 2^-25 gives g / 2, g >= 128 gives g and g <= -128 gives -0.
+
+fp16 inputs round the product to fp16 instead (the reference's from_float<InType>,
+swiglu_quant.cu:63-70, dispatched for kHalf at :128-132):
+
+    swiglu_f16(g, u) = RN_fp16(RN_fp32(silu32(g) * u))
 
 Pinning (tests/test_oracle_swiglu.py): exhaustive comparison with Python's decimal module at
 60 digits over every finite bf16 gate (rounded to the nearest fp32 with ties to even), the
@@ -51,12 +56,20 @@ def swiglu_bf16(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     return bf16_bits_to_f32(f32_to_bf16_bits(prod))
 
 
-def swiglu_rotquant(h: np.ndarray, block: int, bits: int) -> tuple[np.ndarray, np.ndarray]:
-    """Fused SwiGLU quantizer: h float32 (bf16 values) [M, 2K] = gate | up -> rotquant of the
-    bf16 activation [M, K] (swiglu_quant.cu:23-97 with the per-token int8 / int4 quantizer of
-    this path). Returns (q int8 codes [M, K], s float32 [M])."""
+def swiglu_f16(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """fp16-rounded silu(g) * u for fp16 inputs, returned as float32 holding fp16 values."""
+    prod = (silu32(g) * np.asarray(u, dtype=F32)).astype(F32)
+    with np.errstate(over="ignore"):
+        return prod.astype(np.float16).astype(F32)
+
+
+def swiglu_rotquant(h: np.ndarray, block: int, bits: int, dtype: str = "bf16") -> tuple[np.ndarray, np.ndarray]:
+    """Fused SwiGLU quantizer: h float32 (bf16 or fp16 values, per `dtype`) [M, 2K] = gate | up ->
+    rotquant of the activation [M, K] rounded to that type (swiglu_quant.cu:23-97 with the
+    per-token int8 / int4 quantizer of this path). Returns (q int8 codes [M, K], s float32 [M])."""
     h = np.asarray(h, dtype=F32)
     if h.shape[1] % 2:
         raise ValueError("h must hold gate | up halves")
     k = h.shape[1] // 2
-    return rotquant(swiglu_bf16(h[:, :k], h[:, k:]), block, bits)
+    act = swiglu_f16 if dtype == "f16" else swiglu_bf16
+    return rotquant(act(h[:, :k], h[:, k:]), block, bits)

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mq_abi_version() == 6
+    assert lib.mq_abi_version() == 7
 
 
 def _err(lib):
@@ -48,35 +48,49 @@ def _err(lib):
 
 def test_rotquant_validation_rejects_before_launch(lib):
     # null device pointers are never dereferenced: every case fails validation first
-    assert lib.mq_rotquant(None, 4, 256, 256, 256, 5, 0, None, 256, None, None) == -1
+    assert lib.mq_rotquant(None, 0, 4, 256, 256, 256, 5, 0, None, 256, None, None) == -1
     assert "bits" in _err(lib)
-    assert lib.mq_rotquant(None, 4, 256, 256, 32, 8, 0, None, 256, None, None) == -1
+    assert lib.mq_rotquant(None, 0, 4, 256, 256, 32, 8, 0, None, 256, None, None) == -1
     assert "group size" in _err(lib)
-    assert lib.mq_rotquant(None, 4, 200, 200, 0, 8, 0, None, 256, None, None) == -1
+    assert lib.mq_rotquant(None, 0, 4, 200, 200, 0, 8, 0, None, 256, None, None) == -1
     assert "multiple of 16" in _err(lib)
-    assert lib.mq_rotquant(None, 4, 320, 320, 256, 8, 0, None, 320, None, None) == -1
+    assert lib.mq_rotquant(None, 0, 4, 320, 320, 256, 8, 0, None, 320, None, None) == -1
     assert "not a multiple of the group size" in _err(lib)
-    assert lib.mq_rotquant(None, 4, 32768, 32768, 256, 8, 0, None, 32768, None, None) == -2
-    assert lib.mq_rotquant(None, 4, 256, 256, 256, 8, 1, None, 256, None, None) == -1
+    assert lib.mq_rotquant(None, 0, 4, 32768, 32768, 256, 8, 0, None, 32768, None, None) == -2
+    assert lib.mq_rotquant(None, 0, 4, 256, 256, 256, 8, 1, None, 256, None, None) == -1
     assert "packed" in _err(lib)
-    assert lib.mq_rotquant(None, 4, 256, 256, 256, 8, 2, None, 256, None, None) == -1
+    assert lib.mq_rotquant(None, 0, 4, 256, 256, 256, 8, 2, None, 256, None, None) == -1
     assert "packed" in _err(lib)
-    assert lib.mq_rotquant(None, 4, 256, 256, 256, 4, 3, None, 256, None, None) == -1
+    assert lib.mq_rotquant(None, 0, 4, 256, 256, 256, 4, 3, None, 256, None, None) == -1
     assert "layout" in _err(lib)
     # M == 0 is a valid no-op
-    assert lib.mq_rotquant(None, 0, 256, 256, 256, 8, 0, None, 256, None, None) == 0
+    assert lib.mq_rotquant(None, 0, 0, 256, 256, 256, 8, 0, None, 256, None, None) == 0
+    # input types: bf16 (0), fp16 (1), fp32 (2); rows must be multiples of 16 bytes (fake aligned
+    # addresses: every case below fails validation, nothing is dereferenced or launched)
+    a = 1 << 20
+    assert lib.mq_rotquant(None, 3, 4, 256, 256, 256, 8, 0, None, 256, None, None) == -1
+    assert "input type" in _err(lib)
+    assert lib.mq_rotquant(a, 1, 4, 256, 260, 256, 8, 0, a, 256, a, None) == -1
+    assert "ldx % 8" in _err(lib)
+    assert lib.mq_rotquant(a, 2, 4, 256, 258, 256, 8, 0, a, 256, a, None) == -1
+    assert "ldx % 4" in _err(lib)
+    assert lib.mq_rotquant(None, 2, 0, 256, 256, 256, 8, 0, None, 256, None, None) == 0
 
 
 def test_swiglu_rotquant_validation_rejects_before_launch(lib):
     # h holds gate | up: its row stride must cover 2K columns
-    assert lib.mq_swiglu_rotquant(None, 4, 256, 256, 256, 8, 0, None, 256, None, None) == -1
+    assert lib.mq_swiglu_rotquant(None, 0, 4, 256, 256, 256, 8, 0, None, 256, None, None) == -1
     assert "null" in _err(lib)
-    assert lib.mq_swiglu_rotquant(None, 4, 256, 384, 256, 8, 0, None, 256, None, None) == -1
+    assert lib.mq_swiglu_rotquant(None, 0, 4, 256, 384, 256, 8, 0, None, 256, None, None) == -1
     assert "swiglu_rotquant" in _err(lib)
-    assert lib.mq_swiglu_rotquant(None, 4, 320, 640, 256, 8, 0, None, 320, None, None) == -1
+    assert lib.mq_swiglu_rotquant(None, 0, 4, 320, 640, 256, 8, 0, None, 320, None, None) == -1
     assert "not a multiple of the group size" in _err(lib)
-    assert lib.mq_swiglu_rotquant(None, 4, 32768, 65536, 256, 8, 0, None, 32768, None, None) == -2
-    assert lib.mq_swiglu_rotquant(None, 0, 256, 512, 256, 4, 1, None, 128, None, None) == 0
+    assert lib.mq_swiglu_rotquant(None, 0, 4, 32768, 65536, 256, 8, 0, None, 32768, None, None) == -2
+    assert lib.mq_swiglu_rotquant(None, 0, 0, 256, 512, 256, 4, 1, None, 128, None, None) == 0
+    # the SwiGLU prologue takes bf16 or fp16 (as the reference's fused quantizer does)
+    assert lib.mq_swiglu_rotquant(None, 2, 4, 256, 512, 256, 8, 0, None, 256, None, None) == -1
+    assert "input type" in _err(lib)
+    assert lib.mq_swiglu_rotquant(None, 1, 0, 256, 512, 256, 8, 0, None, 256, None, None) == 0
 
 
 def test_decode_codebook_validation_rejects_before_launch(lib):
@@ -90,18 +104,36 @@ def test_decode_codebook_validation_rejects_before_launch(lib):
 
 
 def test_gemm_validation_rejects_before_launch(lib):
-    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 128, 0, None, None, 8, 8, 8, 64, None) == -1
+    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 128, 0, None, 0, None, 0, 8, 8, 8, 64, None) == -1
     assert "group size must be 64" in _err(lib)
-    assert lib.mq_gemm_w4_group(None, 96, None, None, 48, None, 1, None, 1, 64, 0, None, None, 8, 8, 8, 96, None) == -1
+    assert lib.mq_gemm_w4_group(None, 96, None, None, 48, None, 1, None, 1, 64, 0, None, 0, None, 0, 8, 8, 8, 96, None) == -1
     assert "multiple of 64" in _err(lib)
-    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 64, 3, None, None, 8, 8, 8, 64, None) == -1
+    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 64, 3, None, 0, None, 0, 8, 8, 8, 64, None) == -1
     assert "act_mode" in _err(lib)
     assert lib.mq_gemm_w4_group_partials(None, 64, None, 32, None, 1, 64, 7, None, 8, 8, 64, None) == -1
     assert "act_mode" in _err(lib)
-    assert lib.mq_gemm_rowscale(None, 64, None, None, 64, 3, None, None, None, 8, 8, 8, 64, None) == -1
+    assert lib.mq_gemm_rowscale(None, 64, None, None, 64, 3, None, None, 0, None, 0, 8, 8, 8, 64, None) == -1
     assert "wbits" in _err(lib)
     assert lib.mq_gemm_rowscale_acc(None, 64, None, 64, 8, None, 8, 8, 64, None) == -1
     assert "null" in _err(lib)
+
+
+def test_gemm_output_types_are_checked(lib):
+    # operand pointers must be non-null before the output checks run: fake 256-byte aligned addresses
+    # that are never dereferenced (every case fails validation before any launch)
+    a = 1 << 20
+    assert lib.mq_gemm_w4_group(a, 64, a, a, 32, a, 1, None, 1, 64, 0, None, 0, a, 3, 8, 8, 8, 64, None) == -1
+    assert "output type" in _err(lib)
+    assert lib.mq_gemm_w4_group(a, 64, a, a, 32, a, 1, None, 1, 64, 0, a, 5, a, 0, 8, 8, 8, 64, None) == -1
+    assert "bias type" in _err(lib)
+    assert lib.mq_gemm_w4_group(a, 64, a, a, 32, a, 1, None, 1, 64, 0, None, 0, a + 2, 2, 8, 8, 8, 64, None) == -1
+    assert "aligned" in _err(lib)
+    assert lib.mq_gemm_rowscale(a, 64, a, a, 64, 8, a, None, 0, None, 1, 8, 8, 8, 64, None) == -1
+    assert "non-null" in _err(lib)
+    assert lib.mq_gemm_rowscale(a, 64, a, a, 64, 8, a, a + 2, 2, a, 1, 8, 8, 8, 64, None) == -1
+    assert "bias must be aligned" in _err(lib)
+    assert lib.mq_gemm_rowscale(a, 64, a, a, 64, 8, a, None, 0, a, 1, 4, 8, 8, 64, None) == -1
+    assert "ldy" in _err(lib)
 
 
 def test_quantize_weight_validation_rejects_before_launch(lib):
@@ -128,10 +160,10 @@ def test_quantize_weight_validation_rejects_before_launch(lib):
 
 def test_gemm_empty_shapes_are_noops(lib):
     # M == 0 or N == 0 passes the shape checks and touches nothing (null pointers are fine)
-    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 64, 0, None, None, 8, 0, 8, 64, None) == 0
-    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 64, 0, None, None, 8, 8, 0, 64, None) == 0
-    assert lib.mq_gemm_rowscale(None, 64, None, None, 64, 8, None, None, None, 8, 0, 8, 64, None) == 0
+    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 64, 0, None, 0, None, 0, 8, 0, 8, 64, None) == 0
+    assert lib.mq_gemm_w4_group(None, 64, None, None, 32, None, 1, None, 1, 64, 0, None, 0, None, 0, 8, 8, 0, 64, None) == 0
+    assert lib.mq_gemm_rowscale(None, 64, None, None, 64, 8, None, None, 0, None, 0, 8, 0, 8, 64, None) == 0
     assert lib.mq_gemm_rowscale_acc(None, 64, None, 64, 8, None, 0, 8, 64, None) == 0
     assert lib.mq_gemm_w4_group_partials(None, 64, None, 32, None, 1, 64, 0, None, 0, 8, 64, None) == 0
     # shape checks still apply to empty products
-    assert lib.mq_gemm_w4_group(None, 96, None, None, 48, None, 1, None, 1, 64, 0, None, None, 8, 0, 8, 96, None) == -1
+    assert lib.mq_gemm_w4_group(None, 96, None, None, 48, None, 1, None, 1, 64, 0, None, 0, None, 0, 8, 0, 8, 96, None) == -1

@@ -122,7 +122,7 @@ def test_strided_input_c_abi(gpu_device):
     xw = synth.to_bf16_tensor(wide, gpu_device)
     q = torch.full((33, 1040), 99, dtype=torch.int8, device=gpu_device)   # ldq 1040 > K
     s = torch.empty(33, dtype=torch.float32, device=gpu_device)
-    _lib.call("mq_rotquant", xw.data_ptr(), 33, 1024, 1536, 256, 8, 0, q.data_ptr(), 1040, s.data_ptr(),
+    _lib.call("mq_rotquant", xw.data_ptr(), _lib.DT_BF16, 33, 1024, 1536, 256, 8, 0, q.data_ptr(), 1040, s.data_ptr(),
               _lib.stream_of(xw))
     torch.cuda.synchronize()
     q0, s0 = _oracle(xb, 256, 8)

@@ -29,7 +29,7 @@ def _plain_group(qa_d, sa_d, qw_d, s_d, z_d, bias, n, m, k, act_mode=0):
     y = torch.empty((m, n), dtype=torch.bfloat16, device=qa_d.device)
     _lib.call("mq_gemm_w4_group", qa_d.data_ptr(), qa_d.stride(0), sa_d.data_ptr(), qw_d.data_ptr(), qw_d.stride(0),
               s_d.data_ptr(), s_d.stride(0), _lib.ptr(z_d), z_d.stride(0) if z_d is not None else 0, 64, act_mode,
-              _lib.ptr(bias), y.data_ptr(), n, m, n, k, _lib.stream_of(qa_d))
+              _lib.ptr(bias), _lib.DT_BF16, y.data_ptr(), _lib.DT_BF16, n, m, n, k, _lib.stream_of(qa_d))
     return y
 
 

@@ -37,7 +37,7 @@ def test_rowscale_split_equals_unsplit(gpu_device, m, n, k):
     y_split = ops.gemm_rowscale(qa_d, sa_d, qw_d, ws_d, bias, n, 8)
     y_plain = torch.empty_like(y_split)
     _lib.call("mq_gemm_rowscale", qa_d.data_ptr(), k, sa_d.data_ptr(), qw_d.data_ptr(), k, 8, ws_d.data_ptr(),
-              bias.data_ptr(), y_plain.data_ptr(), n, m, n, k, _lib.stream_of(qa_d))
+              bias.data_ptr(), _lib.DT_BF16, y_plain.data_ptr(), _lib.DT_BF16, n, m, n, k, _lib.stream_of(qa_d))
     torch.cuda.synchronize()
     assert torch.equal(y_split, y_plain)
     acc = gemm.partials(qa, qw, k)[0].astype(np.float64)
@@ -59,7 +59,8 @@ def test_group_split_matches_oracle(gpu_device, m, n, k):
     y_split = ops.gemm_w4_group(qa_d, sa_d, qw_d, s_d, z_d, None, n)
     y_plain = torch.empty_like(y_split)
     _lib.call("mq_gemm_w4_group", qa_d.data_ptr(), k, sa_d.data_ptr(), qw_d.data_ptr(), k // 2, s_d.data_ptr(),
-              k // 64, z_d.data_ptr(), z_d.stride(0), 64, 0, None, y_plain.data_ptr(), n, m, n, k,
+              k // 64, z_d.data_ptr(), z_d.stride(0), 64, 0, None, _lib.DT_BF16, y_plain.data_ptr(), _lib.DT_BF16, n,
+              m, n, k,
               _lib.stream_of(qa_d))
     torch.cuda.synchronize()
     p = gemm.partials(qa, gemm.zero_adjusted(q, z, 64), 64)
@@ -93,7 +94,7 @@ def test_tail_rows_split(gpu_device):
     y_split = ops.gemm_rowscale(qa_d, sa_d, qw_d, ws_d, bias, n, 8)
     y_plain = torch.empty_like(y_split)
     _lib.call("mq_gemm_rowscale", qa_d.data_ptr(), k, sa_d.data_ptr(), qw_d.data_ptr(), k, 8, ws_d.data_ptr(),
-              bias.data_ptr(), y_plain.data_ptr(), n, m, n, k, _lib.stream_of(qa_d))
+              bias.data_ptr(), _lib.DT_BF16, y_plain.data_ptr(), _lib.DT_BF16, n, m, n, k, _lib.stream_of(qa_d))
     torch.cuda.synchronize()
     assert torch.equal(y_split, y_plain)
     acc = qa[rows].astype(np.float64) @ qw.astype(np.float64).T          # exact in float64
@@ -108,7 +109,8 @@ def test_tail_rows_split(gpu_device):
     y_split = ops.gemm_w4_group(qa_d, sa_d, qw_d, s_d, z_d, bias, n)
     y_plain = torch.empty_like(y_split)
     _lib.call("mq_gemm_w4_group", qa_d.data_ptr(), k, sa_d.data_ptr(), qw_d.data_ptr(), k // 2, s_d.data_ptr(),
-              k // 64, z_d.data_ptr(), z_d.stride(0), 64, 0, bias.data_ptr(), y_plain.data_ptr(), n, m, n, k,
+              k // 64, z_d.data_ptr(), z_d.stride(0), 64, 0, bias.data_ptr(), _lib.DT_BF16, y_plain.data_ptr(),
+              _lib.DT_BF16, n, m, n, k,
               _lib.stream_of(qa_d))
     torch.cuda.synchronize()
     assert gemm.rel_l2(y_plain.float().cpu().numpy(), y_split.float().cpu().numpy()) < 4e-3

@@ -80,7 +80,7 @@ def test_strided_h_c_abi(gpu_device):
     hw = synth.to_bf16_tensor(wide, gpu_device)
     q = torch.full((m, 1040), 99, dtype=torch.int8, device=gpu_device)
     s = torch.empty(m, dtype=torch.float32, device=gpu_device)
-    _lib.call("mq_swiglu_rotquant", hw.data_ptr(), m, k, 2 * k + 256, 256, 8, 0, q.data_ptr(), 1040,
+    _lib.call("mq_swiglu_rotquant", hw.data_ptr(), _lib.DT_BF16, m, k, 2 * k + 256, 256, 8, 0, q.data_ptr(), 1040,
               s.data_ptr(), _lib.stream_of(hw))
     torch.cuda.synchronize()
     q0, s0 = swiglu.swiglu_rotquant(synth.bf16_bits_to_f32(hb), 256, 8)
@@ -144,5 +144,7 @@ def test_int8_linear_input_act_swiglu(gpu_device):
                               convrot=True, convrot_groupsize=256)
     torch.cuda.synchronize()
     assert torch.equal(y, y_plain)
-    with pytest.raises(NotImplementedError):
-        ops.int8_linear(h, qw, ws, None, convrot=True, input_act="gelu_tanh")
+    # activations outside ComfyUI's INPUT_ACT_EAGER table are refused (gelu_tanh is covered in
+    # tests/test_gpu_dtypes.py)
+    with pytest.raises(ValueError, match="input_act"):
+        ops.int8_linear(h, qw, ws, None, convrot=True, input_act="relu")

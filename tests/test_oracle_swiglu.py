@@ -160,3 +160,52 @@ def test_generated_device_table_matches_oracle():
     _, g = _all_bf16()
     t = (g.view(np.uint32) >> 16) & 0x7FFF
     assert (np.abs(g[t < gen.LO]) < 2.0**-25).all() and (np.abs(g[t >= gen.HI]) >= 128).all()
+
+
+def _all_f16():
+    bits = np.arange(0x10000, dtype=np.uint32).astype(np.uint16)
+    g = bits.view(np.float16).astype(F32)
+    keep = np.isfinite(g)
+    return bits[keep], g[keep]
+
+
+def test_silu32_is_correctly_rounded_for_every_f16_gate():
+    # fp16 gates (the fp16 SwiGLU prologue): every finite pattern against exact decimal arithmetic
+    _, g = _all_f16()
+    got = swiglu.silu32(g).view(np.uint32)
+    with localcontext() as ctx:
+        ctx.prec, ctx.Emax, ctx.Emin = 60, MAX_EMAX, MIN_EMIN
+        for i in range(g.size):
+            d = Decimal(float(g[i]))
+            r = _rn32_decimal(d / (1 + (-d).exp()))
+            r |= 0x80000000 if (r == 0 and np.signbit(g[i])) else 0
+            assert got[i] == r, f"gate {g[i]!r}: {got[i]:#010x} != {r:#010x}"
+
+
+def test_swiglu_f16_product_rounding():
+    rng = np.random.default_rng(3)
+    g = (rng.standard_normal(200_000) * 3).astype(np.float16).astype(F32)
+    u = (rng.standard_normal(200_000) * 2).astype(np.float16).astype(F32)
+    got = swiglu.swiglu_f16(g, u)
+    # one fp32 rounding of silu * u, then fp16 round-to-nearest-even (numpy's float16 cast)
+    assert np.array_equal(got, (swiglu.silu32(g) * u).astype(F32).astype(np.float16).astype(F32))
+    # fp16 values, and within one fp16 step of the float64 product
+    assert np.array_equal(got, got.astype(np.float16).astype(F32))
+    exact = swiglu.silu32(g).astype(np.float64) * u.astype(np.float64)
+    assert (np.abs(got - exact) <= np.spacing(np.abs(got).astype(np.float16)).astype(np.float64)).all()
+    # the bf16 rounding is a different function on the same inputs
+    assert not np.array_equal(got, swiglu.swiglu_bf16(g, u))
+
+
+def test_generated_f16_device_table_matches_oracle():
+    # the fp16 table (one entry per 16-bit pattern) holds the oracle's silu32 of every finite gate
+    path = os.path.join(PKG_ROOT, "csrc", "gen_silu_table.py")
+    spec = importlib.util.spec_from_file_location("gen_silu_table", path)
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    tab = np.array(gen.table_f16(), np.uint32)
+    assert tab.size == 0x10000
+    bits, g = _all_f16()
+    assert np.array_equal(tab[bits.astype(np.int64)], swiglu.silu32(g).view(np.uint32))
+    # non-finite gates follow the formula in IEEE arithmetic: +inf -> +inf, -inf and NaN -> NaN
+    assert tab[0x7C00] == 0x7F800000 and np.isnan(tab[[0xFC00, 0x7E00]].view(F32)).all()
