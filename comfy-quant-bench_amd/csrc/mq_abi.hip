@@ -333,3 +333,98 @@ int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t 
 }
 
 }  // extern "C"
+
+namespace {
+
+constexpr int64_t kWsAlign = 256;
+int64_t align_up(int64_t v) { return (v + kWsAlign - 1) / kWsAlign * kWsAlign; }
+
+// Workspace layout of the whole-linear entry points: codes [M, K] int8, scales [M] fp32, then the
+// GEMM's split-K partials. `need` is what the linear cannot run without.
+struct LinearWs {
+    int64_t codes = 0, scales = 0, split = 0, need = 0, total = 0;
+};
+
+LinearWs linear_ws(int64_t M, int64_t N, int64_t K) {
+    LinearWs w;
+    w.codes = 0;
+    w.scales = align_up(M * K);
+    w.split = w.scales + align_up(M * 4);
+    w.need = w.split;
+    w.total = w.split + align_up(mq_gemm_workspace_bytes(M, N, K));
+    return w;
+}
+
+// Shared argument checks of the whole-linear entry points (the GEMM and quantizer entry points
+// check the rest); returns MQ_OK, an error, or kEmpty for a valid call with nothing to compute.
+int check_linear(const char* what, int act_bits, int swiglu, int64_t M, int64_t N, int64_t K, const void* workspace,
+                 int64_t workspace_bytes) {
+    MQ_REQUIRE(act_bits == 8 || act_bits == 4, "%s: act_bits must be 8 or 4 (got %d)", what, act_bits);
+    MQ_REQUIRE(swiglu == 0 || swiglu == 1, "%s: swiglu must be 0 or 1 (got %d)", what, swiglu);
+    MQ_REQUIRE(M >= 0 && N >= 0 && K > 0 && K % 64 == 0, "%s: bad shape M=%lld N=%lld K=%lld (K %% 64 == 0)", what,
+               (long long)M, (long long)N, (long long)K);
+    MQ_REQUIRE(M < (int64_t(1) << 31), "%s: M too large", what);
+    if (M == 0 || N == 0) return kEmpty;
+    const LinearWs w = linear_ws(M, N, K);
+    MQ_REQUIRE(workspace && aligned(workspace, kWsAlign),
+               "%s: workspace must be non-null and 256-byte aligned", what);
+    MQ_REQUIRE(workspace_bytes >= w.need, "%s: workspace of %lld bytes is below the %lld the codes and scales need",
+               what, (long long)workspace_bytes, (long long)w.need);
+    return MQ_OK;
+}
+
+int quantize_into(const void* x, int x_dtype, int64_t ldx, int hblock, int act_bits, int swiglu, int layout,
+                  int64_t M, int64_t K, uint8_t* ws_base, void* stream) {
+    const LinearWs w = linear_ws(M, 1, K);
+    void* q = ws_base + w.codes;
+    float* s = reinterpret_cast<float*>(ws_base + w.scales);
+    return swiglu ? mq_swiglu_rotquant(x, x_dtype, M, K, ldx, hblock, act_bits, layout, q, K, s, stream)
+                  : mq_rotquant(x, x_dtype, M, K, ldx, hblock, act_bits, layout, q, K, s, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t mq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    return linear_ws(M, N, K).total;
+}
+
+int mq_linear_w4_group(const void* x, int x_dtype, int64_t ldx, int hblock, int act_bits, int swiglu,
+                       const uint8_t* qw, int64_t ldw, const uint16_t* ws, int64_t ldws, const uint8_t* wz,
+                       int64_t ldwz, const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy, int64_t M,
+                       int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = check_linear("linear_w4_group", act_bits, swiglu, M, N, K, workspace, workspace_bytes);
+    if (rc) return rc == kEmpty ? MQ_OK : rc;
+    // int4 activations enter the group GEMM in its x16 operand layout
+    const int layout = act_bits == 4 ? MQ_Q_X16ALT : MQ_Q_BYTES;
+    const int act_mode = act_bits == 4 ? MQ_ACT_X16ALT : MQ_ACT_I8;
+    auto* base = static_cast<uint8_t*>(workspace);
+    rc = quantize_into(x, x_dtype, ldx, hblock, act_bits, swiglu, layout, M, K, base, stream);
+    if (rc) return rc;
+    const LinearWs w = linear_ws(M, N, K);
+    return mq_gemm_w4_group_ws(reinterpret_cast<const int8_t*>(base + w.codes), K,
+                               reinterpret_cast<const float*>(base + w.scales), qw, ldw, ws, ldws, wz, ldwz, 64,
+                               act_mode, bias, bias_dtype, y, y_dtype, ldy, M, N, K, base + w.split,
+                               workspace_bytes - w.split, stream);
+}
+
+int mq_linear_rowscale(const void* x, int x_dtype, int64_t ldx, int hblock, int act_bits, int swiglu, const void* qw,
+                       int64_t ldw, int wbits, const float* ws, const void* bias, int bias_dtype, void* y,
+                       int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace,
+                       int64_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = check_linear("linear_rowscale", act_bits, swiglu, M, N, K, workspace, workspace_bytes);
+    if (rc) return rc == kEmpty ? MQ_OK : rc;
+    auto* base = static_cast<uint8_t*>(workspace);
+    rc = quantize_into(x, x_dtype, ldx, hblock, act_bits, swiglu, MQ_Q_BYTES, M, K, base, stream);
+    if (rc) return rc;
+    const LinearWs w = linear_ws(M, N, K);
+    return mq_gemm_rowscale_ws(reinterpret_cast<const int8_t*>(base + w.codes), K,
+                               reinterpret_cast<const float*>(base + w.scales), qw, ldw, wbits, ws, bias, bias_dtype,
+                               y, y_dtype, ldy, M, N, K, base + w.split, workspace_bytes - w.split, stream);
+}
+
+}  // extern "C"

@@ -42,6 +42,11 @@ _SIGNATURES = {
     "mq_gemm_rowscale_ws": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_int, c_vp, c_int, c_i64, c_i64,
                              c_i64, c_i64, c_vp, c_i64, c_vp], c_int),
     "mq_gemm_rowscale_acc": ([c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_vp], c_int),
+    "mq_linear_workspace_bytes": ([c_i64, c_i64, c_i64], c_i64),
+    "mq_linear_w4_group": ([c_vp, c_int, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp,
+                            c_int, c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp], c_int),
+    "mq_linear_rowscale": ([c_vp, c_int, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_int, c_vp, c_vp, c_int, c_vp,
+                            c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp], c_int),
 }
 
 EXPORTED = tuple(_SIGNATURES)
@@ -100,5 +105,11 @@ def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
+    """hipStream_t of torch's current stream on t's device (the stream every op enqueues on)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream

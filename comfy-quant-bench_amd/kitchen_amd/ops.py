@@ -182,8 +182,14 @@ def decode_w4a8_codebook_weight(qdata: torch.Tensor, s_rel: torch.Tensor, s_chan
 def _check_w4_group(qa, qweight, wscales, wzeros, n, group_size):
     """Buffer-size checks the C ABI cannot do (it sees raw pointers)."""
     m, k = qa.shape
-    if qa.dtype != torch.int8 or qweight.shape != (n, k // 2) or qweight.element_size() != 1:
-        raise ValueError(f"qa must be int8 [M, K] and qweight 8-bit [{n}, {k // 2}]")
+    if qa.dtype != torch.int8:
+        raise ValueError("qa must be int8 [M, K]")
+    _check_w4_group_weights(qweight, wscales, wzeros, n, k, group_size)
+
+
+def _check_w4_group_weights(qweight, wscales, wzeros, n, k, group_size):
+    if qweight.shape != (n, k // 2) or qweight.element_size() != 1:
+        raise ValueError(f"qweight must be 8-bit [{n}, {k // 2}]")
     groups = k // group_size
     if wscales is not None and (wscales.dtype != torch.float16 or wscales.shape[0] != n
                                 or wscales.shape[1] < groups or wscales.stride(1) != 1):
@@ -205,6 +211,17 @@ def _workspace(m: int, n: int, k: int, device):
         with torch.cuda.device(device):
             nbytes = _WS_BYTES[key] = int(_lib.load().mq_gemm_workspace_bytes(m, n, k))
     return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes > 0 else None
+
+
+def _linear_workspace(m: int, n: int, k: int, device) -> torch.Tensor:
+    """Workspace of the whole-linear entry points (activation codes, scales and split-K partials),
+    its size asked of the library once per shape and device."""
+    key = ("linear", device.index, m, n, k)
+    nbytes = _WS_BYTES.get(key)
+    if nbytes is None:
+        with torch.cuda.device(device):
+            nbytes = _WS_BYTES[key] = int(_lib.load().mq_linear_workspace_bytes(m, n, k))
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
 def _bias_args(bias):
@@ -292,20 +309,62 @@ def convrot_w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.T
     if wscales.dim() == 2 and wscales.shape[1] > 1:
         if wscales.shape != (n, k // quant_group_size):
             raise ValueError(f"per-group wscales must be [{n}, {k // quant_group_size}], got {list(wscales.shape)}")
-        # int4 activations go to the group GEMM in its x16 operand layout
-        layout = _lib.Q_X16ALT if bits == 4 else _lib.Q_BYTES
-        qa, sa = rotate_quantize(x, convrot_groupsize, bits, layout, swiglu)
         ws = wscales.to(torch.float16).contiguous()
-        act = _lib.ACT_X16ALT if bits == 4 else _lib.ACT_I8
-        y = gemm_w4_group(qa, sa, qweight.contiguous(), ws, None, _bias(bias, n, qa.device), n, quant_group_size, act,
-                          out_dtype)
+        y = _linear_w4_group(x, swiglu, convrot_groupsize, bits, qweight, ws, None, bias, n, k, out_dtype)
     else:
         ws = wscales.reshape(-1).to(torch.float32).contiguous()
         if ws.numel() != n:
             raise ValueError(f"per-row wscales must have {n} elements, got {ws.numel()}")
-        qa, sa = rotate_quantize(x, convrot_groupsize, bits, swiglu=swiglu)
-        y = gemm_rowscale(qa, sa, qweight.contiguous(), ws, _bias(bias, n, qa.device), n, 4, out_dtype)
+        y = _linear_rowscale(x, swiglu, convrot_groupsize, bits, qweight, 4, ws, bias, n, k, out_dtype)
     return _finish(y, x_out, n)
+
+
+def _linear_input(x: torch.Tensor, swiglu: bool, k: int):
+    """(x as [M, width] for the whole-linear entry points, fused SwiGLU?): fp32 gate | up pairs are
+    formed eagerly (the fused prologue takes bf16 / fp16, as the reference's does)."""
+    if swiglu and x.dtype == torch.float32:
+        x, swiglu = _swiglu_eager(x), False
+    x2 = _as_2d(x, 2 * k if swiglu else k)
+    return x2, swiglu
+
+
+def _linear_w4_group(x, swiglu, cg, act_bits, qweight, wscales, wzeros, bias, n, k, out_dtype):
+    """rotate + quantize + group GEMM in one library call (mq_linear_w4_group)."""
+    x2, swiglu = _linear_input(x, swiglu, k)
+    m = x2.shape[0]
+    qw = qweight.contiguous()
+    zz = None if wzeros is None else wzeros.contiguous()
+    _check_w4_group_weights(qw, wscales, zz, n, k, INT4_GROUP_SIZE)
+    b = _bias(bias, n, x2.device)
+    y = torch.empty((m, n), dtype=out_dtype, device=x2.device)
+    if m == 0:
+        return y
+    work = _linear_workspace(m, n, k, x2.device)
+    _lib.call("mq_linear_w4_group", x2.data_ptr(), _lib.dtype_code(x2.dtype), x2.stride(0), int(cg or 0),
+              int(act_bits), int(swiglu), qw.data_ptr(), qw.stride(0), wscales.data_ptr(), wscales.stride(0),
+              _lib.ptr(zz), 0 if zz is None else zz.stride(0), *_bias_args(b), y.data_ptr(),
+              _lib.dtype_code(out_dtype), y.stride(0), m, n, k, work.data_ptr(), work.numel(), _lib.stream_of(x2))
+    return y
+
+
+def _linear_rowscale(x, swiglu, cg, act_bits, qweight, wbits, wscales, bias, n, k, out_dtype):
+    """rotate + quantize + row-scale GEMM in one library call (mq_linear_rowscale)."""
+    x2, swiglu = _linear_input(x, swiglu, k)
+    m = x2.shape[0]
+    qw = qweight.contiguous()
+    wbytes = k // 2 if wbits == 4 else k
+    if qw.shape != (n, wbytes) or qw.element_size() != 1:
+        raise ValueError(f"weight must be 8-bit [{n}, {wbytes}]")
+    b = _bias(bias, n, x2.device)
+    y = torch.empty((m, n), dtype=out_dtype, device=x2.device)
+    if m == 0:
+        return y
+    work = _linear_workspace(m, n, k, x2.device)
+    _lib.call("mq_linear_rowscale", x2.data_ptr(), _lib.dtype_code(x2.dtype), x2.stride(0), int(cg or 0),
+              int(act_bits), int(swiglu), qw.data_ptr(), qw.stride(0), int(wbits), wscales.data_ptr(), *_bias_args(b),
+              y.data_ptr(), _lib.dtype_code(out_dtype), y.stride(0), m, n, k, work.data_ptr(), work.numel(),
+              _lib.stream_of(x2))
+    return y
 
 
 # Shipped asym_w4a8_int8 weights decoded to (int8 [N, K], row scale [N]) once per weight: one entry
@@ -354,9 +413,10 @@ def int8_rowscale_linear(x, q8, row_scale, bias=None, out_dtype=None, convrot_gr
         raise ValueError(f"Input K={k} does not match weight K={q8.shape[1]}")
     if convrot_groupsize and k % convrot_groupsize:
         raise ValueError(f"Input K={k} is not divisible by convrot_groupsize={convrot_groupsize}")
-    qa, sa = rotate_quantize(x, convrot_groupsize, 8, swiglu=swiglu)
     ws = row_scale.reshape(-1).to(torch.float32).contiguous()
-    y = gemm_rowscale(qa, sa, q8.contiguous(), ws, _bias(bias, n, qa.device), n, 8, _out_dtype(out_dtype, x_out))
+    if ws.numel() != n:
+        raise ValueError(f"row scale must have {n} elements, got {ws.numel()}")
+    y = _linear_rowscale(x, swiglu, convrot_groupsize, 8, q8, 8, ws, bias, n, k, _out_dtype(out_dtype, x_out))
     return _finish(y, x_out, n)
 
 
@@ -394,11 +454,10 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
         raise ValueError(f"s_rel must be [{n}, {k // group_size}], got {list(s_rel.shape)}")
     if correction is not None and correction.shape != (n, (k // group_size + 1) // 2):
         raise ValueError(f"correction (zero-points) must be [{n}, {(k // group_size + 1) // 2}]")
-    qa, sa = rotate_quantize(x, convrot_groupsize, 8)
-    qw = qdata.view(torch.uint8).contiguous()
-    zz = correction.view(torch.uint8).contiguous() if correction is not None else None
-    y = gemm_w4_group(qa, sa, qw, s_rel.contiguous(), zz, _bias(bias, n, qa.device), n, group_size,
-                      out_dtype=_out_dtype(out_dtype, x))
+    qw = qdata.view(torch.uint8)
+    zz = correction.view(torch.uint8) if correction is not None else None
+    y = _linear_w4_group(x, False, convrot_groupsize, 8, qw, s_rel.contiguous(), zz, bias, n, k,
+                         _out_dtype(out_dtype, x))
     return _finish(y, x, n)
 
 

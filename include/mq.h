@@ -250,6 +250,36 @@ int mq_gemm_rowscale_ws(const int8_t* qa, int64_t lda, const float* sa, const vo
 int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t ldw, int wbits,
                          int32_t* acc, int64_t M, int64_t N, int64_t K, void* stream);
 
+/*
+ * Whole linears: rotate + quantize x (or the SwiGLU pair h), then the GEMM, in one call. The
+ * activation codes and scales live in the caller's workspace; the kernels, arithmetic and results
+ * are those of mq_rotquant / mq_swiglu_rotquant followed by mq_gemm_w4_group_ws / mq_gemm_rowscale_ws.
+ *
+ * mq_linear_w4_group replaces w4a8_int8_linear (configs' uint4 asymmetric scheme, act_bits 8,
+ * tools/test_verify_formats.py:375-383) and convrot_w4a4_linear with per-group fp16 weight scales
+ * (act_bits 4 or 8, patches/comfy_kitchen_swiglu_w4a4_fused.patch:41-67); mq_linear_rowscale
+ * replaces int8_linear (tools/verify_w4a4.py:342-370, wbits 8) and convrot_w4a4_linear with the
+ * shipped per-row F32 scale (wbits 4).
+ *
+ *   x       [M, K] (swiglu = 0) or gate | up [M, 2K] (swiglu = 1) of type x_dtype, stride ldx
+ *   hblock  Hadamard block (0, 16, 64, 256); act_bits 8 or 4 (per-token int8 / int4 activations)
+ *   weights, scales, bias, y as mq_gemm_w4_group / mq_gemm_rowscale
+ *   workspace  device memory, 256-byte aligned: the codes [M, K] and scales [M] first (both
+ *           required), then the split-K partials when the shape wants them and they fit;
+ *           mq_linear_workspace_bytes(M, N, K) gives the size that holds all of it.
+ */
+int64_t mq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+int mq_linear_w4_group(const void* x, int x_dtype, int64_t ldx, int hblock, int act_bits, int swiglu,
+                       const uint8_t* qw, int64_t ldw, const uint16_t* ws, int64_t ldws, const uint8_t* wz,
+                       int64_t ldwz, const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy, int64_t M,
+                       int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream);
+
+int mq_linear_rowscale(const void* x, int x_dtype, int64_t ldx, int hblock, int act_bits, int swiglu, const void* qw,
+                       int64_t ldw, int wbits, const float* ws, const void* bias, int bias_dtype, void* y,
+                       int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

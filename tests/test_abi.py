@@ -167,3 +167,32 @@ def test_gemm_empty_shapes_are_noops(lib):
     assert lib.mq_gemm_w4_group_partials(None, 64, None, 32, None, 1, 64, 0, None, 0, 8, 64, None) == 0
     # shape checks still apply to empty products
     assert lib.mq_gemm_w4_group(None, 96, None, None, 48, None, 1, None, 1, 64, 0, None, 0, None, 0, 8, 0, 8, 96, None) == -1
+
+
+def test_linear_validation_rejects_before_launch(lib):
+    # (x, x_dtype, ldx, hblock, act_bits, swiglu, qw, ldw, ws, ldws, wz, ldwz, bias, bias_dtype, y,
+    #  y_dtype, ldy, M, N, K, workspace, workspace_bytes, stream); fake aligned addresses are never
+    # dereferenced: every case fails validation first
+    a = 1 << 20
+    need = 64 * 3072 + 256          # codes [64, 3072] and scales [64] (rounded up to 256 bytes)
+    assert lib.mq_linear_workspace_bytes(64, 1024, 3072) >= need
+    assert lib.mq_linear_workspace_bytes(0, 1024, 3072) == 0
+    args = [a, 0, 3072, 256, 8, 0, a, 1536, a, 48, None, 0, None, 0, a, 0, 1024, 64, 1024, 3072, a, need, None]
+
+    def call(**kw):
+        names = ["x", "x_dtype", "ldx", "hblock", "act_bits", "swiglu", "qw", "ldw", "ws", "ldws", "wz", "ldwz",
+                 "bias", "bias_dtype", "y", "y_dtype", "ldy", "M", "N", "K", "workspace", "workspace_bytes", "stream"]
+        v = dict(zip(names, args))
+        v.update(kw)
+        return lib.mq_linear_w4_group(*[v[n] for n in names])
+
+    assert call(act_bits=6) == -1 and "act_bits" in _err(lib)
+    assert call(swiglu=2) == -1 and "swiglu" in _err(lib)
+    assert call(K=3000) == -1 and "K % 64" in _err(lib)
+    assert call(workspace=None) == -1 and "workspace" in _err(lib)
+    assert call(workspace=a + 16) == -1 and "256-byte" in _err(lib)
+    assert call(workspace_bytes=need - 1) == -1 and "codes and scales" in _err(lib)
+    assert call(M=0) == 0 and call(N=0) == 0            # valid no-ops
+    assert lib.mq_linear_rowscale(a, 0, 3072, 256, 5, 0, a, 3072, 8, a, None, 0, a, 0, 1024, 64, 1024, 3072, a,
+                                  need, None) == -1
+    assert "act_bits" in _err(lib)
