@@ -2,9 +2,11 @@
 // reporting and dispatch to the kernel launchers. Nothing here allocates device memory.
 #include "../../include/mq.h"
 
+#include <algorithm>
 #include <atomic>
 #include <cstdarg>
 #include <cstring>
+#include <mutex>
 
 #include "mq_internal.h"
 
@@ -428,3 +430,74 @@ int mq_linear_rowscale(const void* x, int x_dtype, int64_t ldx, int hblock, int 
 }
 
 }  // extern "C"
+
+// ---- The whole W4 group linear without a caller workspace (mq_linear_w4_group_noalloc): its codes,
+// scales and split-K partials go to a fixed device array instead. Each GPU the library runs on
+// holds its own copy of the array until the process ends. The host-side name `scratch` is only a
+// stand-in for the symbol: its device address on the current GPU comes from hipGetSymbolAddress,
+// taken once per device and kept.
+namespace mq {
+
+constexpr int64_t kScratchBytes = MQ_NOALLOC_SCRATCH_BYTES;
+__device__ __attribute__((aligned(256))) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of the current GPU's scratch array (looked up on its first use on that GPU).
+int scratch_on_current_device(const char* what, void** out) {
+    int dev = 0;
+    const hipError_t ed = hipGetDevice(&dev);
+    if (ed != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+        set_error("%s: no usable current device (%s)", what, hipGetErrorString(ed));
+        return MQ_ELAUNCH;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            set_error("%s: cannot find the scratch array on device %d: %s", what, dev, hipGetErrorString(e));
+            return MQ_ELAUNCH;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MQ_OK;
+}
+
+}  // namespace
+}  // namespace mq
+
+extern "C" {
+
+int mq_linear_w4_group_noalloc(const void* x, int x_dtype, int64_t ldx, int hblock, int act_bits, int swiglu,
+                               const uint8_t* qw, int64_t ldw, const uint16_t* ws, int64_t ldws, const uint8_t* wz,
+                               int64_t ldwz, const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy,
+                               int64_t M, int64_t N, int64_t K, void* stream) {
+    clear_error();
+    if (M > 0 && N > 0 && K > 0) {
+        const LinearWs w = linear_ws(M, N, K);
+        if (w.need > kScratchBytes) {
+            set_error("linear_w4_group_noalloc: the codes and scales of M=%lld K=%lld need %lld bytes, more than "
+                      "the fixed scratch of %lld bytes",
+                      (long long)M, (long long)K, (long long)w.need, (long long)kScratchBytes);
+            return MQ_EINVAL;
+        }
+        void* ptr = nullptr;
+        const int rc = scratch_on_current_device("linear_w4_group_noalloc", &ptr);
+        if (rc) return rc;
+        return mq_linear_w4_group(x, x_dtype, ldx, hblock, act_bits, swiglu, qw, ldw, ws, ldws, wz, ldwz, bias,
+                                  bias_dtype, y, y_dtype, ldy, M, N, K, ptr, std::min(w.total, kScratchBytes),
+                                  stream);
+    }
+    // empty or invalid shapes: the ordinary entry point's checks and messages (nothing is launched)
+    return mq_linear_w4_group(x, x_dtype, ldx, hblock, act_bits, swiglu, qw, ldw, ws, ldws, wz, ldwz, bias, bias_dtype,
+                              y, y_dtype, ldy, M, N, K, nullptr, 0, stream);
+}
+
+}  // extern "C"
+

@@ -47,6 +47,8 @@ _SIGNATURES = {
                             c_int, c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp], c_int),
     "mq_linear_rowscale": ([c_vp, c_int, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_int, c_vp, c_vp, c_int, c_vp,
                             c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp], c_int),
+    "mq_linear_w4_group_noalloc": ([c_vp, c_int, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64,
+                                    c_vp, c_int, c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_vp], c_int),
 }
 
 EXPORTED = tuple(_SIGNATURES)
@@ -55,6 +57,7 @@ EXPORTED = tuple(_SIGNATURES)
 Q_BYTES, Q_PACKED, Q_X16ALT = 0, 1, 2
 ACT_I8, ACT_I4, ACT_X16ALT = 0, 1, 2
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
+NOALLOC_SCRATCH_BYTES = 64 << 20   # MQ_NOALLOC_SCRATCH_BYTES
 DTYPE_CODE = {torch.bfloat16: DT_BF16, torch.float16: DT_F16, torch.float32: DT_F32}
 
 

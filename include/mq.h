@@ -280,6 +280,26 @@ int mq_linear_rowscale(const void* x, int x_dtype, int64_t ldx, int hblock, int 
                        int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace,
                        int64_t workspace_bytes, void* stream);
 
+/* Size of the fixed per-device scratch array behind mq_linear_w4_group_noalloc. */
+#define MQ_NOALLOC_SCRATCH_BYTES (64ll << 20)
+
+/*
+ * mq_linear_w4_group without a workspace argument: it allocates nothing (no hipMalloc, no
+ * allocating library call). No counterpart in the reference; it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * it). The activation codes, scales and split-K partials go to a fixed array of
+ * MQ_NOALLOC_SCRATCH_BYTES in device memory that each GPU the library runs on holds until the
+ * process ends; a call whose codes and scales (about M * K + 4 * M bytes) do not fit returns
+ * MQ_EINVAL, and split-K partials are used only where they fit beside them. Results equal
+ * mq_linear_w4_group's. Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (several streams or threads) race and must be serialized by the caller. Nothing in the array
+ * needs to start at zero: each call writes every byte it reads.
+ */
+int mq_linear_w4_group_noalloc(const void* x, int x_dtype, int64_t ldx, int hblock, int act_bits, int swiglu,
+                               const uint8_t* qw, int64_t ldw, const uint16_t* ws, int64_t ldws, const uint8_t* wz,
+                               int64_t ldwz, const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy,
+                               int64_t M, int64_t N, int64_t K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
