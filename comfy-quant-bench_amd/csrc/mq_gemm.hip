@@ -275,7 +275,8 @@ int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     const bool zs_aligned =
         (wk != WKind::U4Asym || (a.ldwz % 2 == 0 && reinterpret_cast<uintptr_t>(a.wz) % 2 == 0)) &&
         (epi != Epi::GroupScale || (a.ldws % 2 == 0 && reinterpret_cast<uintptr_t>(a.ws16) % 4 == 0));
-    if (a.M > 128 && fits32 && zs_aligned && a.act_mode != 1) {
+    // (K >= 192: the wide kernel's last-row load correction needs at least three K groups)
+    if (a.M > 128 && a.K >= 192 && fits32 && zs_aligned && a.act_mode != 1) {
         GemmArgs w = a;
         w.ksplit = 1;
         if (a.work && (epi == Epi::GroupScale || epi == Epi::RowScale)) {

@@ -310,10 +310,28 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // bits 4u .. 4u + 3), sq the fp16 scales of groups b4 + 2 bhalf and b4 + 2 bhalf + 1. Groups
     // past the last one read zero or another row's values; their scales are zeroed at the store
     // and their activations are zero.
-    uint32_t zq = 0u, sq = 0u;
+    // The tile's last weight row has nothing after its ceil(G/2) zero-point bytes and G scales
+    // inside the resource range (the range check covers the vector offset only): in the block that
+    // runs past G (G % 4 != 0) that row's loads move back to end at the row's end (or, for a scale
+    // pair wholly past G, fail the range check), and the bytes they want are shifted down after
+    // the load (zsh, ssh bits). The host keeps G >= 3 on this kernel, so moving back stays inside
+    // the row.
+    const bool last_row = brow == rows_n - 1;
+    uint32_t zq = 0u, sq = 0u, zsh = 0u, ssh = 0u;
     auto gload_zs = [&](int b4) {
-        if constexpr (WK == WKind::U4Asym) zq = asm_ld16(b4 < G ? dz : d_none, z_off, b4 < G ? b4 >> 1 : 0);
-        if constexpr (EPI == Epi::GroupScale) sq = asm_ld32(b4 < G ? ds : d_none, s_off, soff(b4, 2));
+        if constexpr (WK == WKind::U4Asym) {
+            const bool back = last_row && b4 / 2 + 2 > (G + 1) / 2;
+            zsh = back ? 8u : 0u;
+            const int zv = z_off == kOob ? kOob : z_off - (back ? 1 : 0);
+            zq = asm_ld16(b4 < G ? dz : d_none, zv, b4 < G ? b4 >> 1 : 0);
+        }
+        if constexpr (EPI == Epi::GroupScale) {
+            const int ga = b4 + 2 * bhalf;   // first group of this thread's scale pair
+            const bool none = last_row && ga >= G, back = last_row && ga + 1 == G;
+            ssh = back ? 16u : 0u;
+            const int sv = s_off == kOob || none ? kOob : s_off - (back ? 2 : 0);
+            sq = asm_ld32(b4 < G ? ds : d_none, sv, soff(b4, 2));
+        }
     };
     // Wait until at most N VMEM operations are outstanding; register set SET counts as written by
     // the wait, so no use of it moves above it.
@@ -331,7 +349,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             constexpr bool x16 = AM == 2 && kGroup;
             constexpr bool nw = neg && AM != 2;
             constexpr int pos = decltype(Uc)::value;
-            const uint32_t c = unpack_const<WK, nw>((zq >> (4 * pos)) & 0xfu);
+            const uint32_t c = unpack_const<WK, nw>((zq >> (zsh + 4 * pos)) & 0xfu);
             uint4 u;
             const uint32_t w0 = h ? rb[set].z : rb[set].x, w1 = h ? rb[set].w : rb[set].y;
             unpack_dword<WK, nw, x16>(w0, c, u.x, u.y);
@@ -345,7 +363,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             constexpr bool neg = decltype(PARc)::value == 1;
             constexpr int u = decltype(Uc)::value;
             if (bhalf == (u >> 1)) {
-                float sv = f16_bits_to_f32(static_cast<uint16_t>(sq >> (16 * (u & 1)))) * kSfac;   // exact
+                const uint32_t sh = ssh + 16u * (u & 1);
+                float sv = f16_bits_to_f32(static_cast<uint16_t>(sh < 32u ? sq >> sh : 0u)) * kSfac;   // exact
                 sv = g >= g0 && g < gend ? (neg ? -sv : sv) : 0.0f;
                 ds_write4(s_st, st * TN * 4, sv);
                 cs += sv;
@@ -778,7 +797,7 @@ int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
 
 int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups) {
     *kgroups = 0;
-    if (M <= 128 || K % TK) return 1;                           // the 128-tile kernel has no split
+    if (M <= 128 || K < 192 || K % TK) return 1;               // the 128-tile kernel has no split
     const int cus = device_cu_count();
     if (cus <= 0) return 1;
     const int64_t tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);

@@ -8,6 +8,10 @@ callables.
   and fails on a FakeTensor data pointer). Namespace `kitchen_amd`; idempotent.
 * `install_backend(ck)` sets the drop-in ops on a comfy-kitchen-like namespace (ComfyUI calls
   `quant_ops.ck.<op>(...)` with keyword arguments, `patches/comfyui_swiglu_triton_env.patch:88-95`).
+* `install_compile_support(base)` gives comfy-kitchen's `QuantizedTensor` the other two
+  torch.compile fixes of `compile_support.py`: a stable hash for PT2's cache (`:38-72`) and a
+  `__tensor_unflatten__` that honours the outer size and stride torch.compile passes under dynamic
+  shapes (`:120-165`).
 * `layer_linear(tensors, config)` maps one layer's tensors and its `_quantization_metadata` entry
   (`tools/_formats.py:109-111`, `tools/verify_w4a4.py:205-212`) to the op the loader would call,
   with the loader's constants (`quant_group_size=64`, `linear_dtype="int4"`,
@@ -15,6 +19,7 @@ callables.
 """
 from __future__ import annotations
 
+import dataclasses
 import json
 from pathlib import Path
 from typing import Callable
@@ -85,6 +90,59 @@ def register_custom_ops() -> dict[str, Callable]:
     _registered.update(convrot_w4a4_linear=convrot_w4a4_linear, w4a8_int8_linear=w4a8_int8_linear,
                        int8_linear=int8_linear)
     return dict(_registered)
+
+
+def install_compile_support(kitchen_base=None) -> dict:
+    """Patch `comfy_kitchen.tensor.base.QuantizedTensor` (or the given module's) for torch.compile;
+    idempotent. Returns {"stable_hash": patched now?, "dynamic_shapes": patched now?}."""
+    if kitchen_base is None:
+        import comfy_kitchen.tensor.base as kitchen_base  # noqa: PLC0415 - only inside a ComfyUI process
+    qt = kitchen_base.QuantizedTensor
+    done = {"stable_hash": False, "dynamic_shapes": False}
+
+    if not hasattr(qt, "_stable_hash_for_caching"):
+        def _stable_hash_for_caching(self) -> str:
+            # everything that changes the traced graph: layout, storage and logical type and shape,
+            # and the layout parameters that are not tensors
+            p = self._params
+            parts = [str(self._layout_cls), str(self._qdata.dtype), str(tuple(self._qdata.shape)),
+                     str(p.orig_dtype), str(tuple(p.orig_shape))]
+            parts += [f"{f.name}={getattr(p, f.name)!r}" for f in dataclasses.fields(p)
+                      if f.name not in ("orig_dtype", "orig_shape")
+                      and not isinstance(getattr(p, f.name), torch.Tensor)]
+            return "|".join(parts)
+
+        qt._stable_hash_for_caching = _stable_hash_for_caching
+        done["stable_hash"] = True
+
+    if not getattr(qt, "_kitchen_amd_dynamic_shapes", False):
+        def __new__(cls, qdata, layout_cls, params, outer_stride=None):
+            return torch.Tensor._make_wrapper_subclass(cls, params.orig_shape, strides=outer_stride,
+                                                       device=qdata.device, dtype=params.orig_dtype,
+                                                       requires_grad=False)
+
+        def __init__(self, qdata, layout_cls, params, outer_stride=None):
+            self._qdata = qdata
+            self._layout_cls = layout_cls
+            self._params = params
+
+        def __tensor_unflatten__(inner_tensors, ctx, outer_size, outer_stride):
+            fields = dict(ctx["non_tensor_fields"])
+            fields.update({name: inner_tensors[attr] for name, attr in ctx["tensor_fields"].items()})
+            params = ctx["params_class"](**fields)
+            # torch.compile passes the (possibly symbolic) size and stride the rebuilt tensor must
+            # report; other callers pass scalar placeholders meaning "keep the stored shape"
+            if isinstance(outer_size, (tuple, list, torch.Size)):
+                params = dataclasses.replace(params, orig_shape=tuple(outer_size))
+                return qt(inner_tensors["_qdata"], ctx["layout_cls"], params, outer_stride=outer_stride)
+            return qt(inner_tensors["_qdata"], ctx["layout_cls"], params)
+
+        qt.__new__ = __new__
+        qt.__init__ = __init__
+        qt.__tensor_unflatten__ = staticmethod(__tensor_unflatten__)
+        qt._kitchen_amd_dynamic_shapes = True
+        done["dynamic_shapes"] = True
+    return done
 
 
 BACKEND_OPS = ("convrot_w4a4_linear", "w4a8_int8_linear", "int8_linear")

@@ -1,0 +1,114 @@
+"""Host-side model of the 256 x 256-tile GEMM's global loads (comfy-quant-bench_amd/csrc/
+mq_gemm_wide.hip): for every workgroup, thread role and K group of a launch, the buffer resource
+(base row, byte range), the per-lane vector offset and the wave-uniform scalar offset each load
+uses, restated from the kernel's index arithmetic. Asserts that every load either fails the
+hardware range check on its vector offset (rows past M / N: offset 0x80000000; groups past the
+last: a zero-byte resource), so it returns zeros without touching memory, or reads bytes that lie
+wholly inside its resource range, scalar offset included (the range check does not cover the
+scalar offset). Ragged M and N, K / 64 mod 4 in {0, 1, 2, 3}, split-K slices. CPU only."""
+import itertools
+
+import numpy as np
+import pytest
+
+TM = TN = 256
+TK = 64
+KOOB = 0x80000000
+
+
+def _loads(M, N, K, ldwz, ldws, kgroups=None, slices=1):
+    """Yield (what, range_bytes, voff, soff, width) for every load lane of a launch (vectorised over
+    lanes with numpy where the arithmetic is per lane)."""
+    G = K // TK
+    G4 = (G + 3) // 4 * 4
+    tiles_m, tiles_n = -(-M // TM), -(-N // TN)
+    lda, ldw = K, K // 2
+    tid = np.arange(512)
+    wave, lane = tid >> 6, tid & 63
+    for tm, tn, s in itertools.product(range(tiles_m), range(tiles_n), range(slices)):
+        m0, n0 = tm * TM, tn * TN
+        rows_m, rows_n = min(TM, M - m0), min(TN, N - n0)
+        g0 = s * kgroups if slices > 1 else 0
+        g1 = min(g0 + kgroups, G4) if slices > 1 else G4
+        ra = (rows_m - 1) * lda + K
+        rb = (rows_n - 1) * ldw + K // 2
+        rz = (rows_n - 1) * ldwz + (G + 1) // 2
+        rs = ((rows_n - 1) * ldws + G) * 2
+        # A DMA: wave w copies rows 32 w + 16 h + lane / 4, chunk lane % 4 (swizzled)
+        dma = []
+        for h in range(2):
+            r = 32 * wave + 16 * h + (lane >> 2)
+            c = (lane & 3) ^ ((r >> 1) & 3)
+            dma.append(np.where(r < rows_m, r * lda + c * 16, KOOB))
+        brow, bhalf = tid >> 1, tid & 1
+        b_ok = brow < rows_n
+        b_off = np.where(b_ok, brow * ldw + bhalf * 16, KOOB)
+        z_off = np.where(b_ok, brow * ldwz, KOOB)
+        s_off = np.where(b_ok, brow * ldws * 2 + 4 * bhalf, KOOB)
+        last = brow == rows_n - 1
+        for g in range(g0, g1):
+            live = g < G
+            for h in range(2):
+                yield "A", ra if live else 0, dma[h], g * TK if live else 0, 16
+            yield "B", rb if live else 0, b_off, g * (TK // 2) if live else 0, 16
+            if g % 4 == 0:
+                b4 = g
+                # zero-points of groups b4 .. b4 + 3 (two bytes) and scales of b4 + 2 bhalf,
+                # b4 + 2 bhalf + 1 (four bytes); the tile's last weight row ends at its last valid
+                # byte, so in a block past G its loads move back and their bytes are shifted down
+                zb = (G + 1) // 2
+                z_back = np.where(last & (b4 // 2 + 2 > zb), 1, 0)
+                ga = b4 + 2 * bhalf
+                s_voff = np.where(last & (ga >= G), KOOB,
+                                  np.where(last & (ga + 1 == G), s_off - 2, s_off))
+                s_voff = np.where(s_off == KOOB, KOOB, s_voff)
+                z_voff = np.where(z_off == KOOB, KOOB, z_off - z_back)
+                yield "Z", rz if live else 0, z_voff, (b4 >> 1) if live else 0, 2
+                yield "S", rs if live else 0, s_voff, 2 * b4 if live else 0, 4
+
+
+def _check(M, N, K, ldwz=None, ldws=None, kgroups=None, slices=1, loads=None):
+    G = K // TK
+    ldwz = ldwz if ldwz is not None else ((G + 1) // 2 + 1) // 2 * 2   # the wide kernel needs even strides
+    ldws = ldws if ldws is not None else (G + 1) // 2 * 2
+    for what, rng, voff, soff, width in (loads or _loads)(M, N, K, ldwz, ldws, kgroups, slices):
+        voff = np.asarray(voff, dtype=np.int64)
+        masked = voff >= rng                       # fails the range check: zeros, no memory access
+        ok = masked | ((voff >= 0) & (voff + soff + width <= rng))
+        assert ok.all(), (f"{what} load outside its {rng}-byte range: voff {voff[~ok][:4]}, soff {soff}, "
+                          f"width {width} (M={M} N={N} K={K})")
+
+
+@pytest.mark.parametrize("k", [192, 256, 320, 384, 448, 1472, 3072, 3136])
+@pytest.mark.parametrize("m,n", [(257, 300), (300, 256), (513, 400)])
+def test_every_load_stays_in_its_range(m, n, k):
+    _check(m, n, k)
+
+
+@pytest.mark.parametrize("k", [320, 1472, 3072, 3200])
+def test_split_k_slices_stay_in_range(k):
+    g = k // 64
+    blocks = (g + 3) // 4
+    per = max(2, blocks // 3)
+    slices = -(-blocks // per)
+    _check(256, 520, k, kgroups=per * 4, slices=slices)
+
+
+@pytest.mark.parametrize("which", ["S", "Z"])
+def test_model_catches_an_offset_past_the_range(which):
+    # planted mistakes: the scale dword or the zero-point word of the last block loaded without
+    # moving back on the tile's last weight row (the kernel's loads before that correction) must be
+    # reported for K / 64 = 5 (the block 4..7 runs past G)
+    def unshifted(M, N, K, ldwz, ldws, kgroups=None, slices=1):
+        tid = np.arange(512)
+        brow, bhalf = tid >> 1, tid & 1
+        rows_n = min(TN, N)
+        for what, rng, voff, soff, width in _loads(M, N, K, ldwz, ldws, kgroups, slices):
+            if what == which == "S":
+                voff = np.where(brow < rows_n, brow * ldws * 2 + 4 * bhalf, KOOB)
+            if what == which == "Z":
+                voff = np.where(brow < rows_n, brow * ldwz, KOOB)
+            yield what, rng, voff, soff, width
+
+    with pytest.raises(AssertionError, match=f"{which} load"):
+        _check(300, 200, 320, loads=unshifted)
