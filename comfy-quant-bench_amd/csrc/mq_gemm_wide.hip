@@ -313,24 +313,43 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // The tile's last weight row has nothing after its ceil(G/2) zero-point bytes and G scales
     // inside the resource range (the range check covers the vector offset only): in the block that
     // runs past G (G % 4 != 0) that row's loads move back to end at the row's end (or, for a scale
-    // pair wholly past G, fail the range check), and the bytes they want are shifted down after
-    // the load (zsh, ssh bits). The host keeps G >= 3 on this kernel, so moving back stays inside
-    // the row.
+    // pair wholly past G, fail the range check), and the bytes they want are shifted down once the
+    // loads have arrived (settle_zs, by zsh / ssh bits). The host keeps G >= 3 on this kernel, so
+    // moving back stays inside the row.
+    // Only the last live block (b4 = 4 * ((G - 1) / 4)) can run past G; its offsets and shifts are
+    // worked out once here.
     const bool last_row = brow == rows_n - 1;
+    const int last_b4 = (G - 1) / 4 * 4;
+    int z_last = z_off, s_last = s_off;
+    uint32_t zsh_last = 0u, ssh_last = 0u;
+    if (last_row && z_off != kOob && last_b4 / 2 + 2 > (G + 1) / 2) {
+        z_last = z_off - 1;
+        zsh_last = 8u;
+    }
+    if (last_row && s_off != kOob) {
+        const int ga = last_b4 + 2 * bhalf;   // first group of this thread's scale pair
+        if (ga >= G) s_last = kOob;
+        else if (ga + 1 == G) {
+            s_last = s_off - 2;
+            ssh_last = 16u;
+        }
+    }
     uint32_t zq = 0u, sq = 0u, zsh = 0u, ssh = 0u;
+    // once a block's zero-points and scales have arrived (before their first use): the moved-back
+    // loads of the last block bring the wanted bytes down
+    auto settle_zs = [&]() {
+        if constexpr (WK == WKind::U4Asym) zq >>= zsh;
+        if constexpr (EPI == Epi::GroupScale) sq >>= ssh;
+    };
     auto gload_zs = [&](int b4) {
+        const bool lb = b4 == last_b4;   // wave-uniform
         if constexpr (WK == WKind::U4Asym) {
-            const bool back = last_row && b4 / 2 + 2 > (G + 1) / 2;
-            zsh = back ? 8u : 0u;
-            const int zv = z_off == kOob ? kOob : z_off - (back ? 1 : 0);
-            zq = asm_ld16(b4 < G ? dz : d_none, zv, b4 < G ? b4 >> 1 : 0);
+            zsh = lb ? zsh_last : 0u;
+            zq = asm_ld16(b4 < G ? dz : d_none, lb ? z_last : z_off, b4 < G ? b4 >> 1 : 0);
         }
         if constexpr (EPI == Epi::GroupScale) {
-            const int ga = b4 + 2 * bhalf;   // first group of this thread's scale pair
-            const bool none = last_row && ga >= G, back = last_row && ga + 1 == G;
-            ssh = back ? 16u : 0u;
-            const int sv = s_off == kOob || none ? kOob : s_off - (back ? 2 : 0);
-            sq = asm_ld32(b4 < G ? ds : d_none, sv, soff(b4, 2));
+            ssh = lb ? ssh_last : 0u;
+            sq = asm_ld32(b4 < G ? ds : d_none, lb ? s_last : s_off, soff(b4, 2));
         }
     };
     // Wait until at most N VMEM operations are outstanding; register set SET counts as written by
@@ -349,7 +368,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             constexpr bool x16 = AM == 2 && kGroup;
             constexpr bool nw = neg && AM != 2;
             constexpr int pos = decltype(Uc)::value;
-            const uint32_t c = unpack_const<WK, nw>((zq >> (zsh + 4 * pos)) & 0xfu);
+            const uint32_t c = unpack_const<WK, nw>((zq >> (4 * pos)) & 0xfu);
             uint4 u;
             const uint32_t w0 = h ? rb[set].z : rb[set].x, w1 = h ? rb[set].w : rb[set].y;
             unpack_dword<WK, nw, x16>(w0, c, u.x, u.y);
@@ -363,8 +382,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             constexpr bool neg = decltype(PARc)::value == 1;
             constexpr int u = decltype(Uc)::value;
             if (bhalf == (u >> 1)) {
-                const uint32_t sh = ssh + 16u * (u & 1);
-                float sv = f16_bits_to_f32(static_cast<uint16_t>(sh < 32u ? sq >> sh : 0u)) * kSfac;   // exact
+                float sv = f16_bits_to_f32(static_cast<uint16_t>(sq >> (16 * (u & 1)))) * kSfac;   // exact
                 sv = g >= g0 && g < gend ? (neg ? -sv : sv) : 0.0f;
                 ds_write4(s_st, st * TN * 4, sv);
                 cs += sv;
@@ -437,6 +455,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     gload_b(g0 + 1, 1);
     MQ_WAIT_B(0, 0);
     MQ_WAIT_B(0, 1);
+    settle_zs();
     store_b(0, 0, I0{}, I0{}, 0);
     store_b(0, 0, I0{}, I0{}, 1);
     store_s(0, g0, I0{}, I0{});
@@ -520,6 +539,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             // unpack register set SET (group g + 2, parity PAR) into stage ST2, then reload it with g + 4
             if (t == 8) {
                 MQ_WAIT_B(kWaitB[U], SET);
+                // group g + 2 opens the block of zero-points and scales loaded in group g - 1
+                if constexpr (U == 2) settle_zs();
                 store_b(ST2, SET, PARc{}, U2c{}, 0);
             }
             if (t == 9) store_b(ST2, SET, PARc{}, U2c{}, 1);
@@ -640,24 +661,30 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         return;
     }
     uint16_t* stage = reinterpret_cast<uint16_t*>(smem) + wave * 64 * OROW;
+    // the staging loop once per 16-bit output type (a wave-uniform branch outside the loop)
+    auto stage_tile = [&](auto DTc) {
+        constexpr int DT = decltype(DTc)::value;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int lr0 = i * 16 + 4 * (lane >> 4);
-        const int64_t row0 = m0 + wm * 64 + lr0;
-        float sav[4];
+        for (int i = 0; i < 4; ++i) {
+            const int lr0 = i * 16 + 4 * (lane >> 4);
+            const int64_t row0 = m0 + wm * 64 + lr0;
+            float sav[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sav[r] = row0 + r < M ? a.sa[row0 + r] : 0.0f;
+            for (int r = 0; r < 4; ++r) sav[r] = row0 + r < M ? a.sa[row0 + r] : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int lc = j * 16 + fr;
+            for (int j = 0; j < 8; ++j) {
+                const int lc = j * 16 + fr;
 #pragma unroll
-            for (int r = 0; r < 4; r += 2) {
-                const uint32_t hb = pack_16x2(out_value(i, j, r, sav[r]), out_value(i, j, r + 1, sav[r + 1]), a.y_dtype);
-                stage[(lr0 + r) * OROW + lc] = static_cast<uint16_t>(hb & 0xffffu);
-                stage[(lr0 + r + 1) * OROW + lc] = static_cast<uint16_t>(hb >> 16);
+                for (int r = 0; r < 4; r += 2) {
+                    const uint32_t hb = pack_16x2(out_value(i, j, r, sav[r]), out_value(i, j, r + 1, sav[r + 1]), DT);
+                    stage[(lr0 + r) * OROW + lc] = static_cast<uint16_t>(hb & 0xffffu);
+                    stage[(lr0 + r + 1) * OROW + lc] = static_cast<uint16_t>(hb >> 16);
+                }
             }
         }
-    }
+    };
+    if (a.y_dtype == kDtF16) stage_tile(std::integral_constant<int, kDtF16>{});
+    else stage_tile(std::integral_constant<int, kDtBf16>{});
     __syncthreads();
     const int64_t col0 = n0 + wn * 128;
     const bool vec_ok = (a.ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
