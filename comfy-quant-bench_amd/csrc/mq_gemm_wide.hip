@@ -72,8 +72,10 @@ constexpr int S_LDS = B_LDS + NSTAGE * TILE_BYTES;        // 131072: fp32 scales
 constexpr int PIPE_END = S_LDS + NSTAGE * TN * 4;         // 135168
 constexpr int OROW = 136;                                 // 16-bit pitch of the output staging rows
 constexpr int OUT_END = 8 * 64 * OROW * 2;                // 139264
-constexpr int C_LDS = PIPE_END > OUT_END ? PIPE_END : OUT_END;   // per-column offset correction
-constexpr int SMEM_BYTES = C_LDS + TN * 4;
+constexpr int C_LDS = PIPE_END > OUT_END ? PIPE_END : OUT_END;   // per-column offset correction / fp32 scale
+constexpr int R_LDS = C_LDS + TN * 4;                     // per-row activation scales of the tile
+constexpr int BI_LDS = R_LDS + TM * 4;                    // per-column bias of the tile, as fp32
+constexpr int SMEM_BYTES = BI_LDS + TN * 4;
 
 // byte offset of 16-byte chunk c of tile row r in the swizzled layout
 __device__ __forceinline__ int lds_off(int r, int c) { return r * TK + ((c ^ ((r >> 1) & 3)) << 4); }
@@ -235,6 +237,21 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     const int rows_m = M - m0 < TM ? static_cast<int>(M - m0) : TM;   // valid rows of this tile
     const int rows_n = N - n0 < TN ? static_cast<int>(N - n0) : TN;
     const int kbytes_w = kPacked ? static_cast<int>(a.K / 2) : static_cast<int>(a.K);
+    // The output epilogue's per-row and per-column inputs (activation scales, bias, fp32 weight
+    // scales), loaded now and put into LDS once the prologue's loads have landed, so the epilogue
+    // reads them from LDS: thread t < TM takes row m0 + t, thread TM + c column n0 + c. Rows and
+    // columns past the matrix get 0.
+    constexpr bool kFinal = !SPLIT && (EPI == Epi::GroupScale || EPI == Epi::RowScale);
+    float ep_a = 0.0f, ep_b = 0.0f;
+    if constexpr (kFinal) {
+        if (tid < TM) {
+            if (tid < rows_m) ep_a = a.sa[m0 + tid];
+        } else if (tid - TM < rows_n) {
+            const int64_t col = n0 + (tid - TM);
+            if (a.bias) ep_a = load_as_f32(a.bias, a.bias_dtype, col);
+            if constexpr (EPI == Epi::RowScale) ep_b = a.ws32[col];
+        }
+    }
     const auto ra_rs = rsrc(a.qa + m0 * a.lda, (rows_m - 1) * a.lda + a.K);
     const auto rb_rs = rsrc(a.qw + n0 * a.ldw, (rows_n - 1) * a.ldw + kbytes_w);
 
@@ -463,6 +480,14 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     store_b(1, 1, I1{}, I1{}, 1);
     store_s(1, g0 + 1, I1{}, I1{});
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // A(0), A(1) of every kind (int8 B has no B loads)
+    if constexpr (kFinal) {
+        if (tid < TM) {
+            lds<float>(smem, R_LDS + 4 * tid) = ep_a;
+        } else {
+            lds<float>(smem, BI_LDS + 4 * (tid - TM)) = ep_a;
+            if constexpr (EPI == Epi::RowScale) lds<float>(smem, C_LDS + 4 * (tid - TM)) = ep_b;
+        }
+    }
     gload_b(g0 + 2, 0);
     dma_group(g0 + 2, 2);
     gload_b(g0 + 3, 1);
@@ -627,37 +652,40 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         }
         return;
     }
+    // column inputs of this lane (the fp32 weight scale or offset correction, the bias) and row
+    // scales, all from LDS; rows and columns past the matrix read 0 and are never stored
     float colv[8], biasv[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int lc = wn * 128 + j * 16 + fr;
-        const int64_t col = n0 + lc;
-        const bool ok = col < N;
-        if constexpr (EPI == Epi::GroupScale) colv[j] = lds<float>(smem, C_LDS + 4 * lc);
-        else colv[j] = ok ? a.ws32[col] : 0.0f;
-        biasv[j] = (ok && a.bias) ? load_as_f32(a.bias, a.bias_dtype, col) : 0.0f;
+        colv[j] = lds<float>(smem, C_LDS + 4 * lc);
+        biasv[j] = lds<float>(smem, BI_LDS + 4 * lc);
     }
+    // the row scales of rows 4 (lane / 16) + 0..3 of row block i
+    auto row_scales = [&](int i) { return lds<f4>(smem, R_LDS + 4 * (wm * 64 + i * 16 + 4 * (lane >> 4))); };
     // y[m, n] in fp32 before the rounding to the output type
     auto out_value = [&](int i, int j, int r, float sa_r) {
         if constexpr (EPI == Epi::GroupScale) return __builtin_fmaf(acc[i][j][r] - colv[j], sa_r, biasv[j]);
         else return static_cast<float>(acci[i][j][r]) * sa_r * colv[j] + biasv[j];
     };
+    const bool full = m0 + TM <= M && n0 + TN <= N;   // no row or column of the tile past the matrix
     if (a.y_dtype == kDtF32) {
         // fp32 outputs straight from the registers: the 16 lanes of a row segment write 64
         // consecutive bytes
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+            const f4 sav = row_scales(i);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
-                if (row >= M) continue;
-                const float sa_r = a.sa[row];
+                if (!full && row >= M) continue;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const int64_t col = n0 + wn * 128 + j * 16 + fr;
-                    if (col < N) static_cast<float*>(a.y)[row * a.ldy + col] = out_value(i, j, r, sa_r);
+                    if (full || col < N) static_cast<float*>(a.y)[row * a.ldy + col] = out_value(i, j, r, sav[r]);
                 }
             }
+        }
         return;
     }
     uint16_t* stage = reinterpret_cast<uint16_t*>(smem) + wave * 64 * OROW;
@@ -667,10 +695,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int lr0 = i * 16 + 4 * (lane >> 4);
-            const int64_t row0 = m0 + wm * 64 + lr0;
-            float sav[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sav[r] = row0 + r < M ? a.sa[row0 + r] : 0.0f;
+            const f4 sav = row_scales(i);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int lc = j * 16 + fr;
@@ -687,7 +712,19 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     else stage_tile(std::integral_constant<int, kDtBf16>{});
     __syncthreads();
     const int64_t col0 = n0 + wn * 128;
-    const bool vec_ok = (a.ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+    // 16-byte row stores: lane l of iteration it writes chunk (64 it + l) % 16 of staged row
+    // (64 it + l) / 16
+    if (full && (a.ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0) {
+        uint16_t* ybase = static_cast<uint16_t*>(a.y) + (m0 + wm * 64) * a.ldy + col0;
+#pragma unroll 4
+        for (int it = 0; it < 16; ++it) {
+            const int c = it * 64 + lane;
+            const int lr = c >> 4, ch = c & 15;
+            *reinterpret_cast<uint4*>(ybase + lr * a.ldy + ch * 8) =
+                *reinterpret_cast<const uint4*>(&stage[lr * OROW + ch * 8]);
+        }
+        return;
+    }
 #pragma unroll 4
     for (int it = 0; it < 16; ++it) {
         const int c = it * 64 + lane;
@@ -697,7 +734,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         if (row >= M || col >= N) continue;
         const uint4 v = *reinterpret_cast<const uint4*>(&stage[lr * OROW + ch * 8]);
         uint16_t* dst = static_cast<uint16_t*>(a.y) + row * a.ldy + col;
-        if (vec_ok && col + 8 <= N) {
+        if ((a.ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 && col + 8 <= N) {
             *reinterpret_cast<uint4*>(dst) = v;
         } else {
             const uint32_t w[4] = {v.x, v.y, v.z, v.w};
