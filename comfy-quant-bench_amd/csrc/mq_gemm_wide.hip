@@ -592,6 +592,15 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         group(g + 2, std::integral_constant<int, 2>{});
         group(g + 3, std::integral_constant<int, 3>{});
     }
+    // The last K groups issued loads for groups past the end (zero-size resources) that nothing
+    // waits for: B registers, zero-points, scales and stage DMA. Their data may land at any time
+    // until they complete, so every one of them completes here, and the registers they write stay
+    // reserved up to this wait (the empty asm statements below read them): otherwise the epilogue
+    // could reuse such a register for an address and have it overwritten by a late zero.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if constexpr (kPacked) asm volatile("" : "+v"(rb[0]), "+v"(rb[1]));
+    if constexpr (WK == WKind::U4Asym) asm volatile("" : "+v"(zq));
+    if constexpr (EPI == Epi::GroupScale) asm volatile("" : "+v"(sq));
 #undef MQ_WAIT_B
     // drain: the last LAG tiles of the last group run (dead unless G is a multiple of four)
 #pragma unroll
@@ -603,6 +612,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     }
 
     if constexpr (EPI == Epi::GroupPartials) return;
+
 
     if constexpr (EPI == Epi::RowAcc) {
 #pragma unroll
