@@ -16,7 +16,10 @@
 // column c has bits c0..c9; lane L of the wave loads the 16 consecutive columns of segment
 // s = (L >> 2) + 16 (L & 3) (two 16-byte bf16 loads), so register bits r0..r3 hold c0..c3 and
 // lane bits L0..L5 hold c8 c9 c4 c5 c6 c7. The radix-4 stages over (c0 c1) and (c2 c3) run in
-// registers. The stage over (c4 c5) (blocks 64, 256) first swaps lane bits L2, L3 with register
+// registers. Plain inputs then move c4..c7 into the registers with a 16 x 16 transpose through LDS
+// (rotate_chunk_lds), run the stages over (c4 c5) and (c6 c7) there and transpose back, so the
+// exchanges cost no VALU instructions and the codes leave in the load layout. The SwiGLU kernels
+// exchange through lanes instead: the stage over (c4 c5) (blocks 64, 256) first swaps lane bits L2, L3 with register
 // bits r2, r3 through DPP row shifts written into the lanes of the receiving DPP banks only (one
 // v_mov_b32_dpp per moved value); the stage over (c6 c7) (block 256) swaps L4, L5 with r2, r3
 // through v_permlane16_swap / v_permlane32_swap (one instruction per register pair). Every
@@ -164,6 +167,48 @@ __device__ __forceinline__ void rotate_chunk(float (&v)[16], int lane) {
     }
 }
 
+// The same rotation with the exchanges done through LDS instead of lane swaps (no VALU work for
+// them). Within each group of 16 lanes that share lane bits L0 L1, lane bits L2..L5 hold c4..c7
+// and the 16 registers c0..c3: a 16 x 16 transpose (lane index <-> register index) brings c4..c7
+// into the registers, where the stages over (c4 c5) and (c6 c7) run, and the same transpose
+// brings the load layout back. Lane (g, i) = (L & 3, L >> 2) writes its register j at float
+// g * kTrG + j * kTrS + i and reads its new registers 4q .. 4q + 3 from g * kTrG + i * kTrS + 4q:
+// 16 ds_write_b32, whose 64 lanes hit 64 different banks (kTrG = 16 mod 64 banks), and 4
+// ds_read_b128, whose 16-lane quarters cover the 64 banks once (kTrS = 20). LDS operations of a
+// wave execute in issue order, so a read sees the writes before it and the next transpose's
+// writes never overtake earlier reads.
+constexpr int kTrS = 20, kTrG = 336, kTrWave = 4 * kTrG;   // floats
+struct LdsTranspose {
+    float* w;   // this lane's write base: wave region + g * kTrG + i
+    float* r;   // this lane's read base: wave region + g * kTrG + i * kTrS
+    __device__ __forceinline__ void operator()(float (&v)[16]) const {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) w[j * kTrS] = v[j];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 t = *reinterpret_cast<const float4*>(r + 4 * q);
+            v[4 * q] = t.x;
+            v[4 * q + 1] = t.y;
+            v[4 * q + 2] = t.z;
+            v[4 * q + 3] = t.w;
+        }
+    }
+};
+
+template <int BLK>
+__device__ __forceinline__ void rotate_chunk_lds(float (&v)[16], const LdsTranspose& tr) {
+    if constexpr (BLK >= 16) {
+        stage_reg<0>(v);          // element stride 1  (c0 c1)
+        stage_reg<2>(v);          // element stride 4  (c2 c3)
+    }
+    if constexpr (BLK >= 64) {
+        tr(v);                    // registers now hold c4..c7
+        stage_reg<0>(v);          // element stride 16 (c4 c5)
+        if constexpr (BLK >= 256) stage_reg<2>(v);   // element stride 64 (c6 c7)
+        tr(v);                    // back to the load layout
+    }
+}
+
 // Column bit 6 (the parity of the 64-column group) of register r of lane L after rotate_chunk.
 template <int BLK>
 __device__ __forceinline__ int col_bit6(int lane, int r) {
@@ -210,9 +255,21 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
                 uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale) {
     constexpr int LIMIT = OUT == 0 ? 127 : 7;
     constexpr int RPG = kWaves / W;                      // rows per workgroup step
+    // Plain inputs exchange lanes and registers through LDS (rotate_chunk_lds) and leave the
+    // rotation in the load layout; the SwiGLU prologue, whose LDS holds its silu table, keeps the
+    // lane swaps. LB: the block whose register layout the rotated values are in.
+    constexpr bool kLdsT = ACT == 0 && BLK >= 64;
+    constexpr int LB = kLdsT ? 16 : BLK;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wr = wave % W;                             // this wave's share of its row
+    [[maybe_unused]] LdsTranspose tr{nullptr, nullptr};
+    if constexpr (kLdsT) {
+        __shared__ __attribute__((aligned(16))) float tr_lds[kWaves * kTrWave];
+        float* base = tr_lds + wave * kTrWave + (lane & 3) * kTrG;
+        tr.w = base + (lane >> 2);
+        tr.r = base + (lane >> 2) * kTrS;
+    }
     [[maybe_unused]] const float* tab = nullptr;
     [[maybe_unused]] const uint32_t* tab16 = nullptr;
     if constexpr (ACT == 1 && IN == 1) tab16 = SiluF16Table<IN>::get();
@@ -230,7 +287,7 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
     }
     const int seg_ld = (lane >> 2) + 16 * (lane & 3);   // 16-column segment this lane loads
     // after the final dword exchange a lane holds the 16 codes of segment seg_st
-    const int seg_st = BLK >= 256 ? (lane >> 4) + 4 * ((lane >> 2) & 3) + 16 * (lane & 3) : seg_ld;
+    const int seg_st = LB >= 256 ? (lane >> 4) + 4 * ((lane >> 2) & 3) + 16 * (lane & 3) : seg_ld;
     const int64_t groups = (static_cast<int64_t>(M) + RPG - 1) / RPG;
     int parity = 0;
     // every wave runs the same number of steps (the bound is uniform over the workgroup), so the
@@ -293,7 +350,8 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
         float am = 0.0f;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
-            rotate_chunk<BLK>(v[c], lane);
+            if constexpr (kLdsT) rotate_chunk_lds<BLK>(v[c], tr);
+            else rotate_chunk<BLK>(v[c], lane);
             float amc = 0.0f;
 #pragma unroll
             for (int j = 0; j < 16; ++j) amc = __builtin_fmaxf(amc, __builtin_fabsf(v[c][j]));
@@ -317,17 +375,17 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             // quantization is odd-symmetric (rint and the clamp are), so negating the input of an
-            // odd 64-column group negates its codes exactly; for block 256 the group parity is
-            // register bit r2, so the sign applies per dword below instead
+            // odd 64-column group negates its codes exactly; in the block-256 lane-swap layout the
+            // group parity is register bit r2, so the sign applies per dword below instead
             float mq[16];
-            quant16<LIMIT>(v[c], OUT == 3 && BLK < 256 && col_bit6<BLK>(lane, 0) ? -1.0f : 1.0f, r, s, mq);
+            quant16<LIMIT>(v[c], OUT == 3 && LB < 256 && col_bit6<LB>(lane, 0) ? -1.0f : 1.0f, r, s, mq);
             uint32_t word[4];
 #pragma unroll
             for (int hi = 0; hi < 4; ++hi) {
                 uint32_t m0 = __float_as_uint(mq[4 * hi + 0]), m1 = __float_as_uint(mq[4 * hi + 1]);
                 uint32_t m2 = __float_as_uint(mq[4 * hi + 2]), m3 = __float_as_uint(mq[4 * hi + 3]);
-                if constexpr (OUT == 3 && BLK >= 256) {
-                    if (col_bit6<BLK>(lane, 4 * hi)) {   // negate the four codes (two's complement bytes)
+                if constexpr (OUT == 3 && LB >= 256) {
+                    if (col_bit6<LB>(lane, 4 * hi)) {   // negate the four codes (two's complement bytes)
                         m0 = -m0; m1 = -m1; m2 = -m2; m3 = -m3;
                     }
                 }
@@ -344,7 +402,7 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
             }
             // dword index bits hold (c6 c7) for block 256 and (c4 c5) for block 64; lane bits
             // L2 L3 hold (c2 c3): exchange them so each lane's four dwords are consecutive columns
-            if constexpr (BLK >= 64) {
+            if constexpr (LB >= 64) {
                 swap_lane_reg<2, 0>(word, lane);
                 swap_lane_reg<3, 1>(word, lane);
             }
