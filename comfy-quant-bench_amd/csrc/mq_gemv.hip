@@ -2,21 +2,29 @@
 // calls): HBM-bound, so each weight byte is read once with 16-byte coalesced loads and multiplied
 // on the VALU with v_dot4_i32_i8 (no MFMA, no LDS tiles for the weights).
 //
-// Workgroup: 4 wavefronts; each wavefront owns 4 output columns at a time and splits their K range
-// over its lanes in 16-byte weight chunks (16 K values of int8 weights, 32 of packed 4-bit). The
-// activation rows are staged once per workgroup in LDS; for 4-bit weights each 8-value block is
-// stored de-interleaved (even K in one dword, odd K in the next), so a packed weight dword needs
-// only nibble masks: (w & 0x0f0f0f0f) pairs with the even activations, (w >> 4) & 0x0f0f0f0f with
-// the odd ones. Exact integer chunk sums D then enter the epilogue:
-//   uint4 asym   D = sum a q - z * sum a (the per-chunk activation sums are staged too)
+// Workgroup: 4 wavefronts; each wavefront owns 4 output columns, 16 lanes per column (one DPP row).
+// A column's weight row is read in 16-byte chunks (32 K values of packed 4-bit weights, 16 of int8):
+// lane j takes chunks j, j + 16, j + 32, ..., so every load instruction reads 256 contiguous bytes
+// of each of the wavefront's 4 rows, and every lane issues the loads of all its chunks (with their
+// zero-points and scales) at once, after the activation loads: loads complete in issue order, so
+// the activation staging and the barrier finish while the weights are still on their way, and each
+// lane then works through its chunks as they arrive (rows longer than kH chunks per lane take one
+// round of loads per kH chunks). The activation rows are staged once per workgroup in LDS in
+// 16-value blocks (the first and second half of every packed chunk in separate arrays, so the 16
+// lanes of a column read 256 contiguous bytes); for 4-bit weights each 8-value block is stored
+// de-interleaved (even K in one dword, odd K in the next), so a packed weight dword needs only nibble
+// masks: (w & 0x0f0f0f0f) pairs with the even activations, (w >> 4) & 0x0f0f0f0f with the odd ones.
+// Each chunk's exact integer sum D:
+//   uint4 asym   D = sum a q - z * sum a (sum a staged per 16-value block)
 //   int4 sym     the nibble is moved to the top of its byte (16 v), so D = 16 sum a v
 //   GroupScale   acc += s[n, g] * D * f in fp32, f = 1/16 (int4 sym) times (-1)^g / 16 for the
 //                activation layout 16 q negated in odd groups: every factor a power of two;
-//                y = T(acc * sa[m] + bias[n]) after a wavefront reduction (T: the output type)
+//                y = T(acc * sa[m] + bias[n]) after a reduction over the column's 16 lanes (T: the
+//                output type)
 //   RowScale     an int32 sum over all of K (exact), y = T(P * sa[m] * ws[n] + bias[n])
 //   GroupPartials / RowAcc (parity entries) write the exact int32 group partials P[g, m, n] (the
-//                two half-group chunk sums of adjacent lanes added, the x16 / sign factors of the
-//                int4 layouts undone by exact shifts) or the full-K int32 sums
+//                two chunks of a group sit in lanes 2i and 2i + 1 and are added by a DPP exchange;
+//                the x16 / sign factors of the int4 layouts undone by exact shifts) or the full-K sums
 #include "mq_device.h"
 #include "mq_internal.h"
 
@@ -24,167 +32,202 @@ namespace mq {
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kCols = 4;        // output columns per wavefront step
+constexpr int kCols = 4;        // output columns per wavefront (16 lanes each)
+
+// Sum over the 16 lanes of a DPP row, returned in every lane of the row.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_mov<kRowRor8>(v);
+    v += dpp_mov<kRowRor4>(v);
+    v += dpp_mov<kQuadXor2>(v);
+    v += dpp_mov<kQuadXor1>(v);
+    return v;
+}
+__device__ __forceinline__ int row16_sum(int v) {
+    v += __builtin_amdgcn_mov_dpp(v, kRowRor8, 0xf, 0xf, true);
+    v += __builtin_amdgcn_mov_dpp(v, kRowRor4, 0xf, 0xf, true);
+    v += __builtin_amdgcn_mov_dpp(v, kQuadXor2, 0xf, 0xf, true);
+    v += __builtin_amdgcn_mov_dpp(v, kQuadXor1, 0xf, 0xf, true);
+    return v;
+}
 
 // One row (the adaLN modulation linear, M = 1) is built for five waves per SIMD: 1280 resident
-// workgroups, so config 1's N = 18432 (1152 workgroups) runs in one wave of workgroups instead of
-// a full second wave for its last 128 (the uint4 kernel then keeps 12 bytes of values in scratch).
+// workgroups, so config 1's N = 18432 (1152 workgroups) runs in one wave of workgroups.
 template <WKind WK, Epi EPI, int AM, int MR>
 __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(GemmArgs a) {
     constexpr bool kPacked = WK != WKind::I8;
     constexpr int kChunkK = kPacked ? 32 : 16;          // K values per 16-byte weight chunk
+    constexpr int kH = kPacked ? 6 : 12;                // chunks a lane holds in registers at once
     extern __shared__ __attribute__((aligned(16))) uint32_t gv_smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = static_cast<int>(a.K);
-    const int nchunks = K / kChunkK;
-    uint32_t* act = gv_smem;                            // [MR][K / 4] dwords
-    int* asum = reinterpret_cast<int*>(gv_smem + MR * (K / 4));   // [MR][nchunks] (uint4 asym)
-    const int64_t n_base = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * kCols;
+    const int nch = K / kChunkK;                        // chunks per weight row
+    const int blocks = K / 16;                          // 16-value activation blocks per row
+    // LDS: [MR][blocks][4] dwords of staged activation blocks (packed weights: the first halves of
+    // the chunks, then the second halves), then [MR][blocks] block sums (uint4 asym)
+    uint32_t* act = gv_smem;
+    int* bsum = reinterpret_cast<int*>(gv_smem + MR * blocks * 4);
+    const int sub = lane & 15;                                              // lane within its column
+    const int64_t n = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * kCols + (lane >> 4);
+    const bool col_ok = n < a.N;
+    const int64_t nc = col_ok ? n : 0;
+    const uint8_t* wrow = a.qw + nc * a.ldw;
 
-    // Raw weight chunk, zero-point byte and fp16 scale of chunk ch for the wave's kCols columns
-    // (zero past the row's end or past N). Decoding waits for the loads, so it happens at the use:
-    // the first chunk is loaded before the activation staging and every later one an iteration
-    // ahead, and the loads' latency overlaps the staging and the previous chunk's arithmetic.
-    struct Chunk {
-        uint4 w[kCols];
-        uint32_t z[kCols], s[kCols];
-    };
-    auto load_chunk = [&](int ch, Chunk& t) {
-        const int g = ch * kChunkK / 64;
+    // Every load below is unconditional, from an address inside the operands (chunks past the row
+    // read its last chunk, columns past N column 0, rows past M row M - 1): a load whose value were
+    // selected away afterwards would make the compiler wait for it on the spot. Such values are
+    // never used (the chunk loop stops at the row's end; rows and columns past the matrix are never
+    // stored).
+    constexpr int kStage = 2;                           // activation blocks per thread loaded up front
+    uint4 xs[MR][kStage];
 #pragma unroll
-        for (int c = 0; c < kCols; ++c) {
-            const int64_t n = n_base + c;
-            const bool ok = ch < nchunks && n < a.N;
-            t.w[c] = ok ? *reinterpret_cast<const uint4*>(a.qw + n * a.ldw + ch * 16) : uint4{0u, 0u, 0u, 0u};
-            t.z[c] = 0u;
-            t.s[c] = 0u;
-            if constexpr (WK == WKind::U4Asym) t.z[c] = ok ? a.wz[n * a.ldwz + (g >> 1)] : 0u;
-            if constexpr (EPI == Epi::GroupScale) t.s[c] = ok ? a.ws16[n * a.ldws + g] : 0u;
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int it = 0; it < kStage; ++it) {
+            const int bl = tid + it * 64 * kWaves;
+            const int64_t mr = m < a.M ? m : a.M - 1;
+            xs[m][it] = *reinterpret_cast<const uint4*>(a.qa + mr * a.lda + 16 * (bl < blocks ? bl : 0));
+        }
+    __builtin_amdgcn_sched_barrier(0);   // keep the activation loads ahead of the weight loads
+
+    // chunks c0 + 16 h, h < kH, of this lane: weights, zero-point byte, fp16 scale
+    uint4 w[kH];
+    uint32_t zb[kH], sb[kH];
+    auto load_chunks = [&](int c0) {
+#pragma unroll
+        for (int h = 0; h < kH; ++h) {
+            const int c = min(c0 + 16 * h, nch - 1);
+            const int g = c * kChunkK / 64;
+            w[h] = *reinterpret_cast<const uint4*>(wrow + 16 * static_cast<int64_t>(c));
+            zb[h] = 0u;
+            sb[h] = 0u;
+            if constexpr (WK == WKind::U4Asym) zb[h] = a.wz[nc * a.ldwz + (g >> 1)];
+            if constexpr (EPI == Epi::GroupScale) sb[h] = a.ws16[nc * a.ldws + g];
         }
     };
-    Chunk cur, next;
-    load_chunk(lane, cur);
+    load_chunks(sub);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // stage the activation rows (de-interleaved per 8 values for 4-bit weights)
+    // Stage block bl of row m (de-interleaved per 8 values for 4-bit weights): packed weights put
+    // block 2c + e (half e of chunk c) at position e * nch + c, int8 weights block c at c.
+    auto stage = [&](int m, int bl, uint4 x) {
+        uint4 o = x;
+        int pos = bl;
+        if constexpr (kPacked) {
+            o.x = __builtin_amdgcn_perm(x.y, x.x, 0x06040200u);   // values 0, 2, 4, 6
+            o.y = __builtin_amdgcn_perm(x.y, x.x, 0x07050301u);   // values 1, 3, 5, 7
+            o.z = __builtin_amdgcn_perm(x.w, x.z, 0x06040200u);   // values 8, 10, 12, 14
+            o.w = __builtin_amdgcn_perm(x.w, x.z, 0x07050301u);   // values 9, 11, 13, 15
+            pos = (bl & 1) * nch + (bl >> 1);
+        }
+        *reinterpret_cast<uint4*>(act + (m * blocks + pos) * 4) = o;
+        if constexpr (WK == WKind::U4Asym) {
+            int sm = __builtin_amdgcn_sdot4(static_cast<int>(x.x), 0x01010101, 0, false);
+            sm = __builtin_amdgcn_sdot4(static_cast<int>(x.y), 0x01010101, sm, false);
+            sm = __builtin_amdgcn_sdot4(static_cast<int>(x.z), 0x01010101, sm, false);
+            sm = __builtin_amdgcn_sdot4(static_cast<int>(x.w), 0x01010101, sm, false);
+            bsum[m * blocks + bl] = sm;
+        }
+    };
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-        for (int b = tid; b < K / 8; b += 64 * kWaves) {
-            const uint2 x = m < a.M ? *reinterpret_cast<const uint2*>(a.qa + m * a.lda + 8 * b) : uint2{0u, 0u};
-            uint2 o = x;
-            if constexpr (kPacked) {
-                o.x = __builtin_amdgcn_perm(x.y, x.x, 0x06040200u);   // values 0, 2, 4, 6
-                o.y = __builtin_amdgcn_perm(x.y, x.x, 0x07050301u);   // values 1, 3, 5, 7
-            }
-            *reinterpret_cast<uint2*>(act + m * (K / 4) + 2 * b) = o;
-        }
-    }
-    if constexpr (WK == WKind::U4Asym) {
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            for (int c = tid; c < nchunks; c += 64 * kWaves) {
-                int s = 0;
-                if (m < a.M) {
-                    const uint4 x0 = *reinterpret_cast<const uint4*>(a.qa + m * a.lda + c * kChunkK);
-                    const uint4 x1 = *reinterpret_cast<const uint4*>(a.qa + m * a.lda + c * kChunkK + 16);
-                    const uint32_t w[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) s = __builtin_amdgcn_sdot4(static_cast<int>(w[j]), 0x01010101, s, false);
-                }
-                asum[m * nchunks + c] = s;
-            }
+        for (int it = 0; it < kStage; ++it) {
+            const int bl = tid + it * 64 * kWaves;
+            if (bl < blocks) stage(m, bl, xs[m][it]);
         }
+        // rows longer than kStage * 256 blocks: the rest block by block
+        for (int bl = tid + kStage * 64 * kWaves; bl < blocks; bl += 64 * kWaves)
+            stage(m, bl, *reinterpret_cast<const uint4*>(a.qa + (m < a.M ? m : a.M - 1) * a.lda + 16 * bl));
     }
     __syncthreads();
 
-    float accf[kCols][MR];
-    int acci[kCols][MR];
+    float accf[MR];
+    int acci[MR];
 #pragma unroll
-    for (int c = 0; c < kCols; ++c)
+    for (int m = 0; m < MR; ++m) {
+        accf[m] = 0.0f;
+        acci[m] = 0;
+    }
+    for (int c0 = sub; c0 < nch; c0 += 16 * kH) {
+        if (c0 != sub) load_chunks(c0);
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            accf[c][m] = 0.0f;
-            acci[c][m] = 0;
-        }
-    for (int ch = lane; ch < nchunks; ch += 64) {
-        load_chunk(ch + 64, next);
-        const int g = ch * kChunkK / 64;
-#pragma unroll
-        for (int c = 0; c < kCols; ++c) {
-            const uint32_t wd[4] = {cur.w[c].x, cur.w[c].y, cur.w[c].z, cur.w[c].w};
+        for (int h = 0; h < kH; ++h) {
+            const int c = c0 + 16 * h;
+            if (c >= nch) break;
+            const int g = c * kChunkK / 64;
             int z = 0;
-            if constexpr (WK == WKind::U4Asym) z = (cur.z[c] >> (4 * (g & 1))) & 0xf;
+            if constexpr (WK == WKind::U4Asym) z = (zb[h] >> (4 * (g & 1))) & 0xf;
             [[maybe_unused]] float s = 0.0f;
             if constexpr (EPI == Epi::GroupScale) {
-                s = f16_bits_to_f32(static_cast<uint16_t>(cur.s[c]));
+                s = f16_bits_to_f32(static_cast<uint16_t>(sb[h]));
                 if constexpr (WK == WKind::I4Sym) s *= 0.0625f;
                 if constexpr (AM == 2) s *= (g & 1) ? -0.0625f : 0.0625f;
             }
+            const uint32_t wd[4] = {w[h].x, w[h].y, w[h].z, w[h].w};
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
-                const uint32_t* xr = act + m * (K / 4) + ch * (kChunkK / 4);
                 int d = 0;
+                if constexpr (WK == WKind::I8) {
+                    const uint4 x = *reinterpret_cast<const uint4*>(act + (m * blocks + c) * 4);
+                    const uint32_t xr[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if constexpr (WK == WKind::I8) {
+                    for (int j = 0; j < 4; ++j)
                         d = __builtin_amdgcn_sdot4(static_cast<int>(wd[j]), static_cast<int>(xr[j]), d, false);
-                    } else if constexpr (WK == WKind::U4Asym) {
-                        d = __builtin_amdgcn_sdot4(static_cast<int>(wd[j] & 0x0f0f0f0fu), static_cast<int>(xr[2 * j]), d, false);
-                        d = __builtin_amdgcn_sdot4(static_cast<int>((wd[j] >> 4) & 0x0f0f0f0fu),
-                                                   static_cast<int>(xr[2 * j + 1]), d, false);
-                    } else {   // signed int4 as 16 v
-                        d = __builtin_amdgcn_sdot4(static_cast<int>((wd[j] << 4) & 0xf0f0f0f0u), static_cast<int>(xr[2 * j]), d, false);
-                        d = __builtin_amdgcn_sdot4(static_cast<int>(wd[j] & 0xf0f0f0f0u), static_cast<int>(xr[2 * j + 1]), d, false);
+                } else {
+                    // weight dword j holds k = 32 c + 8 j .. + 7 (low nibbles the even k): block
+                    // half j / 2 of the chunk, de-interleaved dwords 2 (j % 2) (even) and + 1 (odd)
+                    const uint4 x0 = *reinterpret_cast<const uint4*>(act + (m * blocks + c) * 4);
+                    const uint4 x1 = *reinterpret_cast<const uint4*>(act + (m * blocks + nch + c) * 4);
+                    const uint32_t xr[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t lo = WK == WKind::U4Asym ? wd[j] & 0x0f0f0f0fu : (wd[j] << 4) & 0xf0f0f0f0u;
+                        const uint32_t hi = WK == WKind::U4Asym ? (wd[j] >> 4) & 0x0f0f0f0fu : wd[j] & 0xf0f0f0f0u;
+                        d = __builtin_amdgcn_sdot4(static_cast<int>(lo), static_cast<int>(xr[2 * j]), d, false);
+                        d = __builtin_amdgcn_sdot4(static_cast<int>(hi), static_cast<int>(xr[2 * j + 1]), d, false);
+                    }
+                    if constexpr (WK == WKind::U4Asym) {
+                        const int2 bs = *reinterpret_cast<const int2*>(bsum + m * blocks + 2 * c);
+                        d -= z * (bs.x + bs.y);
                     }
                 }
-                if constexpr (WK == WKind::U4Asym) d -= z * asum[m * nchunks + ch];
                 if constexpr (EPI == Epi::GroupScale) {
-                    accf[c][m] = __builtin_fmaf(static_cast<float>(d), s, accf[c][m]);
+                    accf[m] = __builtin_fmaf(static_cast<float>(d), s, accf[m]);
                 } else if constexpr (EPI == Epi::GroupPartials) {
-                    // chunks 2g and 2g + 1 (the two halves of group g) sit in lanes 2j and 2j + 1 of
-                    // the same iteration; both lanes of a pair are active or inactive together
-                    // (the chunk count is even), so the exchange reads a live lane
+                    // chunks 2g and 2g + 1 sit in lanes 2i and 2i + 1 of the same step (nch is even,
+                    // so both lanes of a pair are inside the row or both past it)
                     static_assert(kPacked, "group partials are defined for 4-bit weights");
                     constexpr int shift = (WK == WKind::I4Sym ? 4 : 0) + (AM == 2 ? 4 : 0);
-                    int pv = (d + __shfl_xor(d, 1, 64)) >> shift;   // exact: a multiple of 2^shift
+                    int pv = (d + __builtin_amdgcn_mov_dpp(d, kQuadXor1, 0xf, 0xf, true)) >> shift;   // exact
                     if (AM == 2 && (g & 1)) pv = -pv;
-                    const int64_t n = n_base + c;
-                    if ((lane & 1) == 0 && m < a.M && n < a.N)
+                    if ((sub & 1) == 0 && m < a.M && col_ok)
                         a.part[(static_cast<int64_t>(g) * a.M + m) * a.N + n] = pv;
                 } else {
-                    acci[c][m] += d;
+                    acci[m] += d;
                 }
             }
         }
-        cur = next;
     }
     if constexpr (EPI == Epi::GroupPartials) return;
-    // wavefront reductions and the epilogue (lane 0 writes)
+    // reductions over the column's 16 lanes; lane 0 of each row writes
 #pragma unroll
-    for (int c = 0; c < kCols; ++c) {
-        const int64_t n = n_base + c;
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            float t;
-            if constexpr (EPI == Epi::GroupScale) {
-                float v = accf[c][m];
-#pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-                t = m < a.M ? v * a.sa[m] : 0.0f;
-            } else {
-                int v = acci[c][m];
-#pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-                if constexpr (WK == WKind::I4Sym) v >>= 4;   // exact: a multiple of 16
-                if constexpr (EPI == Epi::RowAcc) {
-                    if (lane == 0 && m < a.M && n < a.N) a.part[m * a.N + n] = v;
-                    continue;
-                }
-                t = m < a.M && n < a.N ? static_cast<float>(v) * a.sa[m] * a.ws32[n] : 0.0f;
+    for (int m = 0; m < MR; ++m) {
+        float t;
+        if constexpr (EPI == Epi::GroupScale) {
+            const float v = row16_sum(accf[m]);
+            t = m < a.M ? v * a.sa[m] : 0.0f;
+        } else {
+            int v = row16_sum(acci[m]);
+            if constexpr (WK == WKind::I4Sym) v >>= 4;   // exact: a multiple of 16
+            if constexpr (EPI == Epi::RowAcc) {
+                if (sub == 0 && m < a.M && col_ok) a.part[m * a.N + n] = v;
+                continue;
             }
-            if (lane == 0 && m < a.M && n < a.N) {
-                if (a.bias) t += load_as_f32(a.bias, a.bias_dtype, n);
-                store_from_f32(a.y, a.y_dtype, m * a.ldy + n, t);
-            }
+            t = m < a.M && col_ok ? static_cast<float>(v) * a.sa[m] * a.ws32[n] : 0.0f;
+        }
+        if (sub == 0 && m < a.M && col_ok) {
+            if (a.bias) t += load_as_f32(a.bias, a.bias_dtype, n);
+            store_from_f32(a.y, a.y_dtype, m * a.ldy + n, t);
         }
     }
 }
@@ -195,7 +238,7 @@ int launch_rows(const GemmArgs& a, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((a.N + cols - 1) / cols));
 #define MQ_GV(MR)                                                                                       \
     do {                                                                                                \
-        const size_t lds = MR * a.K + (WK == WKind::U4Asym ? MR * (a.K / 32) * 4 : 0);                  \
+        const size_t lds = MR * (a.K / 16) * (16 + (WK == WKind::U4Asym ? 4 : 0));                     \
         auto kern = gemv_kernel<WK, EPI, AM, MR>;                                                       \
         if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),                     \
                                                hipFuncAttributeMaxDynamicSharedMemorySize,              \
