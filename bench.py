@@ -369,10 +369,31 @@ def measure_stack(steps: int = 3) -> dict:
     return out
 
 
+def graph_ms(fn, calls: int) -> float:
+    """GPU time per call of fn without the host: `calls` calls captured in one HIP graph (their
+    kernels, outputs and workspaces from the graph's pool) and replayed; median of 3 rounds of 5
+    replays after 50 ms of untimed replays."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()                                         # warm the allocator on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    ms = time_launches(graph.replay, 5, rounds=3, settle_ms=50.0) / calls
+    del graph
+    return ms
+
+
 def sweep() -> dict:
     """Every BASELINE configuration's linear shapes, timed end to end (rotate + quantize + GEMM +
     epilogue through the drop-in ops; median of 3 rounds of 10 calls after 50 ms of untimed calls,
-    inputs resident) on
+    inputs resident; `gpu_ms` the same calls replayed from a HIP graph, i.e. without the host) on
     random-code quantized weights of each shape, plus the rotate+quantize kernel at config 3's
     two activation widths. Returns {"linears": [...], "rotquant": [...]}."""
     import torch
@@ -415,9 +436,11 @@ def sweep() -> dict:
             fn = lambda: ck.convrot_w4a4_linear(x, qw, s16, bias, convrot_groupsize=hb, quant_group_size=64,  # noqa: E731
                                                 linear_dtype="int4")
         ms = time_launches(fn, 10, rounds=3, settle_ms=50.0)
+        gpu_ms = graph_ms(fn, 10)
         tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         out["linears"].append({"config": cfg, "format": fmt, "M": m, "K": k, "N": n, "hadamard_block": hb,
-                               "ms": round(ms, 5), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)})
+                               "ms": round(ms, 5), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4),
+                               "gpu_ms": round(gpu_ms, 5)})
         print(json.dumps(out["linears"][-1]), file=sys.stderr, flush=True)
         del fn
     acts.clear()

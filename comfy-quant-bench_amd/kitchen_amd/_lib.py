@@ -111,8 +111,13 @@ def ptr(t) -> int | None:
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
-def stream_of(t: torch.Tensor) -> int:
-    """hipStream_t of torch's current stream on t's device (the stream every op enqueues on)."""
+def stream_of_device(device) -> int:
+    """hipStream_t of torch's current stream on a CUDA device (the stream every op enqueues on)."""
     if _raw_stream is not None:
-        return _raw_stream(t.device.index)
-    return torch.cuda.current_stream(t.device).cuda_stream
+        return _raw_stream(device.index)
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """hipStream_t of torch's current stream on t's device."""
+    return stream_of_device(t.device)

@@ -201,6 +201,23 @@ def _check_w4_group_weights(qweight, wscales, wzeros, n, k, group_size):
 
 _WS_BYTES: dict = {}
 
+# Workspaces up to this size are kept per (device, stream) and reused by the next call on that
+# stream (calls on one stream run in order, so they never overlap); larger ones, and every
+# workspace taken while a HIP graph is being captured (the graph's own pool then holds it), are
+# allocated per call.
+WORKSPACE_CACHE_BYTES = 64 << 20
+_WS_CACHE: dict = {}
+
+
+def _scratch(nbytes: int, device) -> torch.Tensor:
+    if nbytes > WORKSPACE_CACHE_BYTES or torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    key = (device.index, _lib.stream_of_device(device))
+    buf = _WS_CACHE.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = _WS_CACHE[key] = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return buf
+
 
 def _workspace(m: int, n: int, k: int, device):
     """Split-K workspace for an M x N x K product when the library wants one (small M), else None.
@@ -210,7 +227,7 @@ def _workspace(m: int, n: int, k: int, device):
     if nbytes is None:
         with torch.cuda.device(device):
             nbytes = _WS_BYTES[key] = int(_lib.load().mq_gemm_workspace_bytes(m, n, k))
-    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes > 0 else None
+    return _scratch(nbytes, device) if nbytes > 0 else None
 
 
 def _linear_workspace(m: int, n: int, k: int, device) -> torch.Tensor:
@@ -221,7 +238,7 @@ def _linear_workspace(m: int, n: int, k: int, device) -> torch.Tensor:
     if nbytes is None:
         with torch.cuda.device(device):
             nbytes = _WS_BYTES[key] = int(_lib.load().mq_linear_workspace_bytes(m, n, k))
-    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return _scratch(nbytes, device)
 
 
 def _bias_args(bias):
