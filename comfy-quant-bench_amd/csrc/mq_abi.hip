@@ -312,10 +312,10 @@ int mq_gemm_rowscale(const int8_t* qa, int64_t lda, const float* sa, const void*
 int64_t mq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     int kgroups = 0;
-    const int64_t tail = split_tail_rows(M, N, K);
+    const int64_t tail = tail_rows(M, N, K);
     if (tail > 0) {
         const int s = choose_ksplit(tail, N, K, INT64_MAX, &kgroups);
-        return static_cast<int64_t>(s) * tail * N * 4;
+        return s > 1 ? static_cast<int64_t>(s) * tail * N * 4 : 0;
     }
     const int s = choose_ksplit(M, N, K, INT64_MAX, &kgroups);
     return s > 1 ? static_cast<int64_t>(s) * M * N * 4 : 0;

@@ -279,25 +279,26 @@ int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     if (a.M > 128 && a.K >= 192 && fits32 && zs_aligned && a.act_mode != 1) {
         GemmArgs w = a;
         w.ksplit = 1;
-        if (a.work && (epi == Epi::GroupScale || epi == Epi::RowScale)) {
-            // a last, nearly empty wave of whole tile rows: those rows split along K, the rest not
-            const int64_t tail = split_tail_rows(a.M, a.N, a.K);
+        w.tile = 0;
+        if (epi == Epi::GroupScale || epi == Epi::RowScale) {
+            const bool int_sums = epi == Epi::RowScale;
+            // a last, nearly empty wave of whole tile rows: those rows run as their own product
+            // (smaller tiles, split along K where the workspace allows), the rest without them
+            const int64_t tail = tail_rows(a.M, a.N, a.K);
             if (tail > 0) {
-                GemmArgs t = a;
+                GemmArgs t = w;
                 t.M = tail;
                 t.qa = a.qa + (a.M - tail) * a.lda;
                 t.sa = a.sa + (a.M - tail);
                 t.y = static_cast<char*>(a.y) + (a.M - tail) * a.ldy * (a.y_dtype == kDtF32 ? 4 : 2);
-                t.ksplit = choose_ksplit(t.M, t.N, t.K, t.work_bytes, &t.kgroups);
-                if (t.ksplit > 1) {
-                    w.M = a.M - tail;
-                    w.work = nullptr;
-                    w.work_bytes = 0;
-                    const int rc = launch_gemm_wide(w, wk, epi, stream);
-                    return rc ? rc : launch_gemm_wide(t, wk, epi, stream);
-                }
+                if (a.work) t.ksplit = choose_ksplit(t.M, t.N, t.K, t.work_bytes, &t.kgroups, int_sums);
+                w.M = a.M - tail;
+                w.work = nullptr;
+                w.work_bytes = 0;
+                const int rc = launch_gemm_wide(w, wk, epi, stream);
+                return rc ? rc : launch_gemm_wide(t, wk, epi, stream);
             }
-            w.ksplit = choose_ksplit(a.M, a.N, a.K, a.work_bytes, &w.kgroups);
+            if (a.work) w.ksplit = choose_ksplit(a.M, a.N, a.K, a.work_bytes, &w.kgroups, int_sums);
         }
         return launch_gemm_wide(w, wk, epi, stream);
     }

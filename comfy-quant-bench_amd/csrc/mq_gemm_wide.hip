@@ -1,9 +1,11 @@
-// Large-tile quantized GEMM for gfx950: 256 x 256 output tile per workgroup of 8 wavefronts,
-// int8 MFMA (v_mfma_i32_16x16x64_i8: one instruction covers one 64-wide K group of a 16 x 16
-// output tile), one K group per k-step.
+// Large-tile quantized GEMM for gfx950: a T x T output tile per workgroup of 2T threads (T = 256:
+// 8 wavefronts; T = 128: 4 wavefronts, two workgroups per compute unit), int8 MFMA
+// (v_mfma_i32_16x16x64_i8: one instruction covers one 64-wide K group of a 16 x 16 output tile),
+// one K group per k-step. The 128 tile serves products whose 256 tiles would leave compute units
+// idle (small M, or N of a few thousand).
 //
-// Layout. Waves form a 4 (M) x 2 (N) grid; each owns a 64 x 128 output tile made of 4 x 8 MFMA
-// 16x16 tiles. In the 16x16 output layout lane l holds column l % 16 and rows 4 * (l / 16) + r,
+// Layout. Waves form a (T / 64) (M) x 2 (N) grid; each owns a 64 x T/2 output tile made of 4 x NJ
+// MFMA 16x16 tiles (NJ = T / 32). In the 16x16 output layout lane l holds column l % 16 and rows 4 * (l / 16) + r,
 // r = 0..3, so every lane needs one weight scale per column tile. A (int8 activation codes) and
 // B (weights, unpacked to int8 on their way into LDS) live in a 4-stage LDS ring of 64-byte rows
 // whose four 16-byte chunks are XOR-swizzled by (row >> 1) & 3: the fragment reads (lane l reads
@@ -12,7 +14,7 @@
 //
 // Pipeline. The main loop is unrolled over four K groups, so the LDS stage (g % 4) and the sign
 // parity (g % 2) of every group are compile-time constants and every LDS access is a base register
-// plus an immediate offset. Inside a group the 32 MFMA tiles run column by column (t = 4 j + i);
+// plus an immediate offset. Inside a group the 4 NJ MFMA tiles run column by column (t = 4 j + i);
 // step t issues tile t's MFMA and then the fmas of tile t - 3, so a result is read three MFMAs
 // after it was produced while the MFMA and VALU pipes overlap. B fragments sit in a 4-slot
 // register ring read three columns ahead; A fragments of group g + 1 are read early in group g.
@@ -57,25 +59,33 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float f2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int TM = 256, TN = 256, TK = 64;
-constexpr int NT = 512;                   // threads per workgroup
+constexpr int TK = 64;
 constexpr int LAG = 3;                    // tile t's fmas run LAG MFMAs after it
 constexpr int kSeed = 0x4B400000;         // bits of 1.5 * 2^23
-
-// LDS map (bytes): 4-stage rings of A tiles, unpacked B tiles and fp32 scales. The output staging
-// of the epilogue reuses the ring region.
 constexpr int NSTAGE = 4;
-constexpr int TILE_BYTES = TM * TK;                       // one A or B stage: 256 rows x 64 bytes
-constexpr int A_LDS = 0;
-constexpr int B_LDS = A_LDS + NSTAGE * TILE_BYTES;        // 65536
-constexpr int S_LDS = B_LDS + NSTAGE * TILE_BYTES;        // 131072: fp32 scales, 1 KB per stage
-constexpr int PIPE_END = S_LDS + NSTAGE * TN * 4;         // 135168
-constexpr int OROW = 136;                                 // 16-bit pitch of the output staging rows
-constexpr int OUT_END = 8 * 64 * OROW * 2;                // 139264
-constexpr int C_LDS = PIPE_END > OUT_END ? PIPE_END : OUT_END;   // per-column offset correction / fp32 scale
-constexpr int R_LDS = C_LDS + TN * 4;                     // per-row activation scales of the tile
-constexpr int BI_LDS = R_LDS + TM * 4;                    // per-column bias of the tile, as fp32
-constexpr int SMEM_BYTES = BI_LDS + TN * 4;
+
+// Tile configuration and LDS map (bytes): 4-stage rings of A tiles, unpacked B tiles and fp32
+// scales; the output staging of the epilogue reuses the ring region. T = 256: A / B stages of
+// 16 KB, scales 1 KB per stage, 137 KB in all; T = 128: 8 KB stages, 67.5 KB in all.
+template <int T>
+struct Cfg {
+    static constexpr int TM = T, TN = T;
+    static constexpr int NT = 2 * T;                          // threads per workgroup
+    static constexpr int NJ = T / 32;                         // MFMA column tiles per wave
+    static constexpr int NTL = 4 * NJ;                        // MFMA tiles per wave and K group
+    static constexpr int TILE_BYTES = T * TK;                 // one A or B stage: T rows x 64 bytes
+    static constexpr int A_LDS = 0;
+    static constexpr int B_LDS = A_LDS + NSTAGE * TILE_BYTES;
+    static constexpr int S_LDS = B_LDS + NSTAGE * TILE_BYTES;
+    static constexpr int PIPE_END = S_LDS + NSTAGE * TN * 4;
+    static constexpr int OROW = NJ * 16 + 8;                  // 16-bit pitch of the output staging rows
+    static constexpr int OUT_END = (NT / 64) * 64 * OROW * 2;
+    static constexpr int C_LDS = PIPE_END > OUT_END ? PIPE_END : OUT_END;   // per-column offset correction / fp32 scale
+    static constexpr int R_LDS = C_LDS + TN * 4;              // per-row activation scales of the tile
+    static constexpr int BI_LDS = R_LDS + TM * 4;             // per-column bias of the tile, as fp32
+    static constexpr int SMEM_BYTES = BI_LDS + TN * 4;
+};
+static_assert(Cfg<256>::SMEM_BYTES <= 160 * 1024 && 2 * Cfg<128>::SMEM_BYTES <= 160 * 1024, "LDS budget");
 
 // byte offset of 16-byte chunk c of tile row r in the swizzled layout
 __device__ __forceinline__ int lds_off(int r, int c) { return r * TK + ((c ^ ((r >> 1) & 3)) << 4); }
@@ -185,20 +195,23 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* smem, i
 
 // LDS stores written as inline asm. The compiler orders every LDS access after a pending LDS DMA
 // (buffer_load ... lds) by waiting for the DMA to complete; these stores never alias a DMA in
-// flight (different ring region or stage), and their completion is awaited explicitly.
+// flight (different ring region or stage), and their completion is awaited explicitly. imm is
+// stage * STRIDE (stage 0..3, known once inlined), taken as the instruction's immediate offset.
+template <int STRIDE>
 __device__ __forceinline__ void ds_write16(int base, int imm, uint4 v) {
     typedef uint32_t u4v __attribute__((ext_vector_type(4)));
     const u4v x = {v.x, v.y, v.z, v.w};
     if (imm == 0) asm volatile("ds_write_b128 %0, %1" ::"v"(base), "v"(x) : "memory");
-    else if (imm == 1 * TM * TK) asm volatile("ds_write_b128 %0, %1 offset:16384" ::"v"(base), "v"(x) : "memory");
-    else if (imm == 2 * TM * TK) asm volatile("ds_write_b128 %0, %1 offset:32768" ::"v"(base), "v"(x) : "memory");
-    else asm volatile("ds_write_b128 %0, %1 offset:49152" ::"v"(base), "v"(x) : "memory");
+    else if (imm == STRIDE) asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(base), "v"(x), "n"(STRIDE) : "memory");
+    else if (imm == 2 * STRIDE) asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(base), "v"(x), "n"(2 * STRIDE) : "memory");
+    else asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(base), "v"(x), "n"(3 * STRIDE) : "memory");
 }
+template <int STRIDE>
 __device__ __forceinline__ void ds_write4(int base, int imm, float v) {
     if (imm == 0) asm volatile("ds_write_b32 %0, %1" ::"v"(base), "v"(v) : "memory");
-    else if (imm == 1 * TN * 4) asm volatile("ds_write_b32 %0, %1 offset:1024" ::"v"(base), "v"(v) : "memory");
-    else if (imm == 2 * TN * 4) asm volatile("ds_write_b32 %0, %1 offset:2048" ::"v"(base), "v"(v) : "memory");
-    else asm volatile("ds_write_b32 %0, %1 offset:3072" ::"v"(base), "v"(v) : "memory");
+    else if (imm == STRIDE) asm volatile("ds_write_b32 %0, %1 offset:%2" ::"v"(base), "v"(v), "n"(STRIDE) : "memory");
+    else if (imm == 2 * STRIDE) asm volatile("ds_write_b32 %0, %1 offset:%2" ::"v"(base), "v"(v), "n"(2 * STRIDE) : "memory");
+    else asm volatile("ds_write_b32 %0, %1 offset:%2" ::"v"(base), "v"(v), "n"(3 * STRIDE) : "memory");
 }
 
 template <typename T>
@@ -206,18 +219,23 @@ __device__ __forceinline__ T& lds(uint8_t* smem, int off) {
     return *reinterpret_cast<T*>(smem + off);
 }
 
-// One workgroup: a 256 x 256 output tile. AM is the activation layout of the group epilogues
+// One workgroup: a T x T output tile. AM is the activation layout of the group epilogues
 // (0 int8 codes; 2 int4 codes stored as 16 * q and negated in odd groups, signed int4 weights then
-// entering as 16 * v); row epilogues use 0.
-template <WKind WK, Epi EPI, int AM, bool SPLIT>
-__global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, int tiles_n) {
+// entering as 16 * v); row epilogues use 0. Both tiles run two waves per SIMD (T = 128: two
+// workgroups per compute unit).
+template <int T, WKind WK, Epi EPI, int AM, bool SPLIT>
+__global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int tiles_m, int tiles_n) {
+    using C = Cfg<T>;
+    constexpr int TM = C::TM, TN = C::TN, NJ = C::NJ, NTL = C::NTL, TILE_BYTES = C::TILE_BYTES;
+    constexpr int A_LDS = C::A_LDS, B_LDS = C::B_LDS, S_LDS = C::S_LDS, OROW = C::OROW;
+    constexpr int C_LDS = C::C_LDS, R_LDS = C::R_LDS, BI_LDS = C::BI_LDS;
     static_assert(!SPLIT || EPI == Epi::GroupScale || EPI == Epi::RowScale, "split-K outputs partial results");
     static_assert(AM == 0 || AM == 2, "activation layout 1 is served by the 128-tile kernel");
     constexpr bool kGroup = EPI == Epi::GroupScale || EPI == Epi::GroupPartials;
     constexpr bool kPacked = WK != WKind::I8;
     constexpr int kShift = kGroup && AM == 2 ? (WK == WKind::I4Sym ? 8 : 4) : 0;
     constexpr float kSfac = 1.0f / static_cast<float>(1 << kShift);
-    __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[C::SMEM_BYTES];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -283,15 +301,15 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     const int s_off = has_s && b_ok ? static_cast<int>(brow * a.ldws * 2) + 4 * bhalf : kOob;
     const int b_st00 = B_LDS + lds_off(brow, 2 * bhalf);
     const int b_st10 = B_LDS + lds_off(brow, 2 * bhalf + 1);
-    // scales stored transposed, [wn][column % 16][column tile], so a lane's 8 scales are adjacent
-    const int s_st0 = S_LDS + 4 * ((((brow >> 7) * 16) + (brow & 15)) * 8 + ((brow & 127) >> 4));
+    // scales stored transposed, [wn][column % 16][column tile], so a lane's NJ scales are adjacent
+    const int s_st0 = S_LDS + 4 * ((((brow / (16 * NJ)) * 16) + (brow & 15)) * NJ + ((brow % (16 * NJ)) >> 4));
 
     // fragment reads: lane l reads chunk l / 16 of row l % 16 of a 16-row block (swizzle depends
     // only on the row within the block, so one per-lane offset serves every block)
     const int fr = lane & 15, fk = ((lane >> 4) ^ ((fr >> 1) & 3)) << 4;
     const int a_rd0 = A_LDS + (wm * 64 + fr) * TK + fk;   // + i * 16 * TK
-    const int b_rd0 = B_LDS + (wn * 128 + fr) * TK + fk;  // + j * 16 * TK
-    const int s_rd0 = S_LDS + 4 * ((wn * 16 + fr) * 8);    // + 4 * j
+    const int b_rd0 = B_LDS + (wn * 16 * NJ + fr) * TK + fk;  // + j * 16 * TK
+    const int s_rd0 = S_LDS + 4 * ((wn * 16 + fr) * NJ);        // + 4 * j
     // opaque LDS base registers: every access below is base + a compile-time offset below 64 KB,
     // which the ds instructions take as an immediate
     int a_rd = a_rd0, b_rd = b_rd0, s_rd = s_rd0, b_st0 = b_st00, b_st1 = b_st10, s_st = s_st0;
@@ -390,7 +408,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             const uint32_t w0 = h ? rb[set].z : rb[set].x, w1 = h ? rb[set].w : rb[set].y;
             unpack_dword<WK, nw, x16>(w0, c, u.x, u.y);
             unpack_dword<WK, nw, x16>(w1, c, u.z, u.w);
-            ds_write16(h ? b_st1 : b_st0, st * TILE_BYTES, u);
+            ds_write16<TILE_BYTES>(h ? b_st1 : b_st0, st * TILE_BYTES, u);
         }
     };
     // scale of group g (position u in its block) by the thread of its row that loaded it
@@ -401,18 +419,18 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             if (bhalf == (u >> 1)) {
                 float sv = f16_bits_to_f32(static_cast<uint16_t>(sq >> (16 * (u & 1)))) * kSfac;   // exact
                 sv = g >= g0 && g < gend ? (neg ? -sv : sv) : 0.0f;
-                ds_write4(s_st, st * TN * 4, sv);
+                ds_write4<TN * 4>(s_st, st * TN * 4, sv);
                 cs += sv;
             }
         }
     };
 
-    float acc[4][8][4];
-    v4i acci[4][8];
+    float acc[4][NJ][4];
+    v4i acci[4][NJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < NJ; ++j) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 acc[i][j][r] = 0.0f;
@@ -421,26 +439,27 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         }
 
     // Fragment registers: A fragments of the current and the next K group (set = g % 2), a 4-slot
-    // ring of B fragments read three columns ahead (slot = column % 4), the scales of columns 0-3
-    // and 4-7 in two register quads, and a 4-slot ring of MFMA results (slot = tile % 4). The ring slots a
+    // ring of B fragments read three columns ahead (slot = column % 4), the column scales in two
+    // register quads (NJ = 8: columns 0-3 and 4-7 of a group; NJ = 4: the four columns of the groups
+    // of parity 0 and 1), and a 4-slot ring of MFMA results (slot = tile % 4). The ring slots a
     // tile or column uses are the same in every group, so the pipeline state at a group boundary
     // does not depend on which unrolled copy ran last. Zeroed results and scales make the first
     // group's look-back fmas add nothing.
     v4i fa[2][4], fb[4], d[4];
-    f4 fs[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};   // scales of columns 0-3, 4-7
+    f4 fs[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
     for (int q = 0; q < 4; ++q) d[q] = v4i{0, 0, 0, 0};
     const v4i seed = {kSeed, kSeed, kSeed, kSeed};
     auto read_a = [&](int st, int set, int i) { fa[set][i] = lds<v4i>(smem, a_rd + st * TILE_BYTES + i * 16 * TK); };
     auto read_b = [&](int st, int col) { fb[col & 3] = lds<v4i>(smem, b_rd + st * TILE_BYTES + col * 16 * TK); };
-    // the 4 scales of columns 4 h .. 4 h + 3 (adjacent in the transposed scale layout)
-    auto read_s = [&](int st, int h) {
-        if constexpr (EPI == Epi::GroupScale) fs[h] = lds<f4>(smem, s_rd + st * TN * 4 + 16 * h);
+    // the 4 scales of columns 4 h .. 4 h + 3 (adjacent in the transposed scale layout) into quad q
+    auto read_s = [&](int st, int h, int q) {
+        if constexpr (EPI == Epi::GroupScale) fs[q] = lds<f4>(smem, s_rd + st * TN * 4 + 16 * h);
     };
     // Partials of tile tp (held in d[tp & 3]) of group gp.
     auto write_partials = [&](int tp, int gp, bool odd) {
         const int ip = tp & 3, jp = tp >> 2;
-        const int64_t col = n0 + wn * 128 + jp * 16 + fr;
+        const int64_t col = n0 + wn * 16 * NJ + jp * 16 + fr;
         int32_t* part = a.part + static_cast<int64_t>(gp) * M * N;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -449,12 +468,13 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             if (row < M && col < N) part[row * N + col] = odd ? -pv : pv;
         }
     };
-    // fmas of tile tp: acc += float(seed + X) * (+-s)
-    auto fma_tile = [&](int tp) {
+    // fmas of tile tp of a group of parity par: acc += float(seed + X) * (+-s)
+    auto fma_tile = [&](int tp, int par) {
         const int ip = tp & 3, jp = tp >> 2;
+        const float sv = NJ == 8 ? fs[jp >> 2][jp & 3] : fs[par][jp & 3];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            acc[ip][jp][r] = __builtin_fmaf(__int_as_float(d[tp & 3][r]), fs[jp >> 2][jp & 3], acc[ip][jp][r]);
+            acc[ip][jp][r] = __builtin_fmaf(__int_as_float(d[tp & 3][r]), sv, acc[ip][jp][r]);
         asm volatile("" : "+v"(acc[ip][jp][0]), "+v"(acc[ip][jp][1]), "+v"(acc[ip][jp][2]), "+v"(acc[ip][jp][3]));
     };
 
@@ -499,8 +519,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     read_b(0, 0);
     read_b(0, 1);
     read_b(0, 2);
-    read_s(0, 0);
-    read_s(0, 1);
+    read_s(0, 0, 0);
+    if constexpr (NJ == 8) read_s(0, 1, 1);
 
     // VMEM instructions per group and thread, in issue order: the DMA of A(g + 3) (and int8 B) at
     // step 0, the packed B load of group g + 4 at step 12 and, in groups with g % 4 == 1, the
@@ -532,7 +552,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         using U2c = std::integral_constant<int, (U + 2) % 4>;   // position of group g + 2 in its block
         constexpr int PAR = PARc::value;
 #pragma unroll
-        for (int t = 0; t < 32; ++t) {
+        for (int t = 0; t < NTL; ++t) {
             const int j = t >> 2, i = t & 3;
             if constexpr (kGroup) {
                 d[t & 3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[SET][i], fb[j & 3], seed, 0, 0, 0);
@@ -542,8 +562,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             }
             __builtin_amdgcn_sched_barrier(0);
             // tile t - LAG (for t < LAG: the last tiles of the previous group)
-            const int tp = (t + 32 - LAG) & 31;
-            if constexpr (EPI == Epi::GroupScale) fma_tile(tp);
+            const int tp = (t + NTL - LAG) & (NTL - 1);
+            if constexpr (EPI == Epi::GroupScale) fma_tile(tp, t < LAG ? PAR ^ 1 : PAR);
             if constexpr (EPI == Epi::GroupPartials) {
                 const int gp = t < LAG ? g - 1 : g;
                 if (gp >= 0 && gp < G) write_partials(tp, gp, t < LAG ? PAR == 0 : PAR == 1);
@@ -552,13 +572,19 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             // B fragments three columns ahead (the next group's first columns from stage ST1,
             // complete since the barrier that ended group g - 1)
             if (i == 0) {
-                if (j + 3 < 8) read_b(ST, j + 3);
-                else read_b(ST1, j + 3 - 8);
+                if (j + 3 < NJ) read_b(ST, j + 3);
+                else read_b(ST1, j + 3 - NJ);
             }
-            // Scales: columns 4-7 once the previous group's column 7 is done (its last fma is at step
-            // 2), columns 0-3 of the next group once column 3 is done (last fma at step 18).
-            if (t == 3) read_s(ST, 1);
-            if (t == 19) read_s(ST1, 0);
+            // Scales. NJ = 8: columns 4-7 once the previous group's column 7 is done (its last fma
+            // is at step 2), columns 0-3 of the next group once column 3 is done (last fma at step
+            // 18). NJ = 4: the next group's columns into the quad of its parity once the previous
+            // group's last fma (step 2) has read that quad.
+            if constexpr (NJ == 8) {
+                if (t == 3) read_s(ST, 1, 1);
+                if (t == 19) read_s(ST1, 0, 0);
+            } else {
+                if (t == 3) read_s(ST1, 0, PAR ^ 1);
+            }
             // the next group's A fragments into the other set, early in this group
             if (i == 2 && j < 4) read_a(ST1, SET ^ 1, j);
             // unpack register set SET (group g + 2, parity PAR) into stage ST2, then reload it with g + 4
@@ -605,8 +631,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // drain: the last LAG tiles of the last group run (dead unless G is a multiple of four)
 #pragma unroll
     for (int t = 0; t < LAG; ++t) {
-        const int tp = 32 - LAG + t;
-        if constexpr (EPI == Epi::GroupScale) fma_tile(tp);
+        const int tp = NTL - LAG + t;
+        if constexpr (EPI == Epi::GroupScale) fma_tile(tp, 1);
         if constexpr (EPI == Epi::GroupPartials)
             if (g1 - 1 < G) write_partials(tp, g1 - 1, true);
     }
@@ -618,8 +644,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int64_t col = n0 + wn * 128 + j * 16 + fr;
+            for (int j = 0; j < NJ; ++j) {
+                const int64_t col = n0 + wn * 16 * NJ + j * 16 + fr;
                 if (col >= N) continue;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -642,8 +668,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         // partial outputs of this K slice: fp32 sum_g s P (offset removed) or the int32 sum
         const int64_t slice_off = static_cast<int64_t>(slice) * M * N;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int lc = wn * 128 + j * 16 + fr;
+        for (int j = 0; j < NJ; ++j) {
+            const int lc = wn * 16 * NJ + j * 16 + fr;
             const int64_t col = n0 + lc;
             if (col >= N) continue;
             float cv = 0.0f;
@@ -664,10 +690,10 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     }
     // column inputs of this lane (the fp32 weight scale or offset correction, the bias) and row
     // scales, all from LDS; rows and columns past the matrix read 0 and are never stored
-    float colv[8], biasv[8];
+    float colv[NJ], biasv[NJ];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int lc = wn * 128 + j * 16 + fr;
+    for (int j = 0; j < NJ; ++j) {
+        const int lc = wn * 16 * NJ + j * 16 + fr;
         colv[j] = lds<float>(smem, C_LDS + 4 * lc);
         biasv[j] = lds<float>(smem, BI_LDS + 4 * lc);
     }
@@ -690,8 +716,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
                 const int64_t row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
                 if (!full && row >= M) continue;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int64_t col = n0 + wn * 128 + j * 16 + fr;
+                for (int j = 0; j < NJ; ++j) {
+                    const int64_t col = n0 + wn * 16 * NJ + j * 16 + fr;
                     if (full || col < N) static_cast<float*>(a.y)[row * a.ldy + col] = out_value(i, j, r, sav[r]);
                 }
             }
@@ -707,7 +733,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             const int lr0 = i * 16 + 4 * (lane >> 4);
             const f4 sav = row_scales(i);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            for (int j = 0; j < NJ; ++j) {
                 const int lc = j * 16 + fr;
 #pragma unroll
                 for (int r = 0; r < 4; r += 2) {
@@ -721,24 +747,25 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     if (a.y_dtype == kDtF16) stage_tile(std::integral_constant<int, kDtF16>{});
     else stage_tile(std::integral_constant<int, kDtBf16>{});
     __syncthreads();
-    const int64_t col0 = n0 + wn * 128;
-    // 16-byte row stores: lane l of iteration it writes chunk (64 it + l) % 16 of staged row
-    // (64 it + l) / 16
+    const int64_t col0 = n0 + wn * 16 * NJ;
+    // 16-byte row stores: a staged row holds 2 NJ chunks of 16 bytes; lane l of iteration it
+    // writes chunk (64 it + l) % (2 NJ) of staged row (64 it + l) / (2 NJ)
+    constexpr int kChunks = 2 * NJ, kStoreIt = 64 * kChunks / 64;
     if (full && (a.ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0) {
         uint16_t* ybase = static_cast<uint16_t*>(a.y) + (m0 + wm * 64) * a.ldy + col0;
 #pragma unroll 4
-        for (int it = 0; it < 16; ++it) {
+        for (int it = 0; it < kStoreIt; ++it) {
             const int c = it * 64 + lane;
-            const int lr = c >> 4, ch = c & 15;
+            const int lr = c / kChunks, ch = c % kChunks;
             *reinterpret_cast<uint4*>(ybase + lr * a.ldy + ch * 8) =
                 *reinterpret_cast<const uint4*>(&stage[lr * OROW + ch * 8]);
         }
         return;
     }
 #pragma unroll 4
-    for (int it = 0; it < 16; ++it) {
+    for (int it = 0; it < kStoreIt; ++it) {
         const int c = it * 64 + lane;
-        const int lr = c >> 4, ch = c & 15;
+        const int lr = c / kChunks, ch = c % kChunks;
         const int64_t row = m0 + wm * 64 + lr;
         const int64_t col = col0 + ch * 8;
         if (row >= M || col >= N) continue;
@@ -821,14 +848,15 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a) {
     }
 }
 
-template <WKind WK, Epi EPI, int AM>
-int launch_one(const GemmArgs& a, hipStream_t stream) {
-    const int tiles_m = static_cast<int>((a.M + TM - 1) / TM);
-    const int tiles_n = static_cast<int>((a.N + TN - 1) / TN);
+template <int T, WKind WK, Epi EPI, int AM>
+int launch_tile(const GemmArgs& a, hipStream_t stream) {
+    const int tiles_m = static_cast<int>((a.M + T - 1) / T);
+    const int tiles_n = static_cast<int>((a.N + T - 1) / T);
     if constexpr (EPI == Epi::GroupScale || EPI == Epi::RowScale) {
         if (a.ksplit > 1) {
-            hipLaunchKernelGGL((gemm_wide_kernel<WK, EPI, AM, true>), dim3(static_cast<unsigned>(tiles_m * tiles_n * a.ksplit)),
-                               dim3(NT), 0, stream, a, tiles_m, tiles_n);
+            hipLaunchKernelGGL((gemm_wide_kernel<T, WK, EPI, AM, true>),
+                               dim3(static_cast<unsigned>(tiles_m * tiles_n * a.ksplit)), dim3(2 * T), 0, stream, a,
+                               tiles_m, tiles_n);
             const int rc = launch_status("gemm_wide");
             if (rc) return rc;
             const int64_t threads = a.M * ((a.N + 7) / 8);
@@ -837,9 +865,18 @@ int launch_one(const GemmArgs& a, hipStream_t stream) {
             return launch_status("gemm_splitk_reduce");
         }
     }
-    hipLaunchKernelGGL((gemm_wide_kernel<WK, EPI, AM, false>), dim3(static_cast<unsigned>(tiles_m * tiles_n)), dim3(NT), 0,
-                       stream, a, tiles_m, tiles_n);
+    hipLaunchKernelGGL((gemm_wide_kernel<T, WK, EPI, AM, false>), dim3(static_cast<unsigned>(tiles_m * tiles_n)),
+                       dim3(2 * T), 0, stream, a, tiles_m, tiles_n);
     return launch_status("gemm_wide");
+}
+
+template <WKind WK, Epi EPI, int AM>
+int launch_one(const GemmArgs& a, hipStream_t stream) {
+    const int t = a.tile ? a.tile : choose_tile(a.M, a.N);
+    if (t == 128) return launch_tile<128, WK, EPI, AM>(a, stream);
+    if (t == 256) return launch_tile<256, WK, EPI, AM>(a, stream);
+    set_error("gemm: tile %d is not 128 or 256", t);
+    return -1;
 }
 
 template <WKind WK, Epi EPI>
@@ -869,15 +906,24 @@ int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
 
 }  // namespace
 
-int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups) {
+int choose_tile(int64_t M, int64_t N) {
+    const int cus = device_cu_count();
+    const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
+    return cus > 0 && 4 * tiles256 <= cus ? 128 : 256;
+}
+
+int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups, bool int_sums) {
     *kgroups = 0;
-    if (M <= 128 || K < 192 || K % TK) return 1;               // the 128-tile kernel has no split
+    if (M <= 128 || K < 192 || K % TK) return 1;               // the few-row kernels have no split
     const int cus = device_cu_count();
     if (cus <= 0) return 1;
-    const int64_t tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+    const int t = choose_tile(M, N);
+    const int64_t tiles = ((M + t - 1) / t) * ((N + t - 1) / t);
     const int64_t blocks = (K / TK + 3) / 4;                    // blocks of four K groups
-    if (2 * tiles > cus || blocks < 4) return 1;
-    // at least two blocks per slice; as many slices as keep every compute unit busy
+    // int32 row-scale sums (no per-group fmas) are quick per K group: their partial outputs pay
+    // for themselves only over a long K
+    if (2 * tiles > cus || blocks < (int_sums ? 16 : 4)) return 1;
+    // at least two blocks per slice; as many slices as give every compute unit a workgroup
     int64_t s = std::min<int64_t>(cus / tiles, blocks / 2);
     const int64_t per = (blocks + s - 1) / s;                   // blocks per slice
     s = (blocks + per - 1) / per;
@@ -886,16 +932,15 @@ int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgro
     return static_cast<int>(s);
 }
 
-int64_t split_tail_rows(int64_t M, int64_t N, int64_t K) {
-    if (M <= TM || K % TK) return 0;
+int64_t tail_rows(int64_t M, int64_t N, int64_t K) {
+    constexpr int64_t T = 256;   // only products on 256 tiles leave such a last wave
+    if (M <= T || K % TK || choose_tile(M, N) != T) return 0;
     const int cus = device_cu_count();
     if (cus <= 0) return 0;
-    const int64_t tiles_m = (M + TM - 1) / TM, tiles_n = (N + TN - 1) / TN;
+    const int64_t tiles_m = (M + T - 1) / T, tiles_n = (N + T - 1) / T;
     const int64_t r = (tiles_m * tiles_n) % cus;   // tiles of the last, partial wave
     if (tiles_m * tiles_n <= cus || r == 0 || r % tiles_n || 4 * r > cus) return 0;
-    const int64_t tail = M - (tiles_m - r / tiles_n) * TM;
-    int kgroups = 0;
-    return choose_ksplit(tail, N, K, INT64_MAX, &kgroups) > 1 ? tail : 0;
+    return M - (tiles_m - r / tiles_n) * T;
 }
 
 int launch_gemm_wide(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {

@@ -75,17 +75,25 @@ struct GemmArgs {
     int kgroups = 0;
     void* work = nullptr;
     int64_t work_bytes = 0;   // capacity of work offered by the caller
+    // output tile of the wide kernel, 256 or 128 (0: choose_tile decides)
+    int tile = 0;
 };
 
-// K slices for a GEMM of this shape with a workspace of work_bytes (1 = no split): used when the
-// 256 x 256 tiles leave most compute units idle (small M).
-int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups);
+// Output tile of the wide kernel for an M x N product: 128 when 256 x 256 tiles would occupy at
+// most a quarter of the compute units, else 256.
+int choose_tile(int64_t M, int64_t N);
 
-// Rows at the end of an M x N product that run as a separate split-K GEMM (0: none): when the
-// 256 x 256 tiles leave a last wave of whole tile rows that would occupy at most a quarter of the
-// compute units (M = 4352 = 4096 + 256 tokens against N = 12288: 816 tiles on 256 units), those
-// rows are split along K instead, so they take a fraction of a tile's time.
-int64_t split_tail_rows(int64_t M, int64_t N, int64_t K);
+// K slices for a GEMM of this shape with a workspace of work_bytes (1 = no split): used when the
+// tiles of choose_tile leave most compute units idle (small M). int_sums: the row-scale epilogue
+// (int32 sums), which splits only over a long K; the group-scale policy never asks for less.
+int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups, bool int_sums = false);
+
+// Rows at the end of an M x N product that run as a separate GEMM (0: none): when the 256 x 256
+// tiles leave a last wave of whole tile rows that would occupy at most a quarter of the compute
+// units (M = 4352 = 4096 + 256 tokens against N = 12288: 816 tiles on 256 units), those rows run
+// on their own, on the tile and K split that choose_tile and choose_ksplit give them, so they take
+// a fraction of a 256 tile's time.
+int64_t tail_rows(int64_t M, int64_t N, int64_t K);
 
 // Power-of-two factor by which a group GEMM's MFMA result exceeds the true partial, per
 // activation layout and weight kind (see mq_gemm_wide.hip).

@@ -192,13 +192,15 @@ int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8
                      int64_t K, void* stream);
 
 /*
- * mq_gemm_w4_group with a caller-provided workspace. When the 256 x 256 output tiles would leave
- * most compute units idle (small M: the text-token linears, the adaLN-sized outputs) the K groups
- * are split into slices, each slice's workgroups write fp32 partial outputs [slices][M][N] into
- * the workspace, and a reduction kernel sums them in slice order (deterministic) and applies
- * sa, bias and the bf16 rounding. For large M whose tiles would leave a last wave of whole tile
- * rows occupying at most a quarter of the compute units (M = 4352 against N = 12288 on 256 units),
- * only those trailing rows are split that way, after the others run unsplit.
+ * mq_gemm_w4_group with a caller-provided workspace. Products whose 256 x 256 output tiles would
+ * occupy at most a quarter of the compute units run on 128 x 128 tiles (with or without a
+ * workspace; the same bits either way). When those tiles still leave most compute units idle
+ * (small M: the text-token linears) the K groups are split into slices, each slice's workgroups
+ * write fp32 partial outputs [slices][M][N] into the workspace, and a reduction kernel sums them
+ * in slice order (deterministic) and applies sa, bias and the bf16 rounding. For large M whose
+ * 256 tiles would leave a last wave of whole tile rows occupying at most a quarter of the compute
+ * units (M = 4352 against N = 12288 on 256 units), those trailing rows run as their own product
+ * after the others, with the tile and split that their own shape gets.
  * mq_gemm_workspace_bytes(M, N, K) gives the size that enables the split on the current device
  * (0: no split for this shape); a smaller or NULL workspace runs without it. No reference
  * counterpart: comfy-kitchen's GEMMs allocate internally.

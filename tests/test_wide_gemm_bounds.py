@@ -1,5 +1,5 @@
-"""Host-side model of the 256 x 256-tile GEMM's global loads (comfy-quant-bench_amd/csrc/
-mq_gemm_wide.hip): for every workgroup, thread role and K group of a launch, the buffer resource
+"""Host-side model of the wide GEMM's global loads (comfy-quant-bench_amd/csrc/mq_gemm_wide.hip,
+both tiles: 256 x 256 with 512 threads and 128 x 128 with 256 threads): for every workgroup, thread role and K group of a launch, the buffer resource
 (base row, byte range), the per-lane vector offset and the wave-uniform scalar offset each load
 uses, restated from the kernel's index arithmetic. Asserts that every load either fails the
 hardware range check on its vector offset (rows past M / N: offset 0x80000000; groups past the
@@ -11,19 +11,19 @@ import itertools
 import numpy as np
 import pytest
 
-TM = TN = 256
 TK = 64
 KOOB = 0x80000000
 
 
-def _loads(M, N, K, ldwz, ldws, kgroups=None, slices=1):
-    """Yield (what, range_bytes, voff, soff, width) for every load lane of a launch (vectorised over
-    lanes with numpy where the arithmetic is per lane)."""
+def _loads(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=256):
+    """Yield (what, range_bytes, voff, soff, width) for every load lane of a launch on T x T tiles
+    of 2T threads (vectorised over lanes with numpy where the arithmetic is per lane)."""
+    TM = TN = T
     G = K // TK
     G4 = (G + 3) // 4 * 4
     tiles_m, tiles_n = -(-M // TM), -(-N // TN)
     lda, ldw = K, K // 2
-    tid = np.arange(512)
+    tid = np.arange(2 * T)
     wave, lane = tid >> 6, tid & 63
     for tm, tn, s in itertools.product(range(tiles_m), range(tiles_n), range(slices)):
         m0, n0 = tm * TM, tn * TN
@@ -67,11 +67,11 @@ def _loads(M, N, K, ldwz, ldws, kgroups=None, slices=1):
                 yield "S", rs if live else 0, s_voff, 2 * b4 if live else 0, 4
 
 
-def _check(M, N, K, ldwz=None, ldws=None, kgroups=None, slices=1, loads=None):
+def _check(M, N, K, ldwz=None, ldws=None, kgroups=None, slices=1, loads=None, T=256):
     G = K // TK
     ldwz = ldwz if ldwz is not None else ((G + 1) // 2 + 1) // 2 * 2   # the wide kernel needs even strides
     ldws = ldws if ldws is not None else (G + 1) // 2 * 2
-    for what, rng, voff, soff, width in (loads or _loads)(M, N, K, ldwz, ldws, kgroups, slices):
+    for what, rng, voff, soff, width in (loads or _loads)(M, N, K, ldwz, ldws, kgroups, slices, T):
         voff = np.asarray(voff, dtype=np.int64)
         masked = voff >= rng                       # fails the range check: zeros, no memory access
         ok = masked | ((voff >= 0) & (voff + soff + width <= rng))
@@ -79,19 +79,21 @@ def _check(M, N, K, ldwz=None, ldws=None, kgroups=None, slices=1, loads=None):
                           f"width {width} (M={M} N={N} K={K})")
 
 
+@pytest.mark.parametrize("t", [256, 128])
 @pytest.mark.parametrize("k", [192, 256, 320, 384, 448, 1472, 3072, 3136])
 @pytest.mark.parametrize("m,n", [(257, 300), (300, 256), (513, 400)])
-def test_every_load_stays_in_its_range(m, n, k):
-    _check(m, n, k)
+def test_every_load_stays_in_its_range(m, n, k, t):
+    _check(m, n, k, T=t)
 
 
+@pytest.mark.parametrize("t", [256, 128])
 @pytest.mark.parametrize("k", [320, 1472, 3072, 3200])
-def test_split_k_slices_stay_in_range(k):
+def test_split_k_slices_stay_in_range(k, t):
     g = k // 64
     blocks = (g + 3) // 4
     per = max(2, blocks // 3)
     slices = -(-blocks // per)
-    _check(256, 520, k, kgroups=per * 4, slices=slices)
+    _check(256, 520, k, kgroups=per * 4, slices=slices, T=t)
 
 
 @pytest.mark.parametrize("which", ["S", "Z"])
@@ -99,11 +101,11 @@ def test_model_catches_an_offset_past_the_range(which):
     # planted mistakes: the scale dword or the zero-point word of the last block loaded without
     # moving back on the tile's last weight row (the kernel's loads before that correction) must be
     # reported for K / 64 = 5 (the block 4..7 runs past G)
-    def unshifted(M, N, K, ldwz, ldws, kgroups=None, slices=1):
-        tid = np.arange(512)
+    def unshifted(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=256):
+        tid = np.arange(2 * T)
         brow, bhalf = tid >> 1, tid & 1
-        rows_n = min(TN, N)
-        for what, rng, voff, soff, width in _loads(M, N, K, ldwz, ldws, kgroups, slices):
+        rows_n = min(T, N)
+        for what, rng, voff, soff, width in _loads(M, N, K, ldwz, ldws, kgroups, slices, T):
             if what == which == "S":
                 voff = np.where(brow < rows_n, brow * ldws * 2 + 4 * bhalf, KOOB)
             if what == which == "Z":
