@@ -1,11 +1,10 @@
-// Large-tile quantized GEMM for gfx950: a T x T output tile per workgroup of 2T threads (T = 256:
-// 8 wavefronts; T = 128: 4 wavefronts, two workgroups per compute unit), int8 MFMA
-// (v_mfma_i32_16x16x64_i8: one instruction covers one 64-wide K group of a 16 x 16 output tile),
-// one K group per k-step. The 128 tile serves products whose 256 tiles would leave compute units
-// idle (small M, or N of a few thousand).
+// Large-tile quantized GEMM for gfx950: a T x T output tile (T = 256 or 128) per workgroup of 8
+// wavefronts, int8 MFMA (v_mfma_i32_16x16x64_i8: one instruction covers one 64-wide K group of a
+// 16 x 16 output tile), one K group per k-step. The 128 tile serves products whose 256 tiles
+// would leave most compute units idle (small M).
 //
-// Layout. Waves form a (T / 64) (M) x 2 (N) grid; each owns a 64 x T/2 output tile made of 4 x NJ
-// MFMA 16x16 tiles (NJ = T / 32). In the 16x16 output layout lane l holds column l % 16 and rows 4 * (l / 16) + r,
+// Layout. Waves form a 4 (M) x 2 (N) grid; each owns a T/4 x T/2 output tile made of NI x NJ MFMA
+// 16x16 tiles (4 x 8 for T = 256, 2 x 4 for T = 128). In the 16x16 output layout lane l holds column l % 16 and rows 4 * (l / 16) + r,
 // r = 0..3, so every lane needs one weight scale per column tile. A (int8 activation codes) and
 // B (weights, unpacked to int8 on their way into LDS) live in a 4-stage LDS ring of 64-byte rows
 // whose four 16-byte chunks are XOR-swizzled by (row >> 1) & 3: the fragment reads (lane l reads
@@ -14,13 +13,13 @@
 //
 // Pipeline. The main loop is unrolled over four K groups, so the LDS stage (g % 4) and the sign
 // parity (g % 2) of every group are compile-time constants and every LDS access is a base register
-// plus an immediate offset. Inside a group the 4 NJ MFMA tiles run column by column (t = 4 j + i);
+// plus an immediate offset. Inside a group the NI NJ MFMA tiles run column by column (t = NI j + i);
 // step t issues tile t's MFMA and then the fmas of tile t - 3, so a result is read three MFMAs
 // after it was produced while the MFMA and VALU pipes overlap. B fragments sit in a 4-slot
 // register ring read three columns ahead; A fragments of group g + 1 are read early in group g.
 // A tiles go from HBM to LDS by buffer_load ... lds, three groups ahead; packed B is loaded into
 // one of two register sets four groups ahead (inline-asm loads with explicit vmcnt waits), unpacked
-// into the stage of group g + 2 at steps 8-9, and one barrier per group closes the ring.
+// into the stage of group g + 2 mid-group, and one barrier per group closes the ring.
 // Zero-points and scales are loaded once per block of four groups (one 2-byte and one 4-byte load
 // per weight row), not per group: each such load touches one cache line per row, and per-group
 // loads of 1-2 bytes per row were a third of the kernel's L1 -> L2 requests.
@@ -67,25 +66,29 @@ constexpr int NSTAGE = 4;
 // Tile configuration and LDS map (bytes): 4-stage rings of A tiles, unpacked B tiles and fp32
 // scales; the output staging of the epilogue reuses the ring region. T = 256: A / B stages of
 // 16 KB, scales 1 KB per stage, 137 KB in all; T = 128: 8 KB stages, 67.5 KB in all.
+constexpr int NT = 512;                                       // threads per workgroup: 8 waves
 template <int T>
 struct Cfg {
     static constexpr int TM = T, TN = T;
-    static constexpr int NT = 2 * T;                          // threads per workgroup
-    static constexpr int NJ = T / 32;                         // MFMA column tiles per wave
-    static constexpr int NTL = 4 * NJ;                        // MFMA tiles per wave and K group
+    static constexpr int WR = T / 4, WC = T / 2;              // wave tile (4 x 2 waves)
+    static constexpr int NI = WR / 16, NJ = WC / 16;          // MFMA row / column tiles per wave
+    static constexpr int NTL = NI * NJ;                       // MFMA tiles per wave and K group
+    static constexpr int NH = T / 128;                        // 1 KB DMA blocks per wave and K group
+    static constexpr int TPR = NT / T;                        // threads per packed weight row
+    static constexpr int BPT = 32 / TPR;                      // packed B bytes per thread and K group
     static constexpr int TILE_BYTES = T * TK;                 // one A or B stage: T rows x 64 bytes
     static constexpr int A_LDS = 0;
     static constexpr int B_LDS = A_LDS + NSTAGE * TILE_BYTES;
     static constexpr int S_LDS = B_LDS + NSTAGE * TILE_BYTES;
     static constexpr int PIPE_END = S_LDS + NSTAGE * TN * 4;
-    static constexpr int OROW = NJ * 16 + 8;                  // 16-bit pitch of the output staging rows
-    static constexpr int OUT_END = (NT / 64) * 64 * OROW * 2;
+    static constexpr int OROW = WC + 8;                       // 16-bit pitch of the output staging rows
+    static constexpr int OUT_END = (NT / 64) * WR * OROW * 2;
     static constexpr int C_LDS = PIPE_END > OUT_END ? PIPE_END : OUT_END;   // per-column offset correction / fp32 scale
     static constexpr int R_LDS = C_LDS + TN * 4;              // per-row activation scales of the tile
     static constexpr int BI_LDS = R_LDS + TM * 4;             // per-column bias of the tile, as fp32
     static constexpr int SMEM_BYTES = BI_LDS + TN * 4;
 };
-static_assert(Cfg<256>::SMEM_BYTES <= 160 * 1024 && 2 * Cfg<128>::SMEM_BYTES <= 160 * 1024, "LDS budget");
+static_assert(Cfg<256>::SMEM_BYTES <= 160 * 1024 && Cfg<128>::SMEM_BYTES <= 160 * 1024, "LDS budget");
 
 // byte offset of 16-byte chunk c of tile row r in the swizzled layout
 __device__ __forceinline__ int lds_off(int r, int c) { return r * TK + ((c ^ ((r >> 1) & 3)) << 4); }
@@ -175,6 +178,12 @@ __device__ __forceinline__ u4v asm_ld128(u4v d, int voff, int soff) {
     asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
     return v;
 }
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u2v asm_ld64(u4v d, int voff, int soff) {
+    u2v v;
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx2 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
+    return v;
+}
 __device__ __forceinline__ uint32_t asm_ld32(u4v d, int voff, int soff) {
     uint32_t v;
     asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
@@ -221,12 +230,12 @@ __device__ __forceinline__ T& lds(uint8_t* smem, int off) {
 
 // One workgroup: a T x T output tile. AM is the activation layout of the group epilogues
 // (0 int8 codes; 2 int4 codes stored as 16 * q and negated in odd groups, signed int4 weights then
-// entering as 16 * v); row epilogues use 0. Both tiles run two waves per SIMD (T = 128: two
-// workgroups per compute unit).
+// entering as 16 * v); row epilogues use 0.
 template <int T, WKind WK, Epi EPI, int AM, bool SPLIT>
-__global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int tiles_m, int tiles_n) {
+__global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, int tiles_n) {
     using C = Cfg<T>;
-    constexpr int TM = C::TM, TN = C::TN, NJ = C::NJ, NTL = C::NTL, TILE_BYTES = C::TILE_BYTES;
+    constexpr int TM = C::TM, TN = C::TN, NI = C::NI, NJ = C::NJ, NTL = C::NTL, TILE_BYTES = C::TILE_BYTES;
+    constexpr int WR = C::WR, WC = C::WC, NH = C::NH, TPR = C::TPR;
     constexpr int A_LDS = C::A_LDS, B_LDS = C::B_LDS, S_LDS = C::S_LDS, OROW = C::OROW;
     constexpr int C_LDS = C::C_LDS, R_LDS = C::R_LDS, BI_LDS = C::BI_LDS;
     static_assert(!SPLIT || EPI == Epi::GroupScale || EPI == Epi::RowScale, "split-K outputs partial results");
@@ -273,24 +282,26 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     const auto ra_rs = rsrc(a.qa + m0 * a.lda, (rows_m - 1) * a.lda + a.K);
     const auto rb_rs = rsrc(a.qw + n0 * a.ldw, (rows_n - 1) * a.ldw + kbytes_w);
 
-    // ---- DMA roles (A, and int8 B): wave w copies tile rows [32 w, 32 w + 32) of a K group as two
-    // 1 KB blocks. Lane l of block h writes LDS bytes [16 l, 16 l + 16) of tile rows
-    // 32 w + 16 h + l / 4; that is physical chunk l % 4 of the swizzled row, so it fetches logical
-    // chunk (l % 4) ^ swizzle(row).
-    int dma_a[2], dma_b[2];
+    // ---- DMA roles (A, and int8 B): wave w copies tile rows [16 NH w, 16 NH (w + 1)) of a K group
+    // as NH 1 KB blocks. Lane l of block h writes LDS bytes [16 l, 16 l + 16) of tile row
+    // 16 NH w + 16 h + l / 4; that is physical chunk l % 4 of the swizzled row, so it fetches
+    // logical chunk (l % 4) ^ swizzle(row).
+    int dma_a[NH], dma_b[NH];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int r = 32 * wave + 16 * h + (lane >> 2);
+    for (int h = 0; h < NH; ++h) {
+        const int r = 16 * NH * wave + 16 * h + (lane >> 2);
         const int c = (lane & 3) ^ ((r >> 1) & 3);
         dma_a[h] = r < rows_m ? static_cast<int>(r * a.lda) + c * 16 : kOob;
         dma_b[h] = r < rows_n ? static_cast<int>(r * a.ldw) + c * 16 : kOob;
     }
-    const int dma_lds = (32 * wave) * TK;   // + 16 * TK for block 1
+    const int dma_lds = (16 * NH * wave) * TK;   // + 16 * TK for block h
 
-    // ---- packed B roles: 2 threads per weight row, 16 packed bytes (32 weights) each
-    const int brow = tid >> 1, bhalf = tid & 1;
+    // ---- packed B roles: TPR threads per weight row (2 for T = 256, 4 for T = 128), 32 / TPR packed
+    // bytes (64 / TPR weights, 16-byte LDS chunks 2 bpart and 2 bpart + 1, or chunk bpart) each; the
+    // threads with bpart < 2 also carry the row's scales (bhalf = bpart)
+    const int brow = tid / TPR, bpart = tid % TPR, bhalf = bpart & 1;
     const bool b_ok = brow < rows_n;
-    const int b_off = b_ok ? static_cast<int>(brow * a.ldw) + bhalf * 16 : kOob;
+    const int b_off = b_ok ? static_cast<int>(brow * a.ldw) + bpart * C::BPT : kOob;
     // zero-points and scales (null for the kinds that have none: the range is then empty)
     const bool has_z = WK == WKind::U4Asym, has_s = EPI == Epi::GroupScale;
     const u4v db = sdesc(a.qw + n0 * a.ldw, (rows_n - 1) * a.ldw + kbytes_w);
@@ -298,17 +309,17 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     const u4v ds = sdesc(has_s ? static_cast<const void*>(a.ws16 + n0 * a.ldws) : a.qw,
                          has_s ? ((rows_n - 1) * a.ldws + G) * 2 : 0);
     const int z_off = has_z && b_ok ? static_cast<int>(brow * a.ldwz) : kOob;
-    const int s_off = has_s && b_ok ? static_cast<int>(brow * a.ldws * 2) + 4 * bhalf : kOob;
-    const int b_st00 = B_LDS + lds_off(brow, 2 * bhalf);
-    const int b_st10 = B_LDS + lds_off(brow, 2 * bhalf + 1);
+    const int s_off = has_s && b_ok && bpart < 2 ? static_cast<int>(brow * a.ldws * 2) + 4 * bhalf : kOob;
+    const int b_st00 = B_LDS + lds_off(brow, TPR == 2 ? 2 * bpart : bpart);
+    const int b_st10 = B_LDS + lds_off(brow, TPR == 2 ? 2 * bpart + 1 : bpart);
     // scales stored transposed, [wn][column % 16][column tile], so a lane's NJ scales are adjacent
-    const int s_st0 = S_LDS + 4 * ((((brow / (16 * NJ)) * 16) + (brow & 15)) * NJ + ((brow % (16 * NJ)) >> 4));
+    const int s_st0 = S_LDS + 4 * ((((brow / WC) * 16) + (brow & 15)) * NJ + ((brow % WC) >> 4));
 
     // fragment reads: lane l reads chunk l / 16 of row l % 16 of a 16-row block (swizzle depends
     // only on the row within the block, so one per-lane offset serves every block)
     const int fr = lane & 15, fk = ((lane >> 4) ^ ((fr >> 1) & 3)) << 4;
-    const int a_rd0 = A_LDS + (wm * 64 + fr) * TK + fk;   // + i * 16 * TK
-    const int b_rd0 = B_LDS + (wn * 16 * NJ + fr) * TK + fk;  // + j * 16 * TK
+    const int a_rd0 = A_LDS + (wm * WR + fr) * TK + fk;   // + i * 16 * TK
+    const int b_rd0 = B_LDS + (wn * WC + fr) * TK + fk;   // + j * 16 * TK
     const int s_rd0 = S_LDS + 4 * ((wn * 16 + fr) * NJ);        // + 4 * j
     // opaque LDS base registers: every access below is base + a compile-time offset below 64 KB,
     // which the ds instructions take as an immediate
@@ -327,7 +338,7 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     auto dma_group = [&](int g, int st) {
         const bool live = g < G;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < NH; ++h) {
             dma16(live ? ra_rs : ra_none, smem, A_LDS + st * TILE_BYTES + dma_lds + h * 16 * TK, dma_a[h],
                   soff(g, TK));
             if constexpr (!kPacked)
@@ -336,9 +347,13 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
         }
     };
     // Two register sets carry packed B groups from their global load to their LDS store.
-    u4v rb[2] = {u4v{0u, 0u, 0u, 0u}, u4v{0u, 0u, 0u, 0u}};
+    using BV = std::conditional_t<TPR == 2, u4v, u2v>;
+    BV rb[2] = {BV{}, BV{}};
     auto gload_b = [&](int g, int set) {
-        if constexpr (kPacked) rb[set] = asm_ld128(g < G ? db : d_none, b_off, soff(g, TK / 2));
+        if constexpr (kPacked) {
+            if constexpr (TPR == 2) rb[set] = asm_ld128(g < G ? db : d_none, b_off, soff(g, TK / 2));
+            else rb[set] = asm_ld64(g < G ? db : d_none, b_off, soff(g, TK / 2));
+        }
     };
     // Zero-points and scales of a block of four K groups b4 .. b4 + 3 (b4 % 4 == 0), one load each
     // per block instead of one per group: zq holds the four zero-point nibbles (group b4 + u in
@@ -391,8 +406,8 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     // the wait, so no use of it moves above it.
 #define MQ_WAIT_B(N, SET) \
     asm volatile("s_waitcnt vmcnt(%3)" : "+v"(rb[SET]), "+v"(zq), "+v"(sq) : "n"(N) : "memory")
-    // sum_g (-1)^g s[n, g] over the groups whose scale this thread stores (half of them: the two
-    // threads of a weight row add their sums in the epilogue)
+    // sum_g (-1)^g s[n, g] over the groups whose scale this thread stores (half of them: threads
+    // bpart 0 and 1 of a weight row, adjacent lanes, add their sums in the epilogue)
     float cs = 0.0f;
     // LDS stores of register set `set` (a group of parity PAR) into stage ST, in two halves of the
     // unpacked row (spread over two steps) and the scale.
@@ -405,7 +420,13 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
             constexpr int pos = decltype(Uc)::value;
             const uint32_t c = unpack_const<WK, nw>((zq >> (4 * pos)) & 0xfu);
             uint4 u;
-            const uint32_t w0 = h ? rb[set].z : rb[set].x, w1 = h ? rb[set].w : rb[set].y;
+            uint32_t w0 = rb[set].x, w1 = rb[set].y;
+            if constexpr (TPR == 2) {
+                if (h) {
+                    w0 = rb[set].z;
+                    w1 = rb[set].w;
+                }
+            }
             unpack_dword<WK, nw, x16>(w0, c, u.x, u.y);
             unpack_dword<WK, nw, x16>(w1, c, u.z, u.w);
             ds_write16<TILE_BYTES>(h ? b_st1 : b_st0, st * TILE_BYTES, u);
@@ -416,7 +437,7 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
         if constexpr (EPI == Epi::GroupScale) {
             constexpr bool neg = decltype(PARc)::value == 1;
             constexpr int u = decltype(Uc)::value;
-            if (bhalf == (u >> 1)) {
+            if (bpart == (u >> 1)) {
                 float sv = f16_bits_to_f32(static_cast<uint16_t>(sq >> (16 * (u & 1)))) * kSfac;   // exact
                 sv = g >= g0 && g < gend ? (neg ? -sv : sv) : 0.0f;
                 ds_write4<TN * 4>(s_st, st * TN * 4, sv);
@@ -425,10 +446,10 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
         }
     };
 
-    float acc[4][NJ][4];
-    v4i acci[4][NJ];
+    float acc[NI][NJ][4];
+    v4i acci[NI][NJ];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
 #pragma unroll
@@ -445,7 +466,7 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     // tile or column uses are the same in every group, so the pipeline state at a group boundary
     // does not depend on which unrolled copy ran last. Zeroed results and scales make the first
     // group's look-back fmas add nothing.
-    v4i fa[2][4], fb[4], d[4];
+    v4i fa[2][NI], fb[4], d[4];
     f4 fs[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
     for (int q = 0; q < 4; ++q) d[q] = v4i{0, 0, 0, 0};
@@ -458,19 +479,19 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     };
     // Partials of tile tp (held in d[tp & 3]) of group gp.
     auto write_partials = [&](int tp, int gp, bool odd) {
-        const int ip = tp & 3, jp = tp >> 2;
-        const int64_t col = n0 + wn * 16 * NJ + jp * 16 + fr;
+        const int ip = tp % NI, jp = tp / NI;
+        const int64_t col = n0 + wn * WC + jp * 16 + fr;
         int32_t* part = a.part + static_cast<int64_t>(gp) * M * N;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int64_t row = m0 + wm * 64 + ip * 16 + 4 * (lane >> 4) + r;
+            const int64_t row = m0 + wm * WR + ip * 16 + 4 * (lane >> 4) + r;
             const int32_t pv = (d[tp & 3][r] - kSeed) >> kShift;   // exact: a multiple of 2^kShift
             if (row < M && col < N) part[row * N + col] = odd ? -pv : pv;
         }
     };
     // fmas of tile tp of a group of parity par: acc += float(seed + X) * (+-s)
     auto fma_tile = [&](int tp, int par) {
-        const int ip = tp & 3, jp = tp >> 2;
+        const int ip = tp % NI, jp = tp / NI;
         const float sv = NJ == 8 ? fs[jp >> 2][jp & 3] : fs[par][jp & 3];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -503,7 +524,7 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     if constexpr (kFinal) {
         if (tid < TM) {
             lds<float>(smem, R_LDS + 4 * tid) = ep_a;
-        } else {
+        } else if (tid - TM < TN) {
             lds<float>(smem, BI_LDS + 4 * (tid - TM)) = ep_a;
             if constexpr (EPI == Epi::RowScale) lds<float>(smem, C_LDS + 4 * (tid - TM)) = ep_b;
         }
@@ -515,7 +536,7 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 4; ++i) read_a(0, 0, i);
+    for (int i = 0; i < NI; ++i) read_a(0, 0, i);
     read_b(0, 0);
     read_b(0, 1);
     read_b(0, 2);
@@ -523,10 +544,13 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     if constexpr (NJ == 8) read_s(0, 1, 1);
 
     // VMEM instructions per group and thread, in issue order: the DMA of A(g + 3) (and int8 B) at
-    // step 0, the packed B load of group g + 4 at step 12 and, in groups with g % 4 == 1, the
+    // step 0, the packed B load of group g + 4 at step kTL and, in groups with g % 4 == 1, the
     // zero-points and scales of the block g + 3 .. g + 6 right after it. Waits count the VMEM
     // operations issued after the one awaited.
-    constexpr int kDmaOps = kPacked ? 2 : 4;
+    constexpr int kDmaOps = NH * (kPacked ? 1 : 2);
+    // steps of the B unpack (kTB: wait for the registers, store; kTB + 1: second half for T = 256),
+    // of the scale store (kTS) and of the next packed B load (kTL); kTB > 0 follows the DMA of step 0
+    constexpr int kTB = NTL == 32 ? 8 : 4, kTS = NTL == 32 ? 10 : 5, kTL = NTL == 32 ? 12 : 6;
     constexpr int kB = kPacked ? 1 : 0;
     constexpr int kZS = (WK == WKind::U4Asym) + (EPI == Epi::GroupScale);
     // Before the barrier that ends group g, A(g + 2) (issued at step 0 of group g - 1) must be
@@ -535,7 +559,7 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     constexpr int kVmAfter[4] = {
         EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB, EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB + kZS,
         EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB + kZS, EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB};
-    // At step 8 of group g, register set g % 2 (B(g + 2), loaded at step 12 of group g - 2) must
+    // At step kTB of group g, register set g % 2 (B(g + 2), loaded at step kTL of group g - 2) must
     // have arrived, and in groups with g % 4 == 2 the block of zero-points and scales loaded at the
     // end of group g - 1. Issued after B(g + 2): [zs if g % 4 == 3], A(g + 2), B(g + 3),
     // [zs if g % 4 == 2], A(g + 3).
@@ -544,7 +568,7 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
         EPI == Epi::GroupPartials ? 0 : (kZS > 0 ? kDmaOps : 2 * kDmaOps + kB),
         EPI == Epi::GroupPartials ? 0 : 2 * kDmaOps + kB + kZS};
 
-    // K group g with A stage, B stage and register set fixed by U = g % 4 (compile-time). Step t = 4 j + i.
+    // K group g with A stage, B stage and register set fixed by U = g % 4 (compile-time). Step t = NI j + i.
     auto group = [&](int g, auto Uc) {
         constexpr int U = decltype(Uc)::value;
         constexpr int ST = U, ST1 = (U + 1) % 4, ST2 = (U + 2) % 4, ST3 = (U + 3) % 4, SET = U % 2;
@@ -553,7 +577,7 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
         constexpr int PAR = PARc::value;
 #pragma unroll
         for (int t = 0; t < NTL; ++t) {
-            const int j = t >> 2, i = t & 3;
+            const int j = t / NI, i = t % NI;
             if constexpr (kGroup) {
                 d[t & 3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[SET][i], fb[j & 3], seed, 0, 0, 0);
             } else {
@@ -586,28 +610,31 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
                 if (t == 3) read_s(ST1, 0, PAR ^ 1);
             }
             // the next group's A fragments into the other set, early in this group
-            if (i == 2 && j < 4) read_a(ST1, SET ^ 1, j);
+            if (i == (NI == 4 ? 2 : 1) && j < NI) read_a(ST1, SET ^ 1, j);
             // unpack register set SET (group g + 2, parity PAR) into stage ST2, then reload it with g + 4
-            if (t == 8) {
+            if (t == kTB) {
                 MQ_WAIT_B(kWaitB[U], SET);
                 // group g + 2 opens the block of zero-points and scales loaded in group g - 1
                 if constexpr (U == 2) settle_zs();
                 store_b(ST2, SET, PARc{}, U2c{}, 0);
             }
-            if (t == 9) store_b(ST2, SET, PARc{}, U2c{}, 1);
-            if (t == 10) store_s(ST2, g + 2, PARc{}, U2c{});
-            if (t == 12) {
+            if constexpr (TPR == 2)
+                if (t == kTB + 1) store_b(ST2, SET, PARc{}, U2c{}, 1);
+            if (t == kTS) store_s(ST2, g + 2, PARc{}, U2c{});
+            if (t == kTL) {
                 gload_b(g + 4, SET);
                 if constexpr (U == 1) gload_zs(g + 3);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        // A(g + 2) and this group's B stores become visible to every wave. LDS operations of a wave
-        // complete in issue order, and the MFMAs of steps 16-31 waited for fragment reads issued
-        // after the stores of steps 8-10, so those stores are complete here without a wait. Group
-        // g's own stages were last read by MFMAs that have issued; the next group's fragment reads
-        // stay in flight across the barrier.
+        // A(g + 2) and this group's B stores become visible to every wave. T = 256: LDS operations of
+        // a wave complete in issue order, and the MFMAs of steps 24-27 waited for a fragment read
+        // issued after the stores of steps 8-10, so those stores are complete here without a wait
+        // and the next group's fragment reads stay in flight across the barrier. T = 128: no MFMA of
+        // the group reads a fragment issued after the stores, so the wave waits for its LDS
+        // operations here. Group g's own stages were last read by MFMAs that have issued.
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kVmAfter[U]) : "memory");
+        if constexpr (NTL < 32) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
@@ -642,14 +669,14 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
 
     if constexpr (EPI == Epi::RowAcc) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                const int64_t col = n0 + wn * 16 * NJ + j * 16 + fr;
+                const int64_t col = n0 + wn * WC + j * 16 + fr;
                 if (col >= N) continue;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int64_t row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
+                    const int64_t row = m0 + wm * WR + i * 16 + 4 * (lane >> 4) + r;
                     if (row < M) a.part[row * N + col] = acci[i][j][r];
                 }
             }
@@ -661,7 +688,7 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     __syncthreads();   // every wave is done with the pipeline stages the staging area reuses
     if constexpr (EPI == Epi::GroupScale) {
         const float cs_row = cs + __shfl_xor(cs, 1, 64);   // the two threads of the row
-        if (bhalf == 0) lds<float>(smem, C_LDS + 4 * brow) = cs_row * kMagic;
+        if (bpart == 0) lds<float>(smem, C_LDS + 4 * brow) = cs_row * kMagic;
         __syncthreads();
     }
     if constexpr (SPLIT) {
@@ -669,16 +696,16 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
         const int64_t slice_off = static_cast<int64_t>(slice) * M * N;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            const int lc = wn * 16 * NJ + j * 16 + fr;
+            const int lc = wn * WC + j * 16 + fr;
             const int64_t col = n0 + lc;
             if (col >= N) continue;
             float cv = 0.0f;
             if constexpr (EPI == Epi::GroupScale) cv = lds<float>(smem, C_LDS + 4 * lc);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < NI; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int64_t row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
+                    const int64_t row = m0 + wm * WR + i * 16 + 4 * (lane >> 4) + r;
                     if (row >= M) continue;
                     if constexpr (EPI == Epi::GroupScale)
                         static_cast<float*>(a.work)[slice_off + row * N + col] = acc[i][j][r] - cv;
@@ -693,12 +720,12 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     float colv[NJ], biasv[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        const int lc = wn * 16 * NJ + j * 16 + fr;
+        const int lc = wn * WC + j * 16 + fr;
         colv[j] = lds<float>(smem, C_LDS + 4 * lc);
         biasv[j] = lds<float>(smem, BI_LDS + 4 * lc);
     }
     // the row scales of rows 4 (lane / 16) + 0..3 of row block i
-    auto row_scales = [&](int i) { return lds<f4>(smem, R_LDS + 4 * (wm * 64 + i * 16 + 4 * (lane >> 4))); };
+    auto row_scales = [&](int i) { return lds<f4>(smem, R_LDS + 4 * (wm * WR + i * 16 + 4 * (lane >> 4))); };
     // y[m, n] in fp32 before the rounding to the output type
     auto out_value = [&](int i, int j, int r, float sa_r) {
         if constexpr (EPI == Epi::GroupScale) return __builtin_fmaf(acc[i][j][r] - colv[j], sa_r, biasv[j]);
@@ -709,27 +736,27 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
         // fp32 outputs straight from the registers: the 16 lanes of a row segment write 64
         // consecutive bytes
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NI; ++i) {
             const f4 sav = row_scales(i);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
+                const int64_t row = m0 + wm * WR + i * 16 + 4 * (lane >> 4) + r;
                 if (!full && row >= M) continue;
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) {
-                    const int64_t col = n0 + wn * 16 * NJ + j * 16 + fr;
+                    const int64_t col = n0 + wn * WC + j * 16 + fr;
                     if (full || col < N) static_cast<float*>(a.y)[row * a.ldy + col] = out_value(i, j, r, sav[r]);
                 }
             }
         }
         return;
     }
-    uint16_t* stage = reinterpret_cast<uint16_t*>(smem) + wave * 64 * OROW;
+    uint16_t* stage = reinterpret_cast<uint16_t*>(smem) + wave * WR * OROW;
     // the staging loop once per 16-bit output type (a wave-uniform branch outside the loop)
     auto stage_tile = [&](auto DTc) {
         constexpr int DT = decltype(DTc)::value;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NI; ++i) {
             const int lr0 = i * 16 + 4 * (lane >> 4);
             const f4 sav = row_scales(i);
 #pragma unroll
@@ -747,12 +774,12 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     if (a.y_dtype == kDtF16) stage_tile(std::integral_constant<int, kDtF16>{});
     else stage_tile(std::integral_constant<int, kDtBf16>{});
     __syncthreads();
-    const int64_t col0 = n0 + wn * 16 * NJ;
+    const int64_t col0 = n0 + wn * WC;
     // 16-byte row stores: a staged row holds 2 NJ chunks of 16 bytes; lane l of iteration it
     // writes chunk (64 it + l) % (2 NJ) of staged row (64 it + l) / (2 NJ)
-    constexpr int kChunks = 2 * NJ, kStoreIt = 64 * kChunks / 64;
+    constexpr int kChunks = 2 * NJ, kStoreIt = WR * kChunks / 64;
     if (full && (a.ldy % 8) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0) {
-        uint16_t* ybase = static_cast<uint16_t*>(a.y) + (m0 + wm * 64) * a.ldy + col0;
+        uint16_t* ybase = static_cast<uint16_t*>(a.y) + (m0 + wm * WR) * a.ldy + col0;
 #pragma unroll 4
         for (int it = 0; it < kStoreIt; ++it) {
             const int c = it * 64 + lane;
@@ -766,7 +793,7 @@ __global__ void __launch_bounds__(2 * T, 2) gemm_wide_kernel(GemmArgs a, int til
     for (int it = 0; it < kStoreIt; ++it) {
         const int c = it * 64 + lane;
         const int lr = c / kChunks, ch = c % kChunks;
-        const int64_t row = m0 + wm * 64 + lr;
+        const int64_t row = m0 + wm * WR + lr;
         const int64_t col = col0 + ch * 8;
         if (row >= M || col >= N) continue;
         const uint4 v = *reinterpret_cast<const uint4*>(&stage[lr * OROW + ch * 8]);
@@ -855,7 +882,7 @@ int launch_tile(const GemmArgs& a, hipStream_t stream) {
     if constexpr (EPI == Epi::GroupScale || EPI == Epi::RowScale) {
         if (a.ksplit > 1) {
             hipLaunchKernelGGL((gemm_wide_kernel<T, WK, EPI, AM, true>),
-                               dim3(static_cast<unsigned>(tiles_m * tiles_n * a.ksplit)), dim3(2 * T), 0, stream, a,
+                               dim3(static_cast<unsigned>(tiles_m * tiles_n * a.ksplit)), dim3(NT), 0, stream, a,
                                tiles_m, tiles_n);
             const int rc = launch_status("gemm_wide");
             if (rc) return rc;
@@ -866,7 +893,7 @@ int launch_tile(const GemmArgs& a, hipStream_t stream) {
         }
     }
     hipLaunchKernelGGL((gemm_wide_kernel<T, WK, EPI, AM, false>), dim3(static_cast<unsigned>(tiles_m * tiles_n)),
-                       dim3(2 * T), 0, stream, a, tiles_m, tiles_n);
+                       dim3(NT), 0, stream, a, tiles_m, tiles_n);
     return launch_status("gemm_wide");
 }
 
@@ -909,7 +936,7 @@ int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
 int choose_tile(int64_t M, int64_t N) {
     const int cus = device_cu_count();
     const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
-    return cus > 0 && 4 * tiles256 <= cus ? 128 : 256;
+    return cus > 0 && 2 * tiles256 <= cus ? 128 : 256;
 }
 
 int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups, bool int_sums) {

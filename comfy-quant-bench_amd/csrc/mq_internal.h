@@ -80,7 +80,7 @@ struct GemmArgs {
 };
 
 // Output tile of the wide kernel for an M x N product: 128 when 256 x 256 tiles would occupy at
-// most a quarter of the compute units, else 256.
+// most half of the compute units, else 256.
 int choose_tile(int64_t M, int64_t N);
 
 // K slices for a GEMM of this shape with a workspace of work_bytes (1 = no split): used when the

@@ -193,7 +193,7 @@ int mq_gemm_w4_group(const int8_t* qa, int64_t lda, const float* sa, const uint8
 
 /*
  * mq_gemm_w4_group with a caller-provided workspace. Products whose 256 x 256 output tiles would
- * occupy at most a quarter of the compute units run on 128 x 128 tiles (with or without a
+ * occupy at most half of the compute units run on 128 x 128 tiles (with or without a
  * workspace; the same bits either way). When those tiles still leave most compute units idle
  * (small M: the text-token linears) the K groups are split into slices, each slice's workgroups
  * write fp32 partial outputs [slices][M][N] into the workspace, and a reduction kernel sums them

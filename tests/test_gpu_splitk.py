@@ -130,10 +130,10 @@ def test_tail_rows_split(gpu_device, n):
 
 @pytest.mark.parametrize("wk", ["u4", "i4x16", "i8"])
 def test_tiles_agree_bitwise(gpu_device, wk):
-    """The first 1024 rows of a 2304-row product (9 x 12 tiles of 256 at N = 3072) equal the
+    """The first 1024 rows of a 2816-row product (11 x 12 tiles of 256 at N = 3072) equal the
     1024-row product of the same rows (4 x 12 tiles of 256, so 128 tiles): every output runs the
     same arithmetic in the same order whatever the tile."""
-    n, k, m_small, m_big = 3072, 3072, 1024, 2304
+    n, k, m_small, m_big = 3072, 3072, 1024, 2816
     print(f"[splitk] tiles agree {wk} M={m_small}/{m_big} N={n} K={k}", flush=True)
     rng = np.random.default_rng(5)
     bias = torch.randn(n, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(gpu_device)

@@ -1,5 +1,5 @@
 """Host-side model of the wide GEMM's global loads (comfy-quant-bench_amd/csrc/mq_gemm_wide.hip,
-both tiles: 256 x 256 with 512 threads and 128 x 128 with 256 threads): for every workgroup, thread role and K group of a launch, the buffer resource
+both tiles, 256 x 256 and 128 x 128, each with 512 threads): for every workgroup, thread role and K group of a launch, the buffer resource
 (base row, byte range), the per-lane vector offset and the wave-uniform scalar offset each load
 uses, restated from the kernel's index arithmetic. Asserts that every load either fails the
 hardware range check on its vector offset (rows past M / N: offset 0x80000000; groups past the
@@ -17,13 +17,16 @@ KOOB = 0x80000000
 
 def _loads(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=256):
     """Yield (what, range_bytes, voff, soff, width) for every load lane of a launch on T x T tiles
-    of 2T threads (vectorised over lanes with numpy where the arithmetic is per lane)."""
+    of 512 threads (vectorised over lanes with numpy where the arithmetic is per lane)."""
     TM = TN = T
+    NH = T // 128            # 1 KB DMA blocks per wave and K group
+    TPR = 512 // T           # threads per packed weight row
+    BPT = 32 // TPR          # packed bytes each of them loads per K group
     G = K // TK
     G4 = (G + 3) // 4 * 4
     tiles_m, tiles_n = -(-M // TM), -(-N // TN)
     lda, ldw = K, K // 2
-    tid = np.arange(2 * T)
+    tid = np.arange(512)
     wave, lane = tid >> 6, tid & 63
     for tm, tn, s in itertools.product(range(tiles_m), range(tiles_n), range(slices)):
         m0, n0 = tm * TM, tn * TN
@@ -34,23 +37,24 @@ def _loads(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=256):
         rb = (rows_n - 1) * ldw + K // 2
         rz = (rows_n - 1) * ldwz + (G + 1) // 2
         rs = ((rows_n - 1) * ldws + G) * 2
-        # A DMA: wave w copies rows 32 w + 16 h + lane / 4, chunk lane % 4 (swizzled)
+        # A DMA: wave w copies rows 16 NH w + 16 h + lane / 4, chunk lane % 4 (swizzled)
         dma = []
-        for h in range(2):
-            r = 32 * wave + 16 * h + (lane >> 2)
+        for h in range(NH):
+            r = 16 * NH * wave + 16 * h + (lane >> 2)
             c = (lane & 3) ^ ((r >> 1) & 3)
             dma.append(np.where(r < rows_m, r * lda + c * 16, KOOB))
-        brow, bhalf = tid >> 1, tid & 1
+        brow, bpart = tid // TPR, tid % TPR
+        bhalf = bpart & 1
         b_ok = brow < rows_n
-        b_off = np.where(b_ok, brow * ldw + bhalf * 16, KOOB)
+        b_off = np.where(b_ok, brow * ldw + bpart * BPT, KOOB)
         z_off = np.where(b_ok, brow * ldwz, KOOB)
-        s_off = np.where(b_ok, brow * ldws * 2 + 4 * bhalf, KOOB)
+        s_off = np.where(b_ok & (bpart < 2), brow * ldws * 2 + 4 * bhalf, KOOB)
         last = brow == rows_n - 1
         for g in range(g0, g1):
             live = g < G
-            for h in range(2):
+            for h in range(NH):
                 yield "A", ra if live else 0, dma[h], g * TK if live else 0, 16
-            yield "B", rb if live else 0, b_off, g * (TK // 2) if live else 0, 16
+            yield "B", rb if live else 0, b_off, g * (TK // 2) if live else 0, BPT
             if g % 4 == 0:
                 b4 = g
                 # zero-points of groups b4 .. b4 + 3 (two bytes) and scales of b4 + 2 bhalf,
@@ -96,21 +100,22 @@ def test_split_k_slices_stay_in_range(k, t):
     _check(256, 520, k, kgroups=per * 4, slices=slices, T=t)
 
 
+@pytest.mark.parametrize("t", [256, 128])
 @pytest.mark.parametrize("which", ["S", "Z"])
-def test_model_catches_an_offset_past_the_range(which):
+def test_model_catches_an_offset_past_the_range(which, t):
     # planted mistakes: the scale dword or the zero-point word of the last block loaded without
     # moving back on the tile's last weight row (the kernel's loads before that correction) must be
     # reported for K / 64 = 5 (the block 4..7 runs past G)
     def unshifted(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=256):
-        tid = np.arange(2 * T)
-        brow, bhalf = tid >> 1, tid & 1
+        tid = np.arange(512)
+        brow, bpart = tid // (512 // T), tid % (512 // T)
         rows_n = min(T, N)
         for what, rng, voff, soff, width in _loads(M, N, K, ldwz, ldws, kgroups, slices, T):
             if what == which == "S":
-                voff = np.where(brow < rows_n, brow * ldws * 2 + 4 * bhalf, KOOB)
+                voff = np.where((brow < rows_n) & (bpart < 2), brow * ldws * 2 + 4 * (bpart & 1), KOOB)
             if what == which == "Z":
                 voff = np.where(brow < rows_n, brow * ldwz, KOOB)
             yield what, rng, voff, soff, width
 
     with pytest.raises(AssertionError, match=f"{which} load"):
-        _check(300, 200, 320, loads=unshifted)
+        _check(300, 200, 320, loads=unshifted, T=t)
