@@ -310,15 +310,8 @@ int mq_gemm_rowscale(const int8_t* qa, int64_t lda, const float* sa, const void*
 }
 
 int64_t mq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-    if (M <= 0 || N <= 0 || K <= 0) return 0;
-    int kgroups = 0;
-    const int64_t tail = tail_rows(M, N, K);
-    if (tail > 0) {
-        const int s = choose_ksplit(tail, N, K, INT64_MAX, &kgroups);
-        return s > 1 ? static_cast<int64_t>(s) * tail * N * 4 : 0;
-    }
-    const int s = choose_ksplit(M, N, K, INT64_MAX, &kgroups);
-    return s > 1 ? static_cast<int64_t>(s) * M * N * 4 : 0;
+    // the larger of what the group-scale and the row-scale GEMM would use
+    return std::max(workspace_bytes(M, N, K, false), workspace_bytes(M, N, K, true));
 }
 
 int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t ldw, int wbits, int32_t* acc,

@@ -1,10 +1,11 @@
-// Large-tile quantized GEMM for gfx950: a T x T output tile (T = 256 or 128) per workgroup of 8
-// wavefronts, int8 MFMA (v_mfma_i32_16x16x64_i8: one instruction covers one 64-wide K group of a
-// 16 x 16 output tile), one K group per k-step. The 128 tile serves products whose 256 tiles
-// would leave most compute units idle (small M).
+// Large-tile quantized GEMM for gfx950: a TM x TN output tile (256 x 256, 256 x 192 or 128 x 128)
+// per workgroup of 8 wavefronts, int8 MFMA (v_mfma_i32_16x16x64_i8: one instruction covers one
+// 64-wide K group of a 16 x 16 output tile), one K group per k-step. The 128 tile serves products
+// whose 256 tiles would leave most compute units idle (small M); the 256 x 192 tile fills the last
+// wave of row-scale products such as N = 3072 (16 tile columns instead of 12).
 //
-// Layout. Waves form a 4 (M) x 2 (N) grid; each owns a T/4 x T/2 output tile made of NI x NJ MFMA
-// 16x16 tiles (4 x 8 for T = 256, 2 x 4 for T = 128). In the 16x16 output layout lane l holds column l % 16 and rows 4 * (l / 16) + r,
+// Layout. Waves form a 4 (M) x 2 (N) grid; each owns a TM/4 x TN/2 output tile made of NI x NJ MFMA
+// 16x16 tiles (4 x 8, 4 x 6 or 2 x 4). In the 16x16 output layout lane l holds column l % 16 and rows 4 * (l / 16) + r,
 // r = 0..3, so every lane needs one weight scale per column tile. A (int8 activation codes) and
 // B (weights, unpacked to int8 on their way into LDS) live in a 4-stage LDS ring of 64-byte rows
 // whose four 16-byte chunks are XOR-swizzled by (row >> 1) & 3: the fragment reads (lane l reads
@@ -64,19 +65,21 @@ constexpr int kSeed = 0x4B400000;         // bits of 1.5 * 2^23
 constexpr int NSTAGE = 4;
 
 // Tile configuration and LDS map (bytes): 4-stage rings of A tiles, unpacked B tiles and fp32
-// scales; the output staging of the epilogue reuses the ring region. T = 256: A / B stages of
-// 16 KB, scales 1 KB per stage, 137 KB in all; T = 128: 8 KB stages, 67.5 KB in all.
+// scales; the output staging of the epilogue reuses the ring region. The B stages have TM rows like
+// the A stages, so every thread keeps the same load and store roles; rows TN .. TM - 1 of a B stage
+// (256 x 192 tile) receive only zeros and are never read. 256 tiles: A / B stages of 16 KB, 137 KB
+// in all; 128 tile: 8 KB stages, 67.5 KB in all.
 constexpr int NT = 512;                                       // threads per workgroup: 8 waves
-template <int T>
+template <int TM_, int TN_>
 struct Cfg {
-    static constexpr int TM = T, TN = T;
-    static constexpr int WR = T / 4, WC = T / 2;              // wave tile (4 x 2 waves)
+    static constexpr int TM = TM_, TN = TN_;
+    static constexpr int WR = TM / 4, WC = TN / 2;            // wave tile (4 x 2 waves)
     static constexpr int NI = WR / 16, NJ = WC / 16;          // MFMA row / column tiles per wave
     static constexpr int NTL = NI * NJ;                       // MFMA tiles per wave and K group
-    static constexpr int NH = T / 128;                        // 1 KB DMA blocks per wave and K group
-    static constexpr int TPR = NT / T;                        // threads per packed weight row
+    static constexpr int NH = TM / 128;                       // 1 KB DMA blocks per wave and K group
+    static constexpr int TPR = NT / TM;                       // threads per packed weight row
     static constexpr int BPT = 32 / TPR;                      // packed B bytes per thread and K group
-    static constexpr int TILE_BYTES = T * TK;                 // one A or B stage: T rows x 64 bytes
+    static constexpr int TILE_BYTES = TM * TK;                // one A or B stage: TM rows x 64 bytes
     static constexpr int A_LDS = 0;
     static constexpr int B_LDS = A_LDS + NSTAGE * TILE_BYTES;
     static constexpr int S_LDS = B_LDS + NSTAGE * TILE_BYTES;
@@ -88,7 +91,11 @@ struct Cfg {
     static constexpr int BI_LDS = R_LDS + TM * 4;             // per-column bias of the tile, as fp32
     static constexpr int SMEM_BYTES = BI_LDS + TN * 4;
 };
-static_assert(Cfg<256>::SMEM_BYTES <= 160 * 1024 && Cfg<128>::SMEM_BYTES <= 160 * 1024, "LDS budget");
+static_assert(Cfg<256, 256>::SMEM_BYTES <= 160 * 1024 && Cfg<256, 192>::SMEM_BYTES <= 160 * 1024 &&
+                  Cfg<128, 128>::SMEM_BYTES <= 160 * 1024, "LDS budget");
+
+// Tile codes of GemmArgs::tile / choose_tile: the output tile's N extent (256 and 192: 256 rows).
+constexpr int tile_rows(int code) { return code == 128 ? 128 : 256; }
 
 // byte offset of 16-byte chunk c of tile row r in the swizzled layout
 __device__ __forceinline__ int lds_off(int r, int c) { return r * TK + ((c ^ ((r >> 1) & 3)) << 4); }
@@ -231,9 +238,9 @@ __device__ __forceinline__ T& lds(uint8_t* smem, int off) {
 // One workgroup: a T x T output tile. AM is the activation layout of the group epilogues
 // (0 int8 codes; 2 int4 codes stored as 16 * q and negated in odd groups, signed int4 weights then
 // entering as 16 * v); row epilogues use 0.
-template <int T, WKind WK, Epi EPI, int AM, bool SPLIT>
+template <int TM_, int TN_, WKind WK, Epi EPI, int AM, bool SPLIT>
 __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, int tiles_n) {
-    using C = Cfg<T>;
+    using C = Cfg<TM_, TN_>;
     constexpr int TM = C::TM, TN = C::TN, NI = C::NI, NJ = C::NJ, NTL = C::NTL, TILE_BYTES = C::TILE_BYTES;
     constexpr int WR = C::WR, WC = C::WC, NH = C::NH, TPR = C::TPR;
     constexpr int A_LDS = C::A_LDS, B_LDS = C::B_LDS, S_LDS = C::S_LDS, OROW = C::OROW;
@@ -437,7 +444,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         if constexpr (EPI == Epi::GroupScale) {
             constexpr bool neg = decltype(PARc)::value == 1;
             constexpr int u = decltype(Uc)::value;
-            if (bpart == (u >> 1)) {
+            if (bpart == (u >> 1) && (TN == TM || brow < TN)) {
                 float sv = f16_bits_to_f32(static_cast<uint16_t>(sq >> (16 * (u & 1)))) * kSfac;   // exact
                 sv = g >= g0 && g < gend ? (neg ? -sv : sv) : 0.0f;
                 ds_write4<TN * 4>(s_st, st * TN * 4, sv);
@@ -460,7 +467,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         }
 
     // Fragment registers: A fragments of the current and the next K group (set = g % 2), a 4-slot
-    // ring of B fragments read three columns ahead (slot = column % 4), the column scales in two
+    // ring of B fragments read three columns ahead (slot = running column count % 4), the column scales in two
     // register quads (NJ = 8: columns 0-3 and 4-7 of a group; NJ = 4: the four columns of the groups
     // of parity 0 and 1), and a 4-slot ring of MFMA results (slot = tile % 4). The ring slots a
     // tile or column uses are the same in every group, so the pipeline state at a group boundary
@@ -472,7 +479,9 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     for (int q = 0; q < 4; ++q) d[q] = v4i{0, 0, 0, 0};
     const v4i seed = {kSeed, kSeed, kSeed, kSeed};
     auto read_a = [&](int st, int set, int i) { fa[set][i] = lds<v4i>(smem, a_rd + st * TILE_BYTES + i * 16 * TK); };
-    auto read_b = [&](int st, int col) { fb[col & 3] = lds<v4i>(smem, b_rd + st * TILE_BYTES + col * 16 * TK); };
+    // B column col of a stage into ring slot `slot`: the slot of column j of group g is
+    // (g NJ + j) % 4, a running column count, so the ring wraps across groups for every NJ
+    auto read_b = [&](int st, int col, int slot) { fb[slot] = lds<v4i>(smem, b_rd + st * TILE_BYTES + col * 16 * TK); };
     // the 4 scales of columns 4 h .. 4 h + 3 (adjacent in the transposed scale layout) into quad q
     auto read_s = [&](int st, int h, int q) {
         if constexpr (EPI == Epi::GroupScale) fs[q] = lds<f4>(smem, s_rd + st * TN * 4 + 16 * h);
@@ -492,7 +501,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // fmas of tile tp of a group of parity par: acc += float(seed + X) * (+-s)
     auto fma_tile = [&](int tp, int par) {
         const int ip = tp % NI, jp = tp / NI;
-        const float sv = NJ == 8 ? fs[jp >> 2][jp & 3] : fs[par][jp & 3];
+        const float sv = NJ >= 6 ? fs[jp >> 2][jp & 3] : fs[par][jp & 3];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             acc[ip][jp][r] = __builtin_fmaf(__int_as_float(d[tp & 3][r]), sv, acc[ip][jp][r]);
@@ -537,11 +546,11 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = 0; i < NI; ++i) read_a(0, 0, i);
-    read_b(0, 0);
-    read_b(0, 1);
-    read_b(0, 2);
+    read_b(0, 0, 0);
+    read_b(0, 1, 1);
+    read_b(0, 2, 2);
     read_s(0, 0, 0);
-    if constexpr (NJ == 8) read_s(0, 1, 1);
+    if constexpr (NJ >= 6) read_s(0, 1, 1);
 
     // VMEM instructions per group and thread, in issue order: the DMA of A(g + 3) (and int8 B) at
     // step 0, the packed B load of group g + 4 at step kTL and, in groups with g % 4 == 1, the
@@ -550,7 +559,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     constexpr int kDmaOps = NH * (kPacked ? 1 : 2);
     // steps of the B unpack (kTB: wait for the registers, store; kTB + 1: second half for T = 256),
     // of the scale store (kTS) and of the next packed B load (kTL); kTB > 0 follows the DMA of step 0
-    constexpr int kTB = NTL == 32 ? 8 : 4, kTS = NTL == 32 ? 10 : 5, kTL = NTL == 32 ? 12 : 6;
+    constexpr int kTB = NTL >= 24 ? 8 : 4, kTS = NTL >= 24 ? 10 : 5, kTL = NTL >= 24 ? 12 : 6;
     constexpr int kB = kPacked ? 1 : 0;
     constexpr int kZS = (WK == WKind::U4Asym) + (EPI == Epi::GroupScale);
     // Before the barrier that ends group g, A(g + 2) (issued at step 0 of group g - 1) must be
@@ -579,14 +588,14 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         for (int t = 0; t < NTL; ++t) {
             const int j = t / NI, i = t % NI;
             if constexpr (kGroup) {
-                d[t & 3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[SET][i], fb[j & 3], seed, 0, 0, 0);
+                d[t & 3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[SET][i], fb[(PAR * NJ + j) & 3], seed, 0, 0, 0);
             } else {
                 asm volatile("" : "+a"(acci[i][j]));
-                acci[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[SET][i], fb[j & 3], acci[i][j], 0, 0, 0);
+                acci[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[SET][i], fb[(PAR * NJ + j) & 3], acci[i][j], 0, 0, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
             // tile t - LAG (for t < LAG: the last tiles of the previous group)
-            const int tp = (t + NTL - LAG) & (NTL - 1);
+            const int tp = (t + NTL - LAG) % NTL;
             if constexpr (EPI == Epi::GroupScale) fma_tile(tp, t < LAG ? PAR ^ 1 : PAR);
             if constexpr (EPI == Epi::GroupPartials) {
                 const int gp = t < LAG ? g - 1 : g;
@@ -596,14 +605,14 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             // B fragments three columns ahead (the next group's first columns from stage ST1,
             // complete since the barrier that ended group g - 1)
             if (i == 0) {
-                if (j + 3 < NJ) read_b(ST, j + 3);
-                else read_b(ST1, j + 3 - NJ);
+                if (j + 3 < NJ) read_b(ST, j + 3, (PAR * NJ + j + 3) & 3);
+                else read_b(ST1, j + 3 - NJ, (PAR * NJ + j + 3) & 3);
             }
             // Scales. NJ = 8: columns 4-7 once the previous group's column 7 is done (its last fma
             // is at step 2), columns 0-3 of the next group once column 3 is done (last fma at step
             // 18). NJ = 4: the next group's columns into the quad of its parity once the previous
             // group's last fma (step 2) has read that quad.
-            if constexpr (NJ == 8) {
+            if constexpr (NJ >= 6) {
                 if (t == 3) read_s(ST, 1, 1);
                 if (t == 19) read_s(ST1, 0, 0);
             } else {
@@ -627,14 +636,14 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        // A(g + 2) and this group's B stores become visible to every wave. T = 256: LDS operations of
-        // a wave complete in issue order, and the MFMAs of steps 24-27 waited for a fragment read
+        // A(g + 2) and this group's B stores become visible to every wave. 256 x 256: LDS operations
+        // of a wave complete in issue order, and the MFMAs of steps 24-27 waited for a fragment read
         // issued after the stores of steps 8-10, so those stores are complete here without a wait
-        // and the next group's fragment reads stay in flight across the barrier. T = 128: no MFMA of
-        // the group reads a fragment issued after the stores, so the wave waits for its LDS
+        // and the next group's fragment reads stay in flight across the barrier. The other tiles: no
+        // MFMA of the group reads a fragment issued after the stores, so the wave waits for its LDS
         // operations here. Group g's own stages were last read by MFMAs that have issued.
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kVmAfter[U]) : "memory");
-        if constexpr (NTL < 32) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if constexpr (NJ != 8) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
@@ -688,7 +697,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     __syncthreads();   // every wave is done with the pipeline stages the staging area reuses
     if constexpr (EPI == Epi::GroupScale) {
         const float cs_row = cs + __shfl_xor(cs, 1, 64);   // the two threads of the row
-        if (bpart == 0) lds<float>(smem, C_LDS + 4 * brow) = cs_row * kMagic;
+        if (bpart == 0 && (TN == TM || brow < TN)) lds<float>(smem, C_LDS + 4 * brow) = cs_row * kMagic;
         __syncthreads();
     }
     if constexpr (SPLIT) {
@@ -875,13 +884,13 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a) {
     }
 }
 
-template <int T, WKind WK, Epi EPI, int AM>
+template <int TM, int TN, WKind WK, Epi EPI, int AM>
 int launch_tile(const GemmArgs& a, hipStream_t stream) {
-    const int tiles_m = static_cast<int>((a.M + T - 1) / T);
-    const int tiles_n = static_cast<int>((a.N + T - 1) / T);
+    const int tiles_m = static_cast<int>((a.M + TM - 1) / TM);
+    const int tiles_n = static_cast<int>((a.N + TN - 1) / TN);
     if constexpr (EPI == Epi::GroupScale || EPI == Epi::RowScale) {
         if (a.ksplit > 1) {
-            hipLaunchKernelGGL((gemm_wide_kernel<T, WK, EPI, AM, true>),
+            hipLaunchKernelGGL((gemm_wide_kernel<TM, TN, WK, EPI, AM, true>),
                                dim3(static_cast<unsigned>(tiles_m * tiles_n * a.ksplit)), dim3(NT), 0, stream, a,
                                tiles_m, tiles_n);
             const int rc = launch_status("gemm_wide");
@@ -892,17 +901,18 @@ int launch_tile(const GemmArgs& a, hipStream_t stream) {
             return launch_status("gemm_splitk_reduce");
         }
     }
-    hipLaunchKernelGGL((gemm_wide_kernel<T, WK, EPI, AM, false>), dim3(static_cast<unsigned>(tiles_m * tiles_n)),
+    hipLaunchKernelGGL((gemm_wide_kernel<TM, TN, WK, EPI, AM, false>), dim3(static_cast<unsigned>(tiles_m * tiles_n)),
                        dim3(NT), 0, stream, a, tiles_m, tiles_n);
     return launch_status("gemm_wide");
 }
 
 template <WKind WK, Epi EPI, int AM>
 int launch_one(const GemmArgs& a, hipStream_t stream) {
-    const int t = a.tile ? a.tile : choose_tile(a.M, a.N);
-    if (t == 128) return launch_tile<128, WK, EPI, AM>(a, stream);
-    if (t == 256) return launch_tile<256, WK, EPI, AM>(a, stream);
-    set_error("gemm: tile %d is not 128 or 256", t);
+    const int t = a.tile ? a.tile : choose_tile(a.M, a.N, EPI == Epi::RowScale || EPI == Epi::RowAcc);
+    if (t == 128) return launch_tile<128, 128, WK, EPI, AM>(a, stream);
+    if (t == 192) return launch_tile<256, 192, WK, EPI, AM>(a, stream);
+    if (t == 256) return launch_tile<256, 256, WK, EPI, AM>(a, stream);
+    set_error("gemm: tile code %d is not 128, 192 or 256", t);
     return -1;
 }
 
@@ -933,10 +943,16 @@ int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
 
 }  // namespace
 
-int choose_tile(int64_t M, int64_t N) {
+int choose_tile(int64_t M, int64_t N, bool int_sums) {
     const int cus = device_cu_count();
-    const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
-    return cus > 0 && 2 * tiles256 <= cus ? 128 : 256;
+    if (cus <= 0) return 256;
+    const int64_t tm = (M + 255) / 256, tiles256 = tm * ((N + 255) / 256), tiles192 = tm * ((N + 191) / 192);
+    if (2 * tiles256 <= cus) return 128;
+    if (!int_sums) return 256;
+    // rounds of resident workgroups; a 256 x 192 tile keeps the 256 tile's loads, unpack and LDS
+    // traffic for 3/4 of its MFMAs, so it is costed at 0.8 of a 256 x 256 round
+    const int64_t r256 = (tiles256 + cus - 1) / cus, r192 = (tiles192 + cus - 1) / cus;
+    return 4 * r192 < 5 * r256 ? 192 : 256;
 }
 
 int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups, bool int_sums) {
@@ -944,8 +960,8 @@ int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgro
     if (M <= 128 || K < 192 || K % TK) return 1;               // the few-row kernels have no split
     const int cus = device_cu_count();
     if (cus <= 0) return 1;
-    const int t = choose_tile(M, N);
-    const int64_t tiles = ((M + t - 1) / t) * ((N + t - 1) / t);
+    const int t = choose_tile(M, N, int_sums), tr = tile_rows(t);
+    const int64_t tiles = ((M + tr - 1) / tr) * ((N + t - 1) / t);
     const int64_t blocks = (K / TK + 3) / 4;                    // blocks of four K groups
     // int32 row-scale sums (no per-group fmas) are quick per K group: their partial outputs pay
     // for themselves only over a long K
@@ -959,15 +975,24 @@ int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgro
     return static_cast<int>(s);
 }
 
-int64_t tail_rows(int64_t M, int64_t N, int64_t K) {
+int64_t tail_rows(int64_t M, int64_t N, int64_t K, bool int_sums) {
     constexpr int64_t T = 256;   // only products on 256 tiles leave such a last wave
-    if (M <= T || K % TK || choose_tile(M, N) != T) return 0;
+    if (M <= T || K % TK || choose_tile(M, N, int_sums) != T) return 0;
     const int cus = device_cu_count();
     if (cus <= 0) return 0;
     const int64_t tiles_m = (M + T - 1) / T, tiles_n = (N + T - 1) / T;
     const int64_t r = (tiles_m * tiles_n) % cus;   // tiles of the last, partial wave
     if (tiles_m * tiles_n <= cus || r == 0 || r % tiles_n || 4 * r > cus) return 0;
     return M - (tiles_m - r / tiles_n) * T;
+}
+
+int64_t workspace_bytes(int64_t M, int64_t N, int64_t K, bool int_sums) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    int kgroups = 0;
+    const int64_t tail = tail_rows(M, N, K, int_sums);
+    const int64_t rows = tail > 0 ? tail : M;
+    const int s = choose_ksplit(rows, N, K, INT64_MAX, &kgroups, int_sums);
+    return s > 1 ? static_cast<int64_t>(s) * rows * N * 4 : 0;
 }
 
 int launch_gemm_wide(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {

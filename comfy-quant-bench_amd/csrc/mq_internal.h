@@ -75,25 +75,32 @@ struct GemmArgs {
     int kgroups = 0;
     void* work = nullptr;
     int64_t work_bytes = 0;   // capacity of work offered by the caller
-    // output tile of the wide kernel, 256 or 128 (0: choose_tile decides)
+    // output tile of the wide kernel: 256 (256 x 256), 192 (256 x 192) or 128 (128 x 128); 0:
+    // choose_tile decides
     int tile = 0;
 };
 
-// Output tile of the wide kernel for an M x N product: 128 when 256 x 256 tiles would occupy at
-// most half of the compute units, else 256.
-int choose_tile(int64_t M, int64_t N);
+// Output tile of the wide kernel for an M x N product (a tile code as above): 128 when 256 x 256
+// tiles would occupy at most half of the compute units; for the row-scale epilogues (int_sums)
+// 192 when its rounds of resident workgroups take less time than 256 x 256 tiles would (N = 3072
+// at M = 4096: 256 tiles in one round instead of 192); else 256.
+int choose_tile(int64_t M, int64_t N, bool int_sums);
 
 // K slices for a GEMM of this shape with a workspace of work_bytes (1 = no split): used when the
 // tiles of choose_tile leave most compute units idle (small M). int_sums: the row-scale epilogue
-// (int32 sums), which splits only over a long K; the group-scale policy never asks for less.
-int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups, bool int_sums = false);
+// (int32 sums), which splits only over a long K.
+int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups, bool int_sums);
 
 // Rows at the end of an M x N product that run as a separate GEMM (0: none): when the 256 x 256
 // tiles leave a last wave of whole tile rows that would occupy at most a quarter of the compute
 // units (M = 4352 = 4096 + 256 tokens against N = 12288: 816 tiles on 256 units), those rows run
 // on their own, on the tile and K split that choose_tile and choose_ksplit give them, so they take
 // a fraction of a 256 tile's time.
-int64_t tail_rows(int64_t M, int64_t N, int64_t K);
+int64_t tail_rows(int64_t M, int64_t N, int64_t K, bool int_sums);
+
+// Workspace bytes the split-K of an M x N x K product uses with the group-scale (int_sums false)
+// or row-scale epilogue (0: none).
+int64_t workspace_bytes(int64_t M, int64_t N, int64_t K, bool int_sums);
 
 // Power-of-two factor by which a group GEMM's MFMA result exceeds the true partial, per
 // activation layout and weight kind (see mq_gemm_wide.hip).

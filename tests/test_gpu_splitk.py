@@ -130,11 +130,12 @@ def test_tail_rows_split(gpu_device, n):
 
 @pytest.mark.parametrize("wk", ["u4", "i4x16", "i8"])
 def test_tiles_agree_bitwise(gpu_device, wk):
-    """The first 1024 rows of a 2816-row product (11 x 12 tiles of 256 at N = 3072) equal the
-    1024-row product of the same rows (4 x 12 tiles of 256, so 128 tiles): every output runs the
-    same arithmetic in the same order whatever the tile."""
-    n, k, m_small, m_big = 3072, 3072, 1024, 2816
-    print(f"[splitk] tiles agree {wk} M={m_small}/{m_big} N={n} K={k}", flush=True)
+    """The first 1024 rows of a product are the same bits whatever tile computes them: at N = 3072,
+    M = 1024 runs 128 x 128 tiles, M = 2816 256 x 192 tiles (row scale) or 256 x 256 tiles (group
+    scale), M = 4352 256 x 256 tiles; every output runs the same arithmetic in the same order."""
+    n, k, sizes = 3072, 3072, (1024, 2816, 4352)
+    m_big = sizes[-1]
+    print(f"[splitk] tiles agree {wk} M={sizes} N={n} K={k}", flush=True)
     rng = np.random.default_rng(5)
     bias = torch.randn(n, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(gpu_device)
     sa_d = _t(rng.uniform(0.001, 0.01, m_big).astype(np.float32), gpu_device)
@@ -146,7 +147,7 @@ def test_tiles_agree_bitwise(gpu_device, wk):
     else:
         qa_d = _t(rng.integers(-127, 128, (m_big, k)).astype(np.int8), gpu_device)
     ys = []
-    for m in (m_small, m_big):
+    for m in sizes:
         y = torch.empty((m, n), dtype=torch.bfloat16, device=gpu_device)
         if wk == "i8":
             qw_d = _t(np.random.default_rng(7).integers(-127, 128, (n, k)).astype(np.int8), gpu_device)
@@ -169,4 +170,5 @@ def test_tiles_agree_bitwise(gpu_device, wk):
                       m, n, k, _lib.stream_of(qa_d))
         torch.cuda.synchronize()
         ys.append(y)
-    assert torch.equal(ys[0], ys[1][:m_small])
+    for y in ys[1:]:
+        assert torch.equal(ys[0], y[:sizes[0]])

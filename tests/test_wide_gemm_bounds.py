@@ -1,5 +1,5 @@
 """Host-side model of the wide GEMM's global loads (comfy-quant-bench_amd/csrc/mq_gemm_wide.hip,
-both tiles, 256 x 256 and 128 x 128, each with 512 threads): for every workgroup, thread role and K group of a launch, the buffer resource
+every tile, 256 x 256, 256 x 192 and 128 x 128, each with 512 threads): for every workgroup, thread role and K group of a launch, the buffer resource
 (base row, byte range), the per-lane vector offset and the wave-uniform scalar offset each load
 uses, restated from the kernel's index arithmetic. Asserts that every load either fails the
 hardware range check on its vector offset (rows past M / N: offset 0x80000000; groups past the
@@ -15,12 +15,15 @@ TK = 64
 KOOB = 0x80000000
 
 
-def _loads(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=256):
-    """Yield (what, range_bytes, voff, soff, width) for every load lane of a launch on T x T tiles
+TILES = [(256, 256), (256, 192), (128, 128)]
+
+
+def _loads(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=(256, 256)):
+    """Yield (what, range_bytes, voff, soff, width) for every load lane of a launch on TM x TN tiles
     of 512 threads (vectorised over lanes with numpy where the arithmetic is per lane)."""
-    TM = TN = T
-    NH = T // 128            # 1 KB DMA blocks per wave and K group
-    TPR = 512 // T           # threads per packed weight row
+    TM, TN = T
+    NH = TM // 128           # 1 KB DMA blocks per wave and K group
+    TPR = 512 // TM          # threads per packed weight row (the B stage has TM rows)
     BPT = 32 // TPR          # packed bytes each of them loads per K group
     G = K // TK
     G4 = (G + 3) // 4 * 4
@@ -71,7 +74,7 @@ def _loads(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=256):
                 yield "S", rs if live else 0, s_voff, 2 * b4 if live else 0, 4
 
 
-def _check(M, N, K, ldwz=None, ldws=None, kgroups=None, slices=1, loads=None, T=256):
+def _check(M, N, K, ldwz=None, ldws=None, kgroups=None, slices=1, loads=None, T=(256, 256)):
     G = K // TK
     ldwz = ldwz if ldwz is not None else ((G + 1) // 2 + 1) // 2 * 2   # the wide kernel needs even strides
     ldws = ldws if ldws is not None else (G + 1) // 2 * 2
@@ -83,14 +86,14 @@ def _check(M, N, K, ldwz=None, ldws=None, kgroups=None, slices=1, loads=None, T=
                           f"width {width} (M={M} N={N} K={K})")
 
 
-@pytest.mark.parametrize("t", [256, 128])
+@pytest.mark.parametrize("t", TILES)
 @pytest.mark.parametrize("k", [192, 256, 320, 384, 448, 1472, 3072, 3136])
 @pytest.mark.parametrize("m,n", [(257, 300), (300, 256), (513, 400)])
 def test_every_load_stays_in_its_range(m, n, k, t):
     _check(m, n, k, T=t)
 
 
-@pytest.mark.parametrize("t", [256, 128])
+@pytest.mark.parametrize("t", TILES)
 @pytest.mark.parametrize("k", [320, 1472, 3072, 3200])
 def test_split_k_slices_stay_in_range(k, t):
     g = k // 64
@@ -100,16 +103,16 @@ def test_split_k_slices_stay_in_range(k, t):
     _check(256, 520, k, kgroups=per * 4, slices=slices, T=t)
 
 
-@pytest.mark.parametrize("t", [256, 128])
+@pytest.mark.parametrize("t", TILES)
 @pytest.mark.parametrize("which", ["S", "Z"])
 def test_model_catches_an_offset_past_the_range(which, t):
     # planted mistakes: the scale dword or the zero-point word of the last block loaded without
     # moving back on the tile's last weight row (the kernel's loads before that correction) must be
     # reported for K / 64 = 5 (the block 4..7 runs past G)
-    def unshifted(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=256):
+    def unshifted(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=(256, 256)):
         tid = np.arange(512)
-        brow, bpart = tid // (512 // T), tid % (512 // T)
-        rows_n = min(T, N)
+        brow, bpart = tid // (512 // T[0]), tid % (512 // T[0])
+        rows_n = min(T[1], N)
         for what, rng, voff, soff, width in _loads(M, N, K, ldwz, ldws, kgroups, slices, T):
             if what == which == "S":
                 voff = np.where((brow < rows_n) & (bpart < 2), brow * ldws * 2 + 4 * (bpart & 1), KOOB)
