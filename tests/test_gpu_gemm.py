@@ -116,7 +116,8 @@ def test_rowscale_acc_and_output(gpu_device, wbits, m, n, k):
 
 
 # ---------------------------------------------------------------- activation layouts and tile paths
-# M <= 128 runs the 128 x 128-tile kernel, larger M the 256 x 256-tile kernel: both are covered.
+# M <= 128 runs the few-row 128 x 128-tile kernel; larger M the wide kernel, on 128 x 128 tiles for
+# small products and 256 x 256 or 256 x 192 tiles for large ones: all are covered.
 
 def _x16alt(qa):
     """The group GEMM's int4 operand layout (mq_rotquant MQ_Q_X16ALT): 16 * q, odd groups negated."""
@@ -170,8 +171,8 @@ def test_int4_activation_layouts_output(gpu_device, act_mode, m):
 
 @pytest.mark.parametrize("m,n,k", [(300, 1000, 640), (257, 200, 128), (1000, 520, 3072)])
 def test_wide_tile_ragged_edges(gpu_device, m, n, k):
-    """Ragged M and N (N % 8 != 0 takes the element-wise store path) on the 256 x 256-tile kernel,
-    int8 activations with full-range signed int4 weights (nibble -8 included)."""
+    """Ragged M and N (N % 8 != 0 takes the element-wise store path) on the wide kernel's 128 x 128
+    tiles, int8 activations with full-range signed int4 weights (nibble -8 included)."""
     print(f"[gemm] ragged M={m} N={n} K={k}", flush=True)
     rng = np.random.default_rng(m * 7 + n)
     qa = rng.integers(-127, 128, (m, k)).astype(np.int8)
@@ -185,4 +186,61 @@ def test_wide_tile_ragged_edges(gpu_device, m, n, k):
                           _t(s16, gpu_device), None, None, n)
     torch.cuda.synchronize()
     err = gemm.rel_l2(gemm.epilogue_group(gemm.partials(qa, qw, 64), sa, s16), y.float().cpu().numpy())
+    assert err < TIGHT, err
+
+
+# Products large enough for the wide kernel's large tiles on 256 compute units, with ragged M and N
+# and K / 64 = 5 (a block of four groups that runs past the last): 2900 x 3000 runs 256 x 256 tiles
+# for the group-scale epilogues and 256 x 192 tiles for the row-scale ones (one round of 192 tiles
+# instead of 144 of 256); 4300 x 3000 runs 256 x 256 tiles for both.
+WIDE_RAGGED = [(2900, 3000, 320), (4300, 3000, 320)]
+
+
+@pytest.mark.parametrize("m,n,k", WIDE_RAGGED)
+def test_large_tiles_group_ragged(gpu_device, m, n, k):
+    print(f"[gemm] large-tile group M={m} N={n} K={k}", flush=True)
+    rng = np.random.default_rng(m + n + k)
+    qa = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    q = rng.integers(0, 16, (n, k)).astype(np.uint8)
+    z = rng.integers(0, 16, (n, k // 64)).astype(np.uint8)
+    qa_d, qw_d, z_d = _t(qa, gpu_device), _t(quant.pack_u4(q), gpu_device), _t(quant.pack_u4(z), gpu_device)
+    part = ops.gemm_w4_group_partials(qa_d, qw_d, z_d, n)
+    torch.cuda.synchronize()
+    part = part.cpu().numpy()
+    wq = gemm.zero_adjusted(q, z, 64).astype(np.float64)
+    a64 = qa.astype(np.float64)
+    p = np.empty((k // 64, m, n), dtype=np.int64)
+    for g in range(k // 64):   # float64 products of these integers are exact
+        p[g] = (a64[:, 64 * g:64 * g + 64] @ wq[:, 64 * g:64 * g + 64].T).astype(np.int64)
+        assert np.array_equal(part[g].astype(np.int64), p[g]), g
+    sa = rng.uniform(0.001, 0.01, m).astype(np.float32)
+    s16 = rng.uniform(1e-3, 4e-3, (n, k // 64)).astype(np.float16)
+    bias = _bf16_round(rng.standard_normal(n) * 0.5)
+    y = ops.gemm_w4_group(qa_d, _t(sa, gpu_device), qw_d, _t(s16, gpu_device), z_d,
+                          torch.from_numpy(bias).to(gpu_device, torch.bfloat16), n)
+    torch.cuda.synchronize()
+    err = gemm.rel_l2(gemm.epilogue_group(p, sa, s16.astype(np.float64), bias), y.float().cpu().numpy())
+    assert err < TIGHT, err
+
+
+@pytest.mark.parametrize("wbits", [4, 8])
+@pytest.mark.parametrize("m,n,k", WIDE_RAGGED)
+def test_large_tiles_rowscale_ragged(gpu_device, wbits, m, n, k):
+    print(f"[gemm] large-tile rowscale w{wbits} M={m} N={n} K={k}", flush=True)
+    rng = np.random.default_rng(wbits + m + n)
+    lim = 7 if wbits == 4 else 127
+    qa = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    qw = rng.integers(-lim - (wbits == 4), lim + 1, (n, k)).astype(np.int8)   # int4 nibble -8 included
+    wpk = quant.pack_i4(qw) if wbits == 4 else qw
+    acc = ops.gemm_rowscale_acc(_t(qa, gpu_device), _t(wpk, gpu_device), n, wbits)
+    torch.cuda.synchronize()
+    p0 = (qa.astype(np.float64) @ qw.astype(np.float64).T).astype(np.int64)   # exact in float64
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), p0)
+    sa = rng.uniform(0.01, 0.02, m).astype(np.float32)
+    sw = rng.uniform(0.001, 0.002, n).astype(np.float32)
+    bias = _bf16_round(rng.standard_normal(n))
+    y = ops.gemm_rowscale(_t(qa, gpu_device), _t(sa, gpu_device), _t(wpk, gpu_device), _t(sw, gpu_device),
+                          torch.from_numpy(bias).to(gpu_device, torch.bfloat16), n, wbits)
+    torch.cuda.synchronize()
+    err = gemm.rel_l2(gemm.epilogue_row(p0, sa, sw, bias), y.float().cpu().numpy())
     assert err < TIGHT, err

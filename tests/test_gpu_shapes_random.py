@@ -1,5 +1,6 @@
-"""Seeded random shapes against the oracle. GEMM: every entry point (few-row, 128-tile, 256-tile and
-split-K kernels are all reached), exact int32 partials / accumulators where the entry point exposes
+"""Seeded random shapes against the oracle. GEMM: every entry point (the few-row kernels, the wide
+kernel on 128 x 128 tiles and split-K are reached; the wide kernel's large tiles are covered by
+tests/test_gpu_gemm.py and tests/test_gpu_configs.py), exact int32 partials / accumulators where the entry point exposes
 them, and the bf16 outputs (with and without the split-K workspace) against a float64 product of the
 same codes. Rotate + quantize, plain and with the SwiGLU prologue: codes and scales bit-exact. Sizes
 are drawn so the oracle finishes in seconds."""
