@@ -284,7 +284,7 @@ int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
             const bool int_sums = epi == Epi::RowScale;
             // a last, nearly empty wave of whole tile rows: those rows run as their own product
             // (smaller tiles, split along K where the workspace allows), the rest without them
-            const int64_t tail = tail_rows(a.M, a.N, a.K, int_sums);
+            const int64_t tail = tail_rows(a.M, a.N, a.K);
             if (tail > 0) {
                 GemmArgs t = w;
                 t.M = tail;

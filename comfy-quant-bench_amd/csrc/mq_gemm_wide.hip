@@ -2,7 +2,7 @@
 // per workgroup of 8 wavefronts, int8 MFMA (v_mfma_i32_16x16x64_i8: one instruction covers one
 // 64-wide K group of a 16 x 16 output tile), one K group per k-step. The 128 tile serves products
 // whose 256 tiles would leave most compute units idle (small M); the 256 x 192 tile fills the last
-// wave of row-scale products such as N = 3072 (16 tile columns instead of 12).
+// wave of products such as N = 3072 (16 tile columns instead of 12).
 //
 // Layout. Waves form a 4 (M) x 2 (N) grid; each owns a TM/4 x TN/2 output tile made of NI x NJ MFMA
 // 16x16 tiles (4 x 8, 4 x 6 or 2 x 4). In the 16x16 output layout lane l holds column l % 16 and rows 4 * (l / 16) + r,
@@ -93,6 +93,20 @@ struct Cfg {
 };
 static_assert(Cfg<256, 256>::SMEM_BYTES <= 160 * 1024 && Cfg<256, 192>::SMEM_BYTES <= 160 * 1024 &&
                   Cfg<128, 128>::SMEM_BYTES <= 160 * 1024, "LDS budget");
+
+// LDS operations a wave issues in a group after its last LDS store (step ts): the B fragment reads
+// (steps with i == 0), the next group's A fragment reads and, with group scales, the scale reads
+// (steps 3 and 19 for NJ >= 6, step 3 for NJ == 4), in the step schedule of the kernel's group loop.
+constexpr int lds_ops_after(int ni, int nj, int ts, bool group_scale) {
+    int n = 0;
+    for (int t = ts + 1; t < ni * nj; ++t) {
+        const int j = t / ni, i = t % ni;
+        if (i == 0) ++n;
+        if (i == (ni == 4 ? 2 : 1) && j < ni) ++n;
+        if (group_scale && (t == 3 || (nj >= 6 && t == 19))) ++n;
+    }
+    return n;
+}
 
 // Tile codes of GemmArgs::tile / choose_tile: the output tile's N extent (256 and 192: 256 rows).
 constexpr int tile_rows(int code) { return code == 128 ? 128 : 256; }
@@ -636,14 +650,19 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        // A(g + 2) and this group's B stores become visible to every wave. 256 x 256: LDS operations
-        // of a wave complete in issue order, and the MFMAs of steps 24-27 waited for a fragment read
-        // issued after the stores of steps 8-10, so those stores are complete here without a wait
-        // and the next group's fragment reads stay in flight across the barrier. The other tiles: no
-        // MFMA of the group reads a fragment issued after the stores, so the wave waits for its LDS
-        // operations here. Group g's own stages were last read by MFMAs that have issued.
+        // A(g + 2) and this group's B stores become visible to every wave. LDS operations of a wave
+        // complete in issue order. 256 x 256: the MFMAs of steps 24-27 waited for a fragment read
+        // issued after the stores of steps 8-10, so those stores are complete here without a wait.
+        // The other tiles: no MFMA of the group reads a fragment issued after the stores, so the
+        // wave waits until at most the LDS operations issued after its last store are outstanding
+        // (the next group's fragment and scale reads, which stay in flight across the barrier).
+        // Group g's own stages were last read by MFMAs that have issued.
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kVmAfter[U]) : "memory");
-        if constexpr (NJ != 8) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if constexpr (NJ != 8) {
+            constexpr int kLdsAfter = lds_ops_after(NI, NJ, kTS, EPI == Epi::GroupScale);
+            static_assert(kLdsAfter < 16, "lgkmcnt holds 0-15");
+            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(kLdsAfter) : "memory");
+        }
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
@@ -908,7 +927,7 @@ int launch_tile(const GemmArgs& a, hipStream_t stream) {
 
 template <WKind WK, Epi EPI, int AM>
 int launch_one(const GemmArgs& a, hipStream_t stream) {
-    const int t = a.tile ? a.tile : choose_tile(a.M, a.N, EPI == Epi::RowScale || EPI == Epi::RowAcc);
+    const int t = a.tile ? a.tile : choose_tile(a.M, a.N);
     if (t == 128) return launch_tile<128, 128, WK, EPI, AM>(a, stream);
     if (t == 192) return launch_tile<256, 192, WK, EPI, AM>(a, stream);
     if (t == 256) return launch_tile<256, 256, WK, EPI, AM>(a, stream);
@@ -943,16 +962,21 @@ int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
 
 }  // namespace
 
-int choose_tile(int64_t M, int64_t N, bool int_sums) {
+int choose_tile(int64_t M, int64_t N) {
     const int cus = device_cu_count();
     if (cus <= 0) return 256;
     const int64_t tm = (M + 255) / 256, tiles256 = tm * ((N + 255) / 256), tiles192 = tm * ((N + 191) / 192);
     if (2 * tiles256 <= cus) return 128;
-    if (!int_sums) return 256;
-    // rounds of resident workgroups; a 256 x 192 tile keeps the 256 tile's loads, unpack and LDS
-    // traffic for 3/4 of its MFMAs, so it is costed at 0.8 of a 256 x 256 round
-    const int64_t r256 = (tiles256 + cus - 1) / cus, r192 = (tiles192 + cus - 1) / cus;
-    return 4 * r192 < 5 * r256 ? 192 : 256;
+    // Rounds of resident workgroups, in tenths of a 256 x 256 round. A 256 x 192 round costs 0.9 (3/4
+    // of the MFMAs but the same loads, unpack and LDS traffic per K group: measured 0.87-0.97 of a
+    // 256 x 256 round). A last 256 x 256 round of
+    // whole tile rows on at most a quarter of the compute units runs as its own product on smaller
+    // tiles (tail_rows), costed 0.3.
+    const int64_t tn = (N + 255) / 256, full = tiles256 / cus, part = tiles256 % cus;
+    const bool tail = full > 0 && part > 0 && part % tn == 0 && 4 * part <= cus;
+    const int64_t c256 = 10 * full + (part == 0 ? 0 : tail ? 3 : 10);
+    const int64_t c192 = 9 * ((tiles192 + cus - 1) / cus);
+    return c192 < c256 ? 192 : 256;
 }
 
 int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgroups, bool int_sums) {
@@ -960,7 +984,7 @@ int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgro
     if (M <= 128 || K < 192 || K % TK) return 1;               // the few-row kernels have no split
     const int cus = device_cu_count();
     if (cus <= 0) return 1;
-    const int t = choose_tile(M, N, int_sums), tr = tile_rows(t);
+    const int t = choose_tile(M, N), tr = tile_rows(t);
     const int64_t tiles = ((M + tr - 1) / tr) * ((N + t - 1) / t);
     const int64_t blocks = (K / TK + 3) / 4;                    // blocks of four K groups
     // int32 row-scale sums (no per-group fmas) are quick per K group: their partial outputs pay
@@ -975,9 +999,9 @@ int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgro
     return static_cast<int>(s);
 }
 
-int64_t tail_rows(int64_t M, int64_t N, int64_t K, bool int_sums) {
+int64_t tail_rows(int64_t M, int64_t N, int64_t K) {
     constexpr int64_t T = 256;   // only products on 256 tiles leave such a last wave
-    if (M <= T || K % TK || choose_tile(M, N, int_sums) != T) return 0;
+    if (M <= T || K % TK || choose_tile(M, N) != T) return 0;
     const int cus = device_cu_count();
     if (cus <= 0) return 0;
     const int64_t tiles_m = (M + T - 1) / T, tiles_n = (N + T - 1) / T;
@@ -989,7 +1013,7 @@ int64_t tail_rows(int64_t M, int64_t N, int64_t K, bool int_sums) {
 int64_t workspace_bytes(int64_t M, int64_t N, int64_t K, bool int_sums) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     int kgroups = 0;
-    const int64_t tail = tail_rows(M, N, K, int_sums);
+    const int64_t tail = tail_rows(M, N, K);
     const int64_t rows = tail > 0 ? tail : M;
     const int s = choose_ksplit(rows, N, K, INT64_MAX, &kgroups, int_sums);
     return s > 1 ? static_cast<int64_t>(s) * rows * N * 4 : 0;

@@ -81,10 +81,10 @@ struct GemmArgs {
 };
 
 // Output tile of the wide kernel for an M x N product (a tile code as above): 128 when 256 x 256
-// tiles would occupy at most half of the compute units; for the row-scale epilogues (int_sums)
-// 192 when its rounds of resident workgroups take less time than 256 x 256 tiles would (N = 3072
-// at M = 4096: 256 tiles in one round instead of 192); else 256.
-int choose_tile(int64_t M, int64_t N, bool int_sums);
+// tiles would occupy at most half of the compute units; else 192 when its rounds of resident
+// workgroups take less time than 256 x 256 tiles (with their trailing rows, tail_rows) would
+// (N = 3072 at M = 4096: 256 tiles in one round instead of 192); else 256.
+int choose_tile(int64_t M, int64_t N);
 
 // K slices for a GEMM of this shape with a workspace of work_bytes (1 = no split): used when the
 // tiles of choose_tile leave most compute units idle (small M). int_sums: the row-scale epilogue
@@ -96,7 +96,7 @@ int choose_ksplit(int64_t M, int64_t N, int64_t K, int64_t work_bytes, int* kgro
 // units (M = 4352 = 4096 + 256 tokens against N = 12288: 816 tiles on 256 units), those rows run
 // on their own, on the tile and K split that choose_tile and choose_ksplit give them, so they take
 // a fraction of a 256 tile's time.
-int64_t tail_rows(int64_t M, int64_t N, int64_t K, bool int_sums);
+int64_t tail_rows(int64_t M, int64_t N, int64_t K);
 
 // Workspace bytes the split-K of an M x N x K product uses with the group-scale (int_sums false)
 // or row-scale epilogue (0: none).

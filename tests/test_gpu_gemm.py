@@ -190,9 +190,8 @@ def test_wide_tile_ragged_edges(gpu_device, m, n, k):
 
 
 # Products large enough for the wide kernel's large tiles on 256 compute units, with ragged M and N
-# and K / 64 = 5 (a block of four groups that runs past the last): 2900 x 3000 runs 256 x 256 tiles
-# for the group-scale epilogues and 256 x 192 tiles for the row-scale ones (one round of 192 tiles
-# instead of 144 of 256); 4300 x 3000 runs 256 x 256 tiles for both.
+# and K / 64 = 5 (a block of four groups that runs past the last): 2900 x 3000 runs 256 x 192 tiles
+# (one round of 192 tiles instead of 144 of 256), 4300 x 3000 256 x 256 tiles.
 WIDE_RAGGED = [(2900, 3000, 320), (4300, 3000, 320)]
 
 

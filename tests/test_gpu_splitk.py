@@ -131,8 +131,8 @@ def test_tail_rows_split(gpu_device, n):
 @pytest.mark.parametrize("wk", ["u4", "i4x16", "i8"])
 def test_tiles_agree_bitwise(gpu_device, wk):
     """The first 1024 rows of a product are the same bits whatever tile computes them: at N = 3072,
-    M = 1024 runs 128 x 128 tiles, M = 2816 256 x 192 tiles (row scale) or 256 x 256 tiles (group
-    scale), M = 4352 256 x 256 tiles; every output runs the same arithmetic in the same order."""
+    M = 1024 runs 128 x 128 tiles, M = 2816 256 x 192 tiles, M = 4352 256 x 256 tiles; every output
+    runs the same arithmetic in the same order."""
     n, k, sizes = 3072, 3072, (1024, 2816, 4352)
     m_big = sizes[-1]
     print(f"[splitk] tiles agree {wk} M={sizes} N={n} K={k}", flush=True)
