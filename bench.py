@@ -554,7 +554,7 @@ def main() -> int:
         "data": "synthetic: seeded N(0,1) bf16 activations with 1% x20 outlier channels, N(0,0.02) weights",
         "config": {"workload": "w4a8_linear (rotate H256 + int8 per-token quant + uint4-asym g64 GEMM + epilogue)",
                    "M": m, "K": k, "N": n, "hadamard_block": 256, "group": 64, "out": "bf16"},
-        "roofline": {"bound": "mfma", "kernel": "gemm_wide_kernel<U4Asym,GroupScale,0>",
+        "roofline": {"bound": "mfma", "kernel": "gemm_wide_kernel<256,256,U4Asym,GroupScale,0>",
                      "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
                      "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": gemm_traffic,
                      "ops_per_launch": ops, "avg_launch_ms": round(ms_gemm, 5)},
