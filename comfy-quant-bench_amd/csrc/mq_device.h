@@ -98,4 +98,24 @@ __device__ __forceinline__ float wave_max(float v) {
     return __builtin_fmaxf(__builtin_fmaxf(r0, r1), __builtin_fmaxf(r2, r3));
 }
 
+// wave_max for values that are >= 0 and not NaN (+inf allowed): their bit patterns order as
+// unsigned integers, so every step is an integer maximum, which takes its DPP operand directly
+// (one instruction per step) and needs none of the float maximum's NaN handling; the four row
+// maxima are combined on the scalar unit.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov_u(uint32_t src) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(src), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    uint32_t b = __float_as_uint(v);
+    b = __builtin_elementwise_max(b, dpp_mov_u<kQuadXor1>(b));
+    b = __builtin_elementwise_max(b, dpp_mov_u<kQuadXor2>(b));
+    b = __builtin_elementwise_max(b, dpp_mov_u<kRowRor4>(b));
+    b = __builtin_elementwise_max(b, dpp_mov_u<kRowRor8>(b));
+    const uint32_t r0 = __builtin_amdgcn_readlane(b, 0), r1 = __builtin_amdgcn_readlane(b, 16);
+    const uint32_t r2 = __builtin_amdgcn_readlane(b, 32), r3 = __builtin_amdgcn_readlane(b, 48);
+    return __uint_as_float(__builtin_elementwise_max(__builtin_elementwise_max(r0, r1),
+                                                     __builtin_elementwise_max(r2, r3)));
+}
+
 }  // namespace mq

@@ -28,11 +28,15 @@
 // L3 gives every lane 16 consecutive codes, written with one 16-byte (int8) or 8-byte (packed
 // int4) store.
 //
-// Quantization without a per-element division: with r = 1/s (IEEE), m = fma(v, r, 1.5*2^23)
-// rounds v*r to an integer n. |v*r - v/s| <= 2^-17 and |fl(v/s) - v/s| <= 2^-17 for |v/s| < 128,
-// so rint(fl(v/s)) == n unless v*r lies within 2^-16 of a half-integer; those elements (flagged
-// by |fma(v, r, -n)| > 0.5 - 2^-15) recompute rint(v / s) with the IEEE division. The clamp to
-// [-L, L] never binds on the fast path: |v| <= absmax, so |v*r| <= L (1 + 2^-22).
+// Quantization without a per-element division: with r within 2^-23 relative of 1/s,
+// m = fma(v, r, 1.5*2^23) rounds v*r to an integer n. |v*r - v/s| < 2^-16 and
+// |fl(v/s) - v/s| <= 2^-18 for |v/s| < 128, so rint(fl(v/s)) == n unless v*r lies within
+// 2^-16 + 2^-18 of a half-integer; those elements (flagged by |fma(v, r, -n)| > 0.5 - 2^-15, the
+// fma adding at most 2^-25) recompute rint(v / s) with the IEEE division. The clamp to [-L, L]
+// never binds on the fast path: |v| <= absmax, so |v*r| <= L (1 + 2^-21).
+//
+// Per row, s = max(absmax / L, 1e-10) is the correctly rounded quotient, formed without a division
+// (div_limit), and r comes from v_rcp_f32 and one Newton step (recip_row).
 #pragma once
 
 #include <algorithm>
@@ -209,6 +213,31 @@ __device__ __forceinline__ void rotate_chunk_lds(float (&v)[16], const LdsTransp
     }
 }
 
+// am / L rounded to nearest for every am in [0, +inf] (L = 127 or 7) without a division: with
+// c = RN(1/L), q0 = RN(am c) is within an ulp of am / L, the residual am - q0 L is exact (one
+// fma), and RN(q0 + residual c) is the correctly rounded quotient (Markstein's correction step).
+// Checked bit for bit against the IEEE quotient for every non-negative float on the CPU
+// (tests/test_rotquant_scale.py). +inf, whose residual is NaN, is passed through.
+template <int L>
+__device__ __forceinline__ float div_limit(float am) {
+    constexpr float c = 1.0f / static_cast<float>(L);
+    const float q0 = am * c;
+    const float e = __builtin_fmaf(-q0, static_cast<float>(L), am);
+    const float q1 = __builtin_fmaf(e, c, q0);
+    return am == __builtin_inff() ? am : q1;
+}
+
+// 1/s for a row scale s in [1e-10, +inf]: v_rcp_f32 (within an ulp or so) refined by one Newton
+// step, e = 1 - s r0 and r = r0 + e r0, which leaves a relative error within 2^-23 for any start
+// within 8 ulps (the square of the first error plus the final rounding; checked on the CPU by
+// tests/test_rotquant_scale.py); 1/inf = 0 as the IEEE quotient.
+__device__ __forceinline__ float recip_row(float s) {
+    const float r0 = __builtin_amdgcn_rcpf(s);
+    const float e = __builtin_fmaf(-s, r0, 1.0f);
+    const float r = __builtin_fmaf(e, r0, r0);
+    return s == __builtin_inff() ? 0.0f : r;
+}
+
 // Column bit 6 (the parity of the 64-column group) of register r of lane L after rotate_chunk.
 template <int BLK>
 __device__ __forceinline__ int col_bit6(int lane, int r) {
@@ -357,7 +386,7 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
             for (int j = 0; j < 16; ++j) amc = __builtin_fmaxf(amc, __builtin_fabsf(v[c][j]));
             am = __builtin_fmaxf(am, live && in[c] ? amc : 0.0f);
         }
-        am = wave_max(am);
+        am = wave_max_nonneg(am);
         if constexpr (W > 1) {
             if (lane == 0) red[parity * kWaves + wave] = am;
             __syncthreads();
@@ -367,8 +396,8 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
             if (!live) continue;
         }
 
-        const float s = __builtin_fmaxf(am / static_cast<float>(LIMIT), 1e-10f);
-        const float r = 1.0f / s;
+        const float s = __builtin_fmaxf(div_limit<LIMIT>(am), 1e-10f);
+        const float r = recip_row(s);
         if (lane == 0 && wr == 0) scale[row] = s;
 
         uint8_t* qr = q + row * ldq;
