@@ -44,6 +44,9 @@ def _as_2d(x: torch.Tensor, k: int) -> torch.Tensor:
         raise ValueError("kitchen_amd ops run on the GPU: x must be a device tensor")
     if x.dtype not in FLOAT_TYPES:
         raise ValueError(f"x must be bfloat16, float16 or float32, got {x.dtype}")
+    # a contiguous 2-D x is what the reshape would return: used as it is (no new view per call)
+    if x.dim() == 2 and x.shape[1] == k and x.stride(1) == 1 and x.stride(0) == k:
+        return x
     return x.reshape(-1, k).contiguous()
 
 
@@ -66,7 +69,7 @@ def _out_dtype(out_dtype, x: torch.Tensor):
 
 
 def _finish(y: torch.Tensor, x: torch.Tensor, n: int) -> torch.Tensor:
-    return y.reshape(*x.shape[:-1], n)
+    return y if x.dim() == 2 else y.reshape(*x.shape[:-1], n)
 
 
 # --------------------------------------------------------------------------- activation quantizers
@@ -471,8 +474,10 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
         raise ValueError(f"s_rel must be [{n}, {k // group_size}], got {list(s_rel.shape)}")
     if correction is not None and correction.shape != (n, (k // group_size + 1) // 2):
         raise ValueError(f"correction (zero-points) must be [{n}, {(k // group_size + 1) // 2}]")
-    qw = qdata.view(torch.uint8)
-    zz = correction.view(torch.uint8) if correction is not None else None
+    qw = qdata if qdata.dtype == torch.uint8 else qdata.view(torch.uint8)
+    zz = correction
+    if zz is not None and zz.dtype != torch.uint8:
+        zz = zz.view(torch.uint8)
     y = _linear_w4_group(x, False, convrot_groupsize, 8, qw, s_rel.contiguous(), zz, bias, n, k,
                          _out_dtype(out_dtype, x))
     return _finish(y, x, n)
