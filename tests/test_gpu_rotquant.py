@@ -97,6 +97,24 @@ def test_zero_rows_and_exact_ties(gpu_device):
     _check(xb, 16, 8, False, gpu_device, "ties-rot")
 
 
+@pytest.mark.parametrize("hblock", [0, 256])
+def test_extreme_row_magnitudes(gpu_device, hblock):
+    # Rows scaled across the float range pin the row scale (formed without a division) and the
+    # reciprocal behind the codes at every exponent: subnormal-scale rows (the 1e-10 clamp), tiny,
+    # ordinary and huge rows. Without rotation the largest row reaches 1e38; with it, rows stay
+    # below 1e36 so no butterfly sum overflows.
+    rng = np.random.default_rng(21)
+    exps = [-39, -36, -30, -20, -12, -10, -8, -3, 0, 3, 10, 20, 30, 35, 38]
+    m, k = len(exps), 1024
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    for r, e in enumerate(exps):
+        top = 1.0e38 if hblock == 0 else 1.0e35
+        x[r] *= np.float32(min(10.0 ** e, top) / 4.0)
+    xb = synth.f32_to_bf16_bits(x)
+    for bits, packed in ((8, False), (4, False)):
+        _check(xb, hblock, bits, packed, gpu_device, "magnitudes")
+
+
 def test_near_tie_window_exercised(gpu_device):
     # Rotated fp32 values have full mantissas, so some quotients x*(1/s) land within 2^-16 of a
     # half-integer, where the kernel recomputes x / s exactly. Count them with the oracle's
