@@ -224,6 +224,15 @@ def kernels_child(args) -> int:
     qa, sa = ck.quantize_int8_rowwise_convrot(x, 256)
     for _ in range(3):
         ck.gemm_w4_group(qa, sa, qd.view(torch.uint8), s16, zp.view(torch.uint8), bias, n)
+    if args.with_rowscale:
+        # the W8A8 row-scale GEMM of the same shape (random int8 weights, per-row scales), for
+        # counter runs that compare the two epilogues; the traffic runs leave it out
+        gen = torch.Generator(device=x.device).manual_seed(6)
+        q8 = torch.randint(-127, 128, (n, k), generator=gen, device=x.device, dtype=torch.int8)
+        ws = torch.rand(n, generator=gen, device=x.device) * 1e-3
+        for _ in range(3):
+            ck.gemm_rowscale(qa, sa, q8, ws, bias, n, 8)
+        del q8
     x3 = synth.to_bf16_tensor(synth.activations(RQ_M, k, seed=3), x.device)
     for _ in range(3):
         ck.quantize_int8_rowwise_convrot(x3, 256)
@@ -473,6 +482,8 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true",
                     help="time every configuration's linear shapes instead (one JSON object, not the bench line)")
     ap.add_argument("--kernels-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--with-rowscale", action="store_true",
+                    help="with --kernels-child: also launch the W8A8 row-scale GEMM (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
