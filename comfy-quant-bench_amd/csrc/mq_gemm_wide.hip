@@ -567,16 +567,20 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     if constexpr (NJ >= 6) read_s(0, 1, 1);
 
     // VMEM instructions per group and thread, in issue order: the DMA of A(g + 3) (and int8 B) at
-    // step 0, the packed B load of group g + 4 at step kTL and, in groups with g % 4 == 1, the
+    // step kTD, the packed B load of group g + 4 at step kTL and, in groups with g % 4 == 1, the
     // zero-points and scales of the block g + 3 .. g + 6 right after it. Waits count the VMEM
-    // operations issued after the one awaited.
+    // operations issued after the one awaited. With int8 weights the group's DMA is all its VMEM
+    // work; issued eight MFMAs into the group rather than at its first, it takes 1.5-2 % off the
+    // 256 x 256 row-scale product (measured, same bits).
     constexpr int kDmaOps = NH * (kPacked ? 1 : 2);
+    constexpr int kTD = kPacked ? 0 : 8 % NTL;
     // steps of the B unpack (kTB: wait for the registers, store; kTB + 1: second half for T = 256),
     // of the scale store (kTS) and of the next packed B load (kTL); kTB > 0 follows the DMA of step 0
+    // (packed weights)
     constexpr int kTB = NTL >= 24 ? 8 : 4, kTS = NTL >= 24 ? 10 : 5, kTL = NTL >= 24 ? 12 : 6;
     constexpr int kB = kPacked ? 1 : 0;
     constexpr int kZS = (WK == WKind::U4Asym) + (EPI == Epi::GroupScale);
-    // Before the barrier that ends group g, A(g + 2) (issued at step 0 of group g - 1) must be
+    // Before the barrier that ends group g, A(g + 2) (issued at step kTD of group g - 1) must be
     // complete; issued after it: B(g + 3), [zs if (g - 1) % 4 == 1], A(g + 3), B(g + 4),
     // [zs if g % 4 == 1]. (The partials variant also stores to global memory; it waits for all.)
     constexpr int kVmAfter[4] = {
@@ -615,7 +619,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
                 const int gp = t < LAG ? g - 1 : g;
                 if (gp >= 0 && gp < G) write_partials(tp, gp, t < LAG ? PAR == 0 : PAR == 1);
             }
-            if (t == 0) dma_group(g + 3, ST3);
+            if (t == kTD) dma_group(g + 3, ST3);
             // B fragments three columns ahead (the next group's first columns from stage ST1,
             // complete since the barrier that ended group g - 1)
             if (i == 0) {
