@@ -228,7 +228,7 @@ def kernels_child(args) -> int:
         # the W8A8 row-scale GEMM of the same shape (random int8 weights, per-row scales), for
         # counter runs that compare the two epilogues; the traffic runs leave it out
         gen = torch.Generator(device=x.device).manual_seed(6)
-        q8 = torch.randint(-127, 128, (n, k), generator=gen, device=x.device, dtype=torch.int8)
+        q8 = ck.tile_int8_weight(torch.randint(-127, 128, (n, k), generator=gen, device=x.device, dtype=torch.int8))
         ws = torch.rand(n, generator=gen, device=x.device) * 1e-3
         for _ in range(3):
             ck.gemm_rowscale(qa, sa, q8, ws, bias, n, 8)

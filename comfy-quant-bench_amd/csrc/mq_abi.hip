@@ -78,6 +78,19 @@ int check_gemm_out(const char* what, const void* bias, int bias_dtype, const voi
     return MQ_OK;
 }
 
+// Weights in 16-row tiles (MQ_W8_TILE16): int8 only, K >= 192 (the wide kernel's minimum), the
+// whole tiled array under 2 GiB (32-bit buffer offsets); the row stride becomes K.
+int check_tile16(const char* what, bool tile16, int wbits, int64_t N, int64_t K, int64_t* ldw) {
+    if (!tile16) return MQ_OK;
+    MQ_REQUIRE(wbits == 8, "%s: the 16-row tile layout is for int8 weights (wbits 8)", what);
+    MQ_REQUIRE(K >= 192 && K % 64 == 0, "%s: 16-row tile weights need K %% 64 == 0 and K >= 192 (got %lld)", what,
+               (long long)K);
+    MQ_REQUIRE(N >= 0 && (N + 15) / 16 * 16 * K < (int64_t(1) << 31), "%s: 16-row tile weights must be under 2 GiB",
+               what);
+    *ldw = K;
+    return MQ_OK;
+}
+
 int check_gemm_common(const int8_t* qa, int64_t lda, const void* qw, int64_t ldw, int64_t M, int64_t N,
                       int64_t K, int64_t wbytes_per_row) {
     MQ_REQUIRE(M >= 0 && N >= 0 && K > 0, "gemm: bad shape M=%lld N=%lld K=%lld", (long long)M,
@@ -233,6 +246,19 @@ int mq_quantize_weight(const void* w, int dtype, int64_t N, int64_t K, int64_t l
                                   static_cast<hipStream_t>(stream));
 }
 
+int mq_tile_weight_i8(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t* out, void* stream) {
+    clear_error();
+    MQ_REQUIRE(N >= 0 && K >= 192 && K % 64 == 0, "tile_weight_i8: bad shape N=%lld K=%lld (K %% 64 == 0, K >= 192)",
+               (long long)N, (long long)K);
+    MQ_REQUIRE((N + 15) / 16 * 16 * K < (int64_t(1) << 31), "tile_weight_i8: the tiled weight must be under 2 GiB");
+    if (N == 0) return MQ_OK;
+    MQ_REQUIRE(w && out, "tile_weight_i8: null pointer");
+    MQ_REQUIRE(ldw >= K && ldw % 16 == 0 && aligned(w, 16) && aligned(out, 16),
+               "tile_weight_i8: needs ldw >= K, ldw %% 16 == 0 and 16-byte aligned w and out");
+    return launch_tile_weight_i8(reinterpret_cast<const uint8_t*>(w), ldw, N, K, reinterpret_cast<uint8_t*>(out),
+                                 static_cast<hipStream_t>(stream));
+}
+
 int mq_gemm_w4_group_ws(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
                         const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
                         const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy, int64_t M, int64_t N,
@@ -287,8 +313,12 @@ int mq_gemm_rowscale_ws(const int8_t* qa, int64_t lda, const float* sa, const vo
                         const float* ws, const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy,
                         int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
     clear_error();
+    const bool tile16 = (wbits & MQ_W8_TILE16) != 0;
+    wbits &= ~MQ_W8_TILE16;
     MQ_REQUIRE(wbits == 4 || wbits == 8, "gemm_rowscale: wbits must be 4 or 8 (got %d)", wbits);
-    int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, wbits == 4 ? K / 2 : K);
+    int rc = check_tile16("gemm_rowscale", tile16, wbits, N, K, &ldw);
+    if (rc) return rc;
+    rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, wbits == 4 ? K / 2 : K);
     if (rc) return rc == kEmpty ? MQ_OK : rc;
     MQ_REQUIRE(sa && ws, "gemm_rowscale: null pointer");
     rc = check_gemm_out("gemm_rowscale", bias, bias_dtype, y, y_dtype, ldy, N);
@@ -299,6 +329,7 @@ int mq_gemm_rowscale_ws(const int8_t* qa, int64_t lda, const float* sa, const vo
     a.qa = qa; a.lda = lda; a.sa = sa; a.qw = static_cast<const uint8_t*>(qw); a.ldw = ldw; a.ws32 = ws;
     a.bias = bias; a.bias_dtype = bias_dtype; a.y = y; a.y_dtype = y_dtype; a.ldy = ldy; a.M = M; a.N = N; a.K = K;
     a.work = workspace; a.work_bytes = workspace ? workspace_bytes : 0;
+    a.wtile = tile16;
     return launch_gemm(a, wbits == 4 ? WKind::I4Sym : WKind::I8, Epi::RowScale, static_cast<hipStream_t>(stream));
 }
 
@@ -317,13 +348,18 @@ int64_t mq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
 int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t ldw, int wbits, int32_t* acc,
                          int64_t M, int64_t N, int64_t K, void* stream) {
     clear_error();
+    const bool tile16 = (wbits & MQ_W8_TILE16) != 0;
+    wbits &= ~MQ_W8_TILE16;
     MQ_REQUIRE(wbits == 4 || wbits == 8, "gemm_rowscale_acc: wbits must be 4 or 8 (got %d)", wbits);
-    int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, wbits == 4 ? K / 2 : K);
+    int rc = check_tile16("gemm_rowscale_acc", tile16, wbits, N, K, &ldw);
+    if (rc) return rc;
+    rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, wbits == 4 ? K / 2 : K);
     if (rc) return rc == kEmpty ? MQ_OK : rc;
     MQ_REQUIRE(acc, "gemm_rowscale_acc: null pointer");
     GemmArgs a{};
     a.qa = qa; a.lda = lda; a.qw = static_cast<const uint8_t*>(qw); a.ldw = ldw; a.part = acc;
     a.M = M; a.N = N; a.K = K;
+    a.wtile = tile16;
     return launch_gemm(a, wbits == 4 ? WKind::I4Sym : WKind::I8, Epi::RowAcc, static_cast<hipStream_t>(stream));
 }
 

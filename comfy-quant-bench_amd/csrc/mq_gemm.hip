@@ -276,7 +276,8 @@ int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
         (wk != WKind::U4Asym || (a.ldwz % 2 == 0 && reinterpret_cast<uintptr_t>(a.wz) % 2 == 0)) &&
         (epi != Epi::GroupScale || (a.ldws % 2 == 0 && reinterpret_cast<uintptr_t>(a.ws16) % 4 == 0));
     // (K >= 192: the wide kernel's last-row load correction needs at least three K groups)
-    if (a.M > 128 && a.K >= 192 && fits32 && zs_aligned && a.act_mode != 1) {
+    // Weights in 16-row tiles are read by the wide kernel at every M above the GEMV's few rows.
+    if ((a.M > 128 || a.wtile) && a.K >= 192 && fits32 && zs_aligned && a.act_mode != 1) {
         GemmArgs w = a;
         w.ksplit = 1;
         w.tile = 0;
@@ -301,6 +302,10 @@ int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
             if (a.work) w.ksplit = choose_ksplit(a.M, a.N, a.K, a.work_bytes, &w.kgroups, int_sums);
         }
         return launch_gemm_wide(w, wk, epi, stream);
+    }
+    if (a.wtile) {
+        set_error("gemm: int8 weights in 16-row tiles need K >= 192 and operands under 2 GiB");
+        return -2;
     }
     switch (wk) {
         case WKind::U4Asym:

@@ -301,7 +301,11 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         }
     }
     const auto ra_rs = rsrc(a.qa + m0 * a.lda, (rows_m - 1) * a.lda + a.K);
-    const auto rb_rs = rsrc(a.qw + n0 * a.ldw, (rows_n - 1) * a.ldw + kbytes_w);
+    // int8 weights in 16-row tiles: the K group of 16 rows is one 1 KB block, so every DMA
+    // instruction reads whole 128-byte lines (rows of ldw bytes give it two halves of 16 lines)
+    const bool wt = !kPacked && a.wtile;
+    const auto rb_rs = wt ? rsrc(a.qw + (n0 >> 4) * G * 1024, static_cast<int64_t>((rows_n + 15) >> 4) * G * 1024)
+                          : rsrc(a.qw + n0 * a.ldw, (rows_n - 1) * a.ldw + kbytes_w);
 
     // ---- DMA roles (A, and int8 B): wave w copies tile rows [16 NH w, 16 NH (w + 1)) of a K group
     // as NH 1 KB blocks. Lane l of block h writes LDS bytes [16 l, 16 l + 16) of tile row
@@ -313,7 +317,9 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         const int r = 16 * NH * wave + 16 * h + (lane >> 2);
         const int c = (lane & 3) ^ ((r >> 1) & 3);
         dma_a[h] = r < rows_m ? static_cast<int>(r * a.lda) + c * 16 : kOob;
-        dma_b[h] = r < rows_n ? static_cast<int>(r * a.ldw) + c * 16 : kOob;
+        dma_b[h] = r >= rows_n ? kOob
+                   : wt ? (r >> 4) * G * 1024 + (r & 15) * 64 + c * 16
+                        : static_cast<int>(r * a.ldw) + c * 16;
     }
     const int dma_lds = (16 * NH * wave) * TK;   // + 16 * TK for block h
 
@@ -364,7 +370,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
                   soff(g, TK));
             if constexpr (!kPacked)
                 dma16(live ? rb_rs : rb_none, smem, B_LDS + st * TILE_BYTES + dma_lds + h * 16 * TK, dma_b[h],
-                      soff(g, TK));
+                      soff(g, wt ? 1024 : TK));
         }
     };
     // Two register sets carry packed B groups from their global load to their LDS store.

@@ -70,7 +70,11 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
     const int64_t n = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * kCols + (lane >> 4);
     const bool col_ok = n < a.N;
     const int64_t nc = col_ok ? n : 0;
-    const uint8_t* wrow = a.qw + nc * a.ldw;
+    // int8 weights in 16-row tiles: chunk c of row nc is at block c / 4 of the row's 16-row band,
+    // row nc % 16 within it; the wave's 4 columns are 4 consecutive rows of one band, so a load
+    // still reads 256 contiguous bytes per K group
+    const bool wt = !kPacked && a.wtile;
+    const uint8_t* wrow = wt ? a.qw + (nc >> 4) * (K / 64) * 1024 + (nc & 15) * 64 : a.qw + nc * a.ldw;
 
     // Every load below is unconditional, from an address inside the operands (chunks past the row
     // read its last chunk, columns past N column 0, rows past M row M - 1): a load whose value were
@@ -97,7 +101,8 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
         for (int h = 0; h < kH; ++h) {
             const int c = min(c0 + 16 * h, nch - 1);
             const int g = c * kChunkK / 64;
-            w[h] = *reinterpret_cast<const uint4*>(wrow + 16 * static_cast<int64_t>(c));
+            w[h] = *reinterpret_cast<const uint4*>(wrow + (wt ? (c >> 2) * 1024 + (c & 3) * 16
+                                                                 : 16 * static_cast<int64_t>(c)));
             zb[h] = 0u;
             sb[h] = 0u;
             if constexpr (WK == WKind::U4Asym) zb[h] = a.wz[nc * a.ldwz + (g >> 1)];

@@ -45,6 +45,9 @@ int launch_quantize_weight(const void* w, int dtype, int64_t N, int64_t K, int64
                            void* q, int64_t ldq, void* scale, int64_t ld_scale, void* zero, int64_t ld_zero,
                            hipStream_t stream);
 
+// int8 weights [N, K] into the 16-row tile layout of GemmArgs::wtile (mq_wquant.hip)
+int launch_tile_weight_i8(const uint8_t* w, int64_t ldw, int64_t N, int64_t K, uint8_t* out, hipStream_t stream);
+
 // --- GEMMs (mq_gemm.hip)
 enum class WKind : int { U4Asym = 0, I4Sym = 1, I8 = 2 };
 enum class Epi : int { GroupScale = 0, GroupPartials = 1, RowScale = 2, RowAcc = 3 };
@@ -78,6 +81,9 @@ struct GemmArgs {
     // output tile of the wide kernel: 256 (256 x 256), 192 (256 x 192) or 128 (128 x 128); 0:
     // choose_tile decides
     int tile = 0;
+    // int8 weights (WKind::I8) in 16-row tiles: [ceil(N / 16)][K / 64][16][64] bytes, so that a
+    // 1 KB block holds one K group of 16 consecutive rows (ldw = K); 0: rows of ldw bytes
+    int wtile = 0;
 };
 
 // Output tile of the wide kernel for an M x N product (a tile code as above): 128 when 256 x 256

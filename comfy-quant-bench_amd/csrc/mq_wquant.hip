@@ -17,6 +17,7 @@
 // tools/_formats.py:128-167). The quantizer runs once per weight, so it favours a simple exact
 // structure over speed: the row is read once from HBM and each output byte written once.
 #include "mq_device.h"
+#include <algorithm>
 #include "mq_internal.h"
 
 #pragma clang fp contract(off)
@@ -188,7 +189,28 @@ int launch_dt(const void* w, int64_t ldw, int64_t N, int64_t K, int hblock, int 
     return -1;
 }
 
+// int8 weights [N, K] (row stride ldw) to 16-row tiles [ceil(N / 16)][K / 64][16][64]: one thread
+// per 16-byte unit u of the output, u = ((band * G + g) * 16 + row) * 4 + chunk; rows past N get 0.
+__global__ void __launch_bounds__(256) tile16_kernel(const uint8_t* w, int64_t ldw, int64_t N, int64_t K,
+                                                    uint8_t* out) {
+    const int64_t G = K / 64, units = (N + 15) / 16 * 16 * (K / 16);
+    for (int64_t u = blockIdx.x * int64_t(256) + threadIdx.x; u < units; u += int64_t(gridDim.x) * 256) {
+        const int64_t chunk = u & 3, row = (u >> 2) & 15, g = (u >> 6) % G, band = (u >> 6) / G;
+        const int64_t n = band * 16 + row;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (n < N) v = *reinterpret_cast<const uint4*>(w + n * ldw + g * 64 + chunk * 16);
+        *reinterpret_cast<uint4*>(out + u * 16) = v;
+    }
+}
+
 }  // namespace
+
+int launch_tile_weight_i8(const uint8_t* w, int64_t ldw, int64_t N, int64_t K, uint8_t* out, hipStream_t stream) {
+    const int64_t units = (N + 15) / 16 * 16 * (K / 16);
+    const int64_t blocks = std::min<int64_t>((units + 255) / 256, 65536);
+    hipLaunchKernelGGL(tile16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, w, ldw, N, K, out);
+    return launch_status("tile_weight_i8");
+}
 
 int launch_quantize_weight(const void* w, int dtype, int64_t N, int64_t K, int64_t ldw, int hblock, int format,
                            void* q, int64_t ldq, void* scale, int64_t ld_scale, void* zero, int64_t ld_zero,

@@ -21,10 +21,12 @@ from .ops import (
     gemm_w4_group_partials,
     int8_linear,
     int8_rowscale_linear,
+    is_tile16,
     quantize_int4_rowwise_convrot64,
     quantize_int8_rowwise_convrot,
     rotate_quantize,
     swiglu_quantize_int4_rowwise_convrot64,
+    tile_int8_weight,
     w4a8_int8_linear,
 )
 from .weights import (

@@ -11,7 +11,7 @@ import os
 
 import torch  # noqa: F401  (must be imported before the library is loaded)
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmq.so")
 
@@ -41,6 +41,7 @@ _SIGNATURES = {
                           c_i64, c_vp], c_int),
     "mq_gemm_rowscale_ws": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_int, c_vp, c_int, c_i64, c_i64,
                              c_i64, c_i64, c_vp, c_i64, c_vp], c_int),
+    "mq_tile_weight_i8": ([c_vp, c_i64, c_i64, c_i64, c_vp, c_vp], c_int),
     "mq_gemm_rowscale_acc": ([c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_vp], c_int),
     "mq_linear_workspace_bytes": ([c_i64, c_i64, c_i64], c_i64),
     "mq_linear_w4_group": ([c_vp, c_int, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp,
@@ -55,6 +56,7 @@ EXPORTED = tuple(_SIGNATURES)
 
 # code layouts (include/mq.h)
 Q_BYTES, Q_PACKED, Q_X16ALT = 0, 1, 2
+W8_TILE16 = 0x100            # wbits flag: int8 weights in 16-row tiles (include/mq.h)
 ACT_I8, ACT_I4, ACT_X16ALT = 0, 1, 2
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 64 << 20   # MQ_NOALLOC_SCRATCH_BYTES

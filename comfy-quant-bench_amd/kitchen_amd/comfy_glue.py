@@ -70,7 +70,8 @@ def register_custom_ops() -> dict[str, Callable]:
 
     @_int8.register_fake
     def _(x, weight, weight_scale, bias, out_dtype, convrot, convrot_groupsize, input_act):
-        return x.new_empty((*x.shape[:-1], weight.shape[0]), dtype=out_dtype)
+        n = weight_scale.numel() if ops.is_tile16(weight) else weight.shape[0]
+        return x.new_empty((*x.shape[:-1], n), dtype=out_dtype)
 
     def convrot_w4a4_linear(x, qweight, wscales, bias=None, convrot_groupsize=256, quant_group_size=64,
                             linear_dtype="int4", input_act=None):
@@ -207,6 +208,8 @@ def layer_linear(tensors: dict, layer: str, config: dict, compile_safe: bool = F
         # (tools/_formats.py:150-152) and the loader reads layer_conf.get("convrot", False)
         # (tools/verify_w4a4.py:313-315,338)
         convrot = bool(config.get("convrot", False))
+        if w.is_cuda and w.dim() == 2 and w.shape[1] >= 192 and w.shape[1] % 64 == 0:
+            w = ops.tile_int8_weight(w)   # prepared once at load: same results, whole-line weight loads
         return lambda x, bias=None, out_dtype=torch.bfloat16, input_act=None: lin["int8_linear"](
             x, w, scale, bias, out_dtype, convrot, cg if cg else 256, input_act)
     raise NotImplementedError(f"{layer}: format {fmt!r} is not on this path")

@@ -280,14 +280,47 @@ def gemm_w4_group_partials(qa, qweight, wzeros, n: int, group_size: int = INT4_G
     return part
 
 
+def is_tile16(weight) -> bool:
+    """True for int8 weights in the 16-row tile layout of tile_int8_weight."""
+    return weight.dim() == 4 and tuple(weight.shape[2:]) == (16, 64)
+
+
+def tile_int8_weight(weight: torch.Tensor) -> torch.Tensor:
+    """int8 weights [N, K] -> the 16-row tile layout [ceil(N / 16), K / 64, 16, 64]
+    (mq_tile_weight_i8): block [b, g] holds bytes 64 g .. 64 g + 63 of rows 16 b .. 16 b + 15, rows
+    past N zero. The int8 row-scale linears and GEMMs take it in place of [N, K] (N is then the
+    length of the row scale) with the same results bit for bit; every K group of the GEMM's weight
+    loads is then whole cache lines. Prepare it once per weight. Needs K % 64 == 0 and K >= 192."""
+    if weight.dim() != 2 or weight.element_size() != 1:
+        raise ValueError(f"expected 8-bit weights [N, K], got {weight.dtype} {list(weight.shape)}")
+    n, k = weight.shape
+    w = weight if weight.stride(1) == 1 and weight.stride(0) % 16 == 0 else weight.contiguous()
+    out = torch.empty(((n + 15) // 16, k // 64, 16, 64), dtype=torch.int8, device=weight.device)
+    _lib.call("mq_tile_weight_i8", w.data_ptr(), w.stride(0), n, k, out.data_ptr(), _lib.stream_of(w))
+    return out
+
+
+def _weight_args(qweight, n: int, k: int, wbits: int):
+    """(ldw, wbits) of the row-scale entries for [N, K'] rows or the 16-row tile layout."""
+    if is_tile16(qweight):
+        if wbits != 8 or qweight.element_size() != 1:
+            raise ValueError("the 16-row tile layout holds int8 weights (wbits 8)")
+        if tuple(qweight.shape) != ((n + 15) // 16, k // 64, 16, 64) or not qweight.is_contiguous():
+            raise ValueError(f"16-row tile weights for N={n} K={k} must be contiguous "
+                             f"[{(n + 15) // 16}, {k // 64}, 16, 64], got {list(qweight.shape)}")
+        return k, wbits | _lib.W8_TILE16
+    return qweight.stride(0), wbits
+
+
 def gemm_rowscale(qa, sa, qweight, wscales, bias, n: int, wbits: int, out_dtype=torch.bfloat16):
     """y [M, N] = (qa . w^T) * sa[m] * wscales[n] + bias in out_dtype, full-K int32 accumulator (split
     over K into int32 partial sums for small M, summed exactly)."""
     m, k = qa.shape
     y = torch.empty((m, n), dtype=out_dtype, device=qa.device)
     work = _workspace(m, n, k, qa.device)
+    ldw, wb = _weight_args(qweight, n, k, int(wbits))
     _lib.call("mq_gemm_rowscale_ws", qa.data_ptr(), qa.stride(0), sa.data_ptr(), qweight.data_ptr(),
-              qweight.stride(0), int(wbits), wscales.data_ptr(), *_bias_args(bias), y.data_ptr(),
+              ldw, wb, wscales.data_ptr(), *_bias_args(bias), y.data_ptr(),
               _lib.dtype_code(out_dtype), y.stride(0), m, n, k, _lib.ptr(work), 0 if work is None else work.numel(),
               _lib.stream_of(qa))
     return y
@@ -297,8 +330,9 @@ def gemm_rowscale_acc(qa, qweight, n: int, wbits: int):
     """Parity entry: the full-K int32 accumulator [M, N] of gemm_rowscale."""
     m, k = qa.shape
     acc = torch.empty((m, n), dtype=torch.int32, device=qa.device)
-    _lib.call("mq_gemm_rowscale_acc", qa.data_ptr(), qa.stride(0), qweight.data_ptr(), qweight.stride(0),
-              int(wbits), acc.data_ptr(), m, n, k, _lib.stream_of(qa))
+    ldw, wb = _weight_args(qweight, n, k, int(wbits))
+    _lib.call("mq_gemm_rowscale_acc", qa.data_ptr(), qa.stride(0), qweight.data_ptr(), ldw, wb, acc.data_ptr(),
+              m, n, k, _lib.stream_of(qa))
     return acc
 
 
@@ -371,17 +405,18 @@ def _linear_rowscale(x, swiglu, cg, act_bits, qweight, wbits, wscales, bias, n, 
     """rotate + quantize + row-scale GEMM in one library call (mq_linear_rowscale)."""
     x2, swiglu = _linear_input(x, swiglu, k)
     m = x2.shape[0]
-    qw = qweight.contiguous()
+    qw = qweight if is_tile16(qweight) else qweight.contiguous()
     wbytes = k // 2 if wbits == 4 else k
-    if qw.shape != (n, wbytes) or qw.element_size() != 1:
+    if not is_tile16(qw) and (qw.shape != (n, wbytes) or qw.element_size() != 1):
         raise ValueError(f"weight must be 8-bit [{n}, {wbytes}]")
+    ldw, wbits = _weight_args(qw, n, k, int(wbits))
     b = _bias(bias, n, x2.device)
     y = torch.empty((m, n), dtype=out_dtype, device=x2.device)
     if m == 0:
         return y
     work = _linear_workspace(m, n, k, x2.device)
     _lib.call("mq_linear_rowscale", x2.data_ptr(), _lib.dtype_code(x2.dtype), x2.stride(0), int(cg or 0),
-              int(act_bits), int(swiglu), qw.data_ptr(), qw.stride(0), int(wbits), wscales.data_ptr(), *_bias_args(b),
+              int(act_bits), int(swiglu), qw.data_ptr(), ldw, wbits, wscales.data_ptr(), *_bias_args(b),
               y.data_ptr(), _lib.dtype_code(out_dtype), y.stride(0), m, n, k, work.data_ptr(), work.numel(),
               _lib.stream_of(x2))
     return y
@@ -413,8 +448,10 @@ class PreparedW4A8:
     the row-scale GEMM takes; calling it runs only rotate + quantize and the int8 GEMM."""
 
     def __init__(self, qdata, s_rel, s_channel, codebook=None, group_size: int = 16, convrot_groupsize: int = 256):
-        self.q8, self.row_scale = decode_w4a8_codebook_weight(qdata, s_rel, s_channel, codebook, group_size)
-        self.n, self.k = self.q8.shape
+        q8, self.row_scale = decode_w4a8_codebook_weight(qdata, s_rel, s_channel, codebook, group_size)
+        self.n, self.k = q8.shape
+        # held in 16-row tiles where the GEMM takes them (same results, whole-line weight loads)
+        self.q8 = tile_int8_weight(q8) if self.k >= 192 and self.k % 64 == 0 else q8
         self.convrot_groupsize = convrot_groupsize
 
     def __call__(self, x, bias=None, out_dtype=None):
@@ -428,9 +465,11 @@ def int8_rowscale_linear(x, q8, row_scale, bias=None, out_dtype=None, convrot_gr
     x_out = x
     x, swiglu = _input_act(x, input_act)
     k = x.shape[-1] // 2 if swiglu else x.shape[-1]
-    n = q8.shape[0]
-    if q8.shape[1] != k:
-        raise ValueError(f"Input K={k} does not match weight K={q8.shape[1]}")
+    # [N, K] rows, or the 16-row tile layout of tile_int8_weight (N = the row scale's length)
+    n = row_scale.numel() if is_tile16(q8) else q8.shape[0]
+    kw = q8.shape[1] * 64 if is_tile16(q8) else q8.shape[1]
+    if kw != k:
+        raise ValueError(f"Input K={k} does not match weight K={kw}")
     if convrot_groupsize and k % convrot_groupsize:
         raise ValueError(f"Input K={k} is not divisible by convrot_groupsize={convrot_groupsize}")
     ws = row_scale.reshape(-1).to(torch.float32).contiguous()

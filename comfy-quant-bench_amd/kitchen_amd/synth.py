@@ -62,6 +62,8 @@ def mmdit_linear_stack(blocks: int = 60, w4a4_frac: float = 0.35, seed: int = 4,
     random positive scales), which is what quantizing random-init weights produces.
 
     Returns a list of dicts: {"name", "stream", "M", "K", "N", "fmt", "tensors"}."""
+    from . import ops
+
     gen = torch.Generator(device="cpu").manual_seed(seed)
     pick = torch.rand(blocks * 2 * len(MMDIT_LINEARS), generator=gen) < w4a4_frac
     dgen = torch.Generator(device=device).manual_seed(seed + 1)
@@ -80,7 +82,8 @@ def mmdit_linear_stack(blocks: int = 60, w4a4_frac: float = 0.35, seed: int = 4,
                 else:
                     w = torch.randint(-127, 128, (n, k), generator=dgen, device=device, dtype=torch.int8)
                     s = torch.rand(n, 1, generator=dgen, device=device) * 2e-4 + 3e-4
-                    tensors = {"weight": w, "weight_scale": s, "bias": bias}
+                    # held in the 16-row tile layout a loader prepares (ops.tile_int8_weight)
+                    tensors = {"weight": ops.tile_int8_weight(w), "weight_scale": s, "bias": bias}
                     fmt = "w8a8"
                 layers.append({"name": f"blocks.{b}.{stream}.{name}", "stream": stream, "M": m, "K": k, "N": n,
                                "fmt": fmt, "tensors": tensors})

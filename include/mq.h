@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MQ_ABI_VERSION 7
+#define MQ_ABI_VERSION 8
 
 enum {
     MQ_OK = 0,
@@ -233,11 +233,25 @@ int mq_gemm_w4_group_partials(const int8_t* qa, int64_t lda, const uint8_t* qw, 
  * int8 x int8 GEMM of int8_linear (tools/verify_w4a4.py:342-370) when wbits = 8.
  *
  *   qa    int8 activation codes [M, K], stride lda bytes
- *   qw    wbits 4: signed int4 packed [N, K/2]; wbits 8: int8 [N, K]; stride ldw bytes
+ *   qw    wbits 4: signed int4 packed [N, K/2]; wbits 8: int8 [N, K]; stride ldw bytes;
+ *         wbits 8 | MQ_W8_TILE16: int8 in the 16-row tile layout below (ldw ignored)
  *   ws    fp32 [N]
  *   bias, y as mq_gemm_w4_group
  * Requires K % 64 == 0.
  */
+
+/* wbits flag of the int8 row-scale entries (mq_gemm_rowscale*, mq_linear_rowscale): the int8
+ * weights are in 16-row tiles, [ceil(N/16)][K/64][16][64] bytes, block (b, g) holding bytes
+ * [64 g, 64 g + 64) of rows 16 b .. 16 b + 15 (rows past N zero). No counterpart in the reference,
+ * whose int8 weights are [N, K] rows (tools/verify_w4a4.py:342-370): it is the same weight in a
+ * layout whose K groups are whole cache lines for the GEMM's loads, written once per weight by
+ * mq_tile_weight_i8, and gives the same results bit for bit. Needs K >= 192 and a tiled array
+ * under 2 GiB. */
+#define MQ_W8_TILE16 0x100
+
+/* int8 weights [N, K] (stride ldw bytes, ldw % 16 == 0, 16-byte aligned) into the MQ_W8_TILE16
+ * layout at out (ceil(N/16) * 16 * K bytes, 16-byte aligned). */
+int mq_tile_weight_i8(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t* out, void* stream);
 int mq_gemm_rowscale(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw,
                      int wbits, const float* ws, const void* bias, int bias_dtype, void* y, int y_dtype,
                      int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream);

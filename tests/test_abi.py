@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mq_abi_version() == 7
+    assert lib.mq_abi_version() == 8
 
 
 def _err(lib):
@@ -116,6 +116,22 @@ def test_gemm_validation_rejects_before_launch(lib):
     assert "wbits" in _err(lib)
     assert lib.mq_gemm_rowscale_acc(None, 64, None, 64, 8, None, 8, 8, 64, None) == -1
     assert "null" in _err(lib)
+
+
+def test_tile16_weight_validation(lib):
+    # the 16-row tile layout: int8 weights only, K >= 192, whole tiled array under 2 GiB
+    a = 1 << 20
+    assert lib.mq_gemm_rowscale(a, 64, a, a, 32, 4 | 0x100, a, None, 0, a, 0, 64, 8, 8, 64, None) == -1
+    assert "int8 weights" in _err(lib)
+    assert lib.mq_gemm_rowscale(a, 128, a, a, 128, 8 | 0x100, a, None, 0, a, 0, 64, 8, 8, 128, None) == -1
+    assert "K >= 192" in _err(lib)
+    assert lib.mq_gemm_rowscale_acc(a, 1 << 16, a, 0, 8 | 0x100, a, 8, 1 << 16, 1 << 16, None) == -1
+    assert "2 GiB" in _err(lib)
+    assert lib.mq_tile_weight_i8(a, 128, 8, 128, a, None) == -1
+    assert "K >= 192" in _err(lib)
+    assert lib.mq_tile_weight_i8(a, 200, 8, 192, a, None) == -1
+    assert "ldw" in _err(lib)
+    assert lib.mq_tile_weight_i8(None, 192, 0, 192, None, None) == 0
 
 
 def test_gemm_output_types_are_checked(lib):

@@ -41,7 +41,10 @@ def test_one_block_against_oracle(gpu_device):
             p = gemm.partials(qa, quant.unpack_i4(t["qweight"].numpy()), 64)
             ref = gemm.epilogue_group(p, sa, t["wscales"].numpy().astype(np.float64), bias)
         else:
-            ref = linear.w8a8_linear(xf, t["weight"].numpy(), t["weight_scale"].numpy(), bias, 256).y
+            w = t["weight"].numpy()
+            if w.ndim == 4:   # 16-row tiles [N/16, K/64, 16, 64] back to rows
+                w = w.transpose(0, 2, 1, 3).reshape(-1, k)[:n]
+            ref = linear.w8a8_linear(xf, w, t["weight_scale"].numpy(), bias, 256).y
         err = gemm.rel_l2(ref, y.float().cpu().numpy()[rows])
         assert err < 4e-3, (layer["name"], err)
 

@@ -122,3 +122,59 @@ def test_model_catches_an_offset_past_the_range(which, t):
 
     with pytest.raises(AssertionError, match=f"{which} load"):
         _check(300, 200, 320, loads=unshifted, T=t)
+
+
+def _loads_i8(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=(256, 256), tiled=True):
+    """The int8-weight kinds' DMA loads (A, and B through the same DMA roles): B rows of K bytes or,
+    tiled, 16-row tiles [ceil(N / 16)][K / 64][16][64] whose K group of 16 rows is one 1 KB block
+    (mq_gemm_wide.hip, wt). Also checks that each tile's B resource lies inside the tiled array."""
+    TM, TN = T
+    NH = TM // 128
+    G = K // TK
+    G4 = (G + 3) // 4 * 4
+    tiles_m, tiles_n = -(-M // TM), -(-N // TN)
+    tid = np.arange(512)
+    wave, lane = tid >> 6, tid & 63
+    for tm, tn, s in itertools.product(range(tiles_m), range(tiles_n), range(slices)):
+        m0, n0 = tm * TM, tn * TN
+        rows_m, rows_n = min(TM, M - m0), min(TN, N - n0)
+        g0 = s * kgroups if slices > 1 else 0
+        g1 = min(g0 + kgroups, G4) if slices > 1 else G4
+        ra = (rows_m - 1) * K + K
+        if tiled:
+            rb = ((rows_n + 15) >> 4) * G * 1024
+            assert (n0 >> 4) * G * 1024 + rb <= -(-N // 16) * G * 1024
+        else:
+            rb = (rows_n - 1) * K + K
+        dma_a, dma_b = [], []
+        for h in range(NH):
+            r = 16 * NH * wave + 16 * h + (lane >> 2)
+            c = (lane & 3) ^ ((r >> 1) & 3)
+            dma_a.append(np.where(r < rows_m, r * K + c * 16, KOOB))
+            tb = (r >> 4) * G * 1024 + (r & 15) * 64 + c * 16 if tiled else r * K + c * 16
+            dma_b.append(np.where(r < rows_n, tb, KOOB))
+        for g in range(g0, g1):
+            live = g < G
+            for h in range(NH):
+                yield "A", ra if live else 0, dma_a[h], g * TK if live else 0, 16
+                yield "B8", rb if live else 0, dma_b[h], (g * (1024 if tiled else TK)) if live else 0, 16
+
+
+@pytest.mark.parametrize("tiled", [True, False])
+@pytest.mark.parametrize("t", TILES)
+@pytest.mark.parametrize("m,n,k", [(257, 300, 192), (300, 256, 320), (513, 400, 3136), (5, 3000, 1024),
+                                   (64, 17, 448), (1, 16, 192)])
+def test_int8_weight_dma_stays_in_range(m, n, k, t, tiled):
+    _check(m, n, k, T=t, loads=lambda *a, **kw: _loads_i8(*a, **kw, tiled=tiled))
+
+
+def test_int8_tiled_model_catches_a_wrong_band_stride():
+    # a band stride of one K group (instead of G) runs past the tile's range for K > 64
+    def wrong(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=(256, 256)):
+        for what, rng, voff, soff, width in _loads_i8(M, N, K, ldwz, ldws, kgroups, slices, T, tiled=True):
+            if what == "B8":
+                voff = np.where(voff == KOOB, KOOB, voff + (voff // (K // TK * 1024)) * 1024 * 3)
+            yield what, rng, voff, soff, width
+
+    with pytest.raises(AssertionError):
+        _check(300, 256, 256, loads=wrong)
