@@ -259,15 +259,19 @@ int mq_tile_weight_i8(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t
                                  static_cast<hipStream_t>(stream));
 }
 
-int mq_gemm_w4_group_ws(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
-                        const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
-                        const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy, int64_t M, int64_t N,
-                        int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
-    clear_error();
+}  // extern "C"
+
+namespace {
+
+// Validated arguments of the group-scale GEMM (mq_gemm_w4_group_ws); kEmpty for an empty product.
+int w4_group_args(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw, const uint16_t* ws,
+                  int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode, const void* bias,
+                  int bias_dtype, void* y, int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace,
+                  int64_t workspace_bytes, GemmArgs* out) {
     MQ_REQUIRE(group == 64, "gemm_w4_group: quant group size must be 64 (got %d)", group);
     MQ_REQUIRE(act_mode >= MQ_ACT_I8 && act_mode <= MQ_ACT_X16ALT, "gemm_w4_group: unknown act_mode %d", act_mode);
     int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, K / 2);
-    if (rc) return rc == kEmpty ? MQ_OK : rc;
+    if (rc) return rc;
     MQ_REQUIRE(sa && ws, "gemm_w4_group: null pointer");
     rc = check_gemm_out("gemm_w4_group", bias, bias_dtype, y, y_dtype, ldy, N);
     if (rc) return rc;
@@ -281,6 +285,49 @@ int mq_gemm_w4_group_ws(const int8_t* qa, int64_t lda, const float* sa, const ui
     a.M = M; a.N = N; a.K = K;
     a.act_mode = act_mode;
     a.work = workspace; a.work_bytes = workspace ? workspace_bytes : 0;
+    *out = a;
+    return MQ_OK;
+}
+
+// Validated arguments of the row-scale GEMM (mq_gemm_rowscale_ws), wbits with its layout flag.
+int rowscale_args(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw, int wbits,
+                  const float* ws, const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy, int64_t M,
+                  int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, GemmArgs* out, WKind* wk) {
+    const bool tile16 = (wbits & MQ_W8_TILE16) != 0;
+    wbits &= ~MQ_W8_TILE16;
+    MQ_REQUIRE(wbits == 4 || wbits == 8, "gemm_rowscale: wbits must be 4 or 8 (got %d)", wbits);
+    int rc = check_tile16("gemm_rowscale", tile16, wbits, N, K, &ldw);
+    if (rc) return rc;
+    rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, wbits == 4 ? K / 2 : K);
+    if (rc) return rc;
+    MQ_REQUIRE(sa && ws, "gemm_rowscale: null pointer");
+    rc = check_gemm_out("gemm_rowscale", bias, bias_dtype, y, y_dtype, ldy, N);
+    if (rc) return rc;
+    MQ_REQUIRE(workspace_bytes >= 0 && (!workspace || aligned(workspace, 16)),
+               "gemm_rowscale: workspace must be 16-byte aligned");
+    GemmArgs a{};
+    a.qa = qa; a.lda = lda; a.sa = sa; a.qw = static_cast<const uint8_t*>(qw); a.ldw = ldw; a.ws32 = ws;
+    a.bias = bias; a.bias_dtype = bias_dtype; a.y = y; a.y_dtype = y_dtype; a.ldy = ldy; a.M = M; a.N = N; a.K = K;
+    a.work = workspace; a.work_bytes = workspace ? workspace_bytes : 0;
+    a.wtile = tile16;
+    *out = a;
+    *wk = wbits == 4 ? WKind::I4Sym : WKind::I8;
+    return MQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mq_gemm_w4_group_ws(const int8_t* qa, int64_t lda, const float* sa, const uint8_t* qw, int64_t ldw,
+                        const uint16_t* ws, int64_t ldws, const uint8_t* wz, int64_t ldwz, int group, int act_mode,
+                        const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy, int64_t M, int64_t N,
+                        int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
+    clear_error();
+    GemmArgs a;
+    const int rc = w4_group_args(qa, lda, sa, qw, ldw, ws, ldws, wz, ldwz, group, act_mode, bias, bias_dtype, y,
+                                 y_dtype, ldy, M, N, K, workspace, workspace_bytes, &a);
+    if (rc) return rc == kEmpty ? MQ_OK : rc;
     return launch_gemm(a, wz ? WKind::U4Asym : WKind::I4Sym, Epi::GroupScale, static_cast<hipStream_t>(stream));
 }
 
@@ -313,24 +360,12 @@ int mq_gemm_rowscale_ws(const int8_t* qa, int64_t lda, const float* sa, const vo
                         const float* ws, const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy,
                         int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
     clear_error();
-    const bool tile16 = (wbits & MQ_W8_TILE16) != 0;
-    wbits &= ~MQ_W8_TILE16;
-    MQ_REQUIRE(wbits == 4 || wbits == 8, "gemm_rowscale: wbits must be 4 or 8 (got %d)", wbits);
-    int rc = check_tile16("gemm_rowscale", tile16, wbits, N, K, &ldw);
-    if (rc) return rc;
-    rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, wbits == 4 ? K / 2 : K);
+    GemmArgs a;
+    WKind wk;
+    const int rc = rowscale_args(qa, lda, sa, qw, ldw, wbits, ws, bias, bias_dtype, y, y_dtype, ldy, M, N, K, workspace,
+                                 workspace_bytes, &a, &wk);
     if (rc) return rc == kEmpty ? MQ_OK : rc;
-    MQ_REQUIRE(sa && ws, "gemm_rowscale: null pointer");
-    rc = check_gemm_out("gemm_rowscale", bias, bias_dtype, y, y_dtype, ldy, N);
-    if (rc) return rc;
-    MQ_REQUIRE(workspace_bytes >= 0 && (!workspace || aligned(workspace, 16)),
-               "gemm_rowscale: workspace must be 16-byte aligned");
-    GemmArgs a{};
-    a.qa = qa; a.lda = lda; a.sa = sa; a.qw = static_cast<const uint8_t*>(qw); a.ldw = ldw; a.ws32 = ws;
-    a.bias = bias; a.bias_dtype = bias_dtype; a.y = y; a.y_dtype = y_dtype; a.ldy = ldy; a.M = M; a.N = N; a.K = K;
-    a.work = workspace; a.work_bytes = workspace ? workspace_bytes : 0;
-    a.wtile = tile16;
-    return launch_gemm(a, wbits == 4 ? WKind::I4Sym : WKind::I8, Epi::RowScale, static_cast<hipStream_t>(stream));
+    return launch_gemm(a, wk, Epi::RowScale, static_cast<hipStream_t>(stream));
 }
 
 int mq_gemm_rowscale(const int8_t* qa, int64_t lda, const float* sa, const void* qw, int64_t ldw, int wbits,
@@ -379,7 +414,9 @@ struct LinearWs {
 LinearWs linear_ws(int64_t M, int64_t N, int64_t K) {
     LinearWs w;
     w.codes = 0;
-    w.scales = align_up(M * K);
+    // codes for M rows rounded up to 16: in the 16-row tile layout the last band spans 16 rows
+    // whatever M is (its rows past M are never written or read)
+    w.scales = align_up((M + 15) / 16 * 16 * K);
     w.split = w.scales + align_up(M * 4);
     w.need = w.split;
     w.total = w.split + align_up(mq_gemm_workspace_bytes(M, N, K));
@@ -404,13 +441,30 @@ int check_linear(const char* what, int act_bits, int swiglu, int64_t M, int64_t 
     return MQ_OK;
 }
 
+// tiled: the codes in 16-row tiles [ceil(M / 16)][K / 64][16][64] (GemmArgs::atile) instead of rows
+// of K bytes; the kernels take that layout from a row stride of 0
 int quantize_into(const void* x, int x_dtype, int64_t ldx, int hblock, int act_bits, int swiglu, int layout,
-                  int64_t M, int64_t K, uint8_t* ws_base, void* stream) {
+                  bool tiled, int64_t M, int64_t K, uint8_t* ws_base, void* stream) {
     const LinearWs w = linear_ws(M, 1, K);
     void* q = ws_base + w.codes;
     float* s = reinterpret_cast<float*>(ws_base + w.scales);
-    return swiglu ? mq_swiglu_rotquant(x, x_dtype, M, K, ldx, hblock, act_bits, layout, q, K, s, stream)
-                  : mq_rotquant(x, x_dtype, M, K, ldx, hblock, act_bits, layout, q, K, s, stream);
+    if (!tiled)
+        return swiglu ? mq_swiglu_rotquant(x, x_dtype, M, K, ldx, hblock, act_bits, layout, q, K, s, stream)
+                      : mq_rotquant(x, x_dtype, M, K, ldx, hblock, act_bits, layout, q, K, s, stream);
+    const int rc = swiglu ? check_rotquant("swiglu_rotquant", x, x_dtype, false, M, K, 2 * K, ldx, hblock, act_bits,
+                                           layout, q, K, s)
+                          : check_rotquant("rotquant", x, x_dtype, true, M, K, K, ldx, hblock, act_bits, layout, q, K,
+                                           s);
+    if (rc != MQ_OK) return rc;
+    auto* xs = static_cast<const uint16_t*>(x);
+    auto* st = static_cast<hipStream_t>(stream);
+    if (swiglu)
+        return x_dtype == MQ_DT_F16 ? launch_swiglu_rotquant_f16(xs, M, K, ldx, hblock, act_bits, layout, q, 0, s, st)
+                                    : launch_swiglu_rotquant_bf16(xs, M, K, ldx, hblock, act_bits, layout, q, 0, s, st);
+    if (x_dtype == MQ_DT_F32)
+        return launch_rotquant_f32(static_cast<const float*>(x), M, K, ldx, hblock, act_bits, layout, q, 0, s, st);
+    return x_dtype == MQ_DT_F16 ? launch_rotquant_f16(xs, M, K, ldx, hblock, act_bits, layout, q, 0, s, st)
+                                : launch_rotquant_bf16(xs, M, K, ldx, hblock, act_bits, layout, q, 0, s, st);
 }
 
 }  // namespace
@@ -433,13 +487,18 @@ int mq_linear_w4_group(const void* x, int x_dtype, int64_t ldx, int hblock, int 
     const int layout = act_bits == 4 ? MQ_Q_X16ALT : MQ_Q_BYTES;
     const int act_mode = act_bits == 4 ? MQ_ACT_X16ALT : MQ_ACT_I8;
     auto* base = static_cast<uint8_t*>(workspace);
-    rc = quantize_into(x, x_dtype, ldx, hblock, act_bits, swiglu, layout, M, K, base, stream);
-    if (rc) return rc;
     const LinearWs w = linear_ws(M, N, K);
-    return mq_gemm_w4_group_ws(reinterpret_cast<const int8_t*>(base + w.codes), K,
-                               reinterpret_cast<const float*>(base + w.scales), qw, ldw, ws, ldws, wz, ldwz, 64,
-                               act_mode, bias, bias_dtype, y, y_dtype, ldy, M, N, K, base + w.split,
-                               workspace_bytes - w.split, stream);
+    GemmArgs a;
+    rc = w4_group_args(reinterpret_cast<const int8_t*>(base + w.codes), K,
+                       reinterpret_cast<const float*>(base + w.scales), qw, ldw, ws, ldws, wz, ldwz, 64, act_mode, bias,
+                       bias_dtype, y, y_dtype, ldy, M, N, K, base + w.split, workspace_bytes - w.split, &a);
+    if (rc) return rc == kEmpty ? MQ_OK : rc;
+    const WKind wk = wz ? WKind::U4Asym : WKind::I4Sym;
+    a.atile = 1;   // the codes in 16-row tiles wherever the wide kernel reads them
+    a.atile = gemm_runs_wide(a, wk, Epi::GroupScale);
+    rc = quantize_into(x, x_dtype, ldx, hblock, act_bits, swiglu, layout, a.atile, M, K, base, stream);
+    if (rc) return rc;
+    return launch_gemm(a, wk, Epi::GroupScale, static_cast<hipStream_t>(stream));
 }
 
 int mq_linear_rowscale(const void* x, int x_dtype, int64_t ldx, int hblock, int act_bits, int swiglu, const void* qw,
@@ -450,12 +509,18 @@ int mq_linear_rowscale(const void* x, int x_dtype, int64_t ldx, int hblock, int 
     int rc = check_linear("linear_rowscale", act_bits, swiglu, M, N, K, workspace, workspace_bytes);
     if (rc) return rc == kEmpty ? MQ_OK : rc;
     auto* base = static_cast<uint8_t*>(workspace);
-    rc = quantize_into(x, x_dtype, ldx, hblock, act_bits, swiglu, MQ_Q_BYTES, M, K, base, stream);
-    if (rc) return rc;
     const LinearWs w = linear_ws(M, N, K);
-    return mq_gemm_rowscale_ws(reinterpret_cast<const int8_t*>(base + w.codes), K,
-                               reinterpret_cast<const float*>(base + w.scales), qw, ldw, wbits, ws, bias, bias_dtype,
-                               y, y_dtype, ldy, M, N, K, base + w.split, workspace_bytes - w.split, stream);
+    GemmArgs a;
+    WKind wk;
+    rc = rowscale_args(reinterpret_cast<const int8_t*>(base + w.codes), K, reinterpret_cast<const float*>(base + w.scales),
+                       qw, ldw, wbits, ws, bias, bias_dtype, y, y_dtype, ldy, M, N, K, base + w.split,
+                       workspace_bytes - w.split, &a, &wk);
+    if (rc) return rc == kEmpty ? MQ_OK : rc;
+    a.atile = 1;   // the codes in 16-row tiles wherever the wide kernel reads them
+    a.atile = gemm_runs_wide(a, wk, Epi::RowScale);
+    rc = quantize_into(x, x_dtype, ldx, hblock, act_bits, swiglu, MQ_Q_BYTES, a.atile, M, K, base, stream);
+    if (rc) return rc;
+    return launch_gemm(a, wk, Epi::RowScale, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

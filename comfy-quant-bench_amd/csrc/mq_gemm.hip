@@ -258,17 +258,22 @@ int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
 
 }  // namespace
 
-int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
-    if (a.M == 0 || a.N == 0) return 0;
-    // a few rows: HBM-bound, served by the dot4 kernel (activation rows staged in LDS); its parity
-    // entries (exact group partials, full-K sums) run the same kernel
-    if (a.M <= 4 && a.M * a.K <= 131072 && !(wk == WKind::I8 && epi == Epi::GroupPartials) &&
-        !(wk == WKind::U4Asym && epi == Epi::RowAcc))
-        return launch_gemv(a, wk, epi, stream);
+namespace {
+
+bool runs_gemv(const GemmArgs& a, WKind wk, Epi epi) {
+    return a.M <= 4 && a.M * a.K <= 131072 && !(wk == WKind::I8 && epi == Epi::GroupPartials) &&
+           !(wk == WKind::U4Asym && epi == Epi::RowAcc);
+}
+
+}  // namespace
+
+bool gemm_runs_wide(const GemmArgs& a, WKind wk, Epi epi) {
+    if (runs_gemv(a, wk, epi)) return false;
     // The 256 x 256-tile kernel addresses each operand with 32-bit buffer offsets.
     const int64_t wbytes = wk == WKind::I8 ? a.K : a.K / 2;
     const bool fits32 = a.M * a.lda < (int64_t(1) << 31) && a.N * a.ldw < (int64_t(1) << 31) &&
-                        (a.N * a.ldws + a.K / 64) * 2 < (int64_t(1) << 31) && wbytes <= a.ldw;
+                        (a.N * a.ldws + a.K / 64) * 2 < (int64_t(1) << 31) && wbytes <= a.ldw &&
+                        (!a.atile || (a.M + 15) / 16 * 16 * a.K < (int64_t(1) << 31));
     // (activation layout 1, int4 codes scaled in the kernel, is served by the 128-tile kernel only)
     // the wide kernel loads the zero-points of four groups as one 2-byte word and two groups'
     // scales as one dword per weight row
@@ -277,7 +282,19 @@ int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
         (epi != Epi::GroupScale || (a.ldws % 2 == 0 && reinterpret_cast<uintptr_t>(a.ws16) % 4 == 0));
     // (K >= 192: the wide kernel's last-row load correction needs at least three K groups)
     // Weights in 16-row tiles are read by the wide kernel at every M above the GEMV's few rows.
-    if ((a.M > 128 || a.wtile) && a.K >= 192 && fits32 && zs_aligned && a.act_mode != 1) {
+    return (a.M > 128 || a.wtile) && a.K >= 192 && fits32 && zs_aligned && a.act_mode != 1;
+}
+
+int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
+    if (a.M == 0 || a.N == 0) return 0;
+    if (a.atile && !gemm_runs_wide(a, wk, epi)) {
+        set_error("gemm: activation codes in 16-row tiles are read by the wide kernel only");
+        return -2;
+    }
+    // a few rows: HBM-bound, served by the dot4 kernel (activation rows staged in LDS); its parity
+    // entries (exact group partials, full-K sums) run the same kernel
+    if (runs_gemv(a, wk, epi)) return launch_gemv(a, wk, epi, stream);
+    if (gemm_runs_wide(a, wk, epi)) {
         GemmArgs w = a;
         w.ksplit = 1;
         w.tile = 0;
@@ -289,7 +306,7 @@ int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
             if (tail > 0) {
                 GemmArgs t = w;
                 t.M = tail;
-                t.qa = a.qa + (a.M - tail) * a.lda;
+                t.qa = a.atile ? a.qa + ((a.M - tail) >> 4) * (a.K << 4) : a.qa + (a.M - tail) * a.lda;
                 t.sa = a.sa + (a.M - tail);
                 t.y = static_cast<char*>(a.y) + (a.M - tail) * a.ldy * (a.y_dtype == kDtF32 ? 4 : 2);
                 if (a.work) t.ksplit = choose_ksplit(t.M, t.N, t.K, t.work_bytes, &t.kgroups, int_sums);

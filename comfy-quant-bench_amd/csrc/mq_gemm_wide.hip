@@ -300,7 +300,10 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             if constexpr (EPI == Epi::RowScale) ep_b = a.ws32[col];
         }
     }
-    const auto ra_rs = rsrc(a.qa + m0 * a.lda, (rows_m - 1) * a.lda + a.K);
+    // activation codes in 16-row tiles (the linears' own codes): whole-line DMA rows, as for B
+    const bool at = a.atile;
+    const auto ra_rs = at ? rsrc(a.qa + (m0 >> 4) * G * 1024, static_cast<int64_t>((rows_m + 15) >> 4) * G * 1024)
+                          : rsrc(a.qa + m0 * a.lda, (rows_m - 1) * a.lda + a.K);
     // int8 weights in 16-row tiles: the K group of 16 rows is one 1 KB block, so every DMA
     // instruction reads whole 128-byte lines (rows of ldw bytes give it two halves of 16 lines)
     const bool wt = !kPacked && a.wtile;
@@ -316,7 +319,9 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     for (int h = 0; h < NH; ++h) {
         const int r = 16 * NH * wave + 16 * h + (lane >> 2);
         const int c = (lane & 3) ^ ((r >> 1) & 3);
-        dma_a[h] = r < rows_m ? static_cast<int>(r * a.lda) + c * 16 : kOob;
+        dma_a[h] = r >= rows_m ? kOob
+                   : at ? (r >> 4) * G * 1024 + (r & 15) * 64 + c * 16
+                        : static_cast<int>(r * a.lda) + c * 16;
         dma_b[h] = r >= rows_n ? kOob
                    : wt ? (r >> 4) * G * 1024 + (r & 15) * 64 + c * 16
                         : static_cast<int>(r * a.ldw) + c * 16;
@@ -367,7 +372,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
             dma16(live ? ra_rs : ra_none, smem, A_LDS + st * TILE_BYTES + dma_lds + h * 16 * TK, dma_a[h],
-                  soff(g, TK));
+                  soff(g, at ? 1024 : TK));
             if constexpr (!kPacked)
                 dma16(live ? rb_rs : rb_none, smem, B_LDS + st * TILE_BYTES + dma_lds + h * 16 * TK, dma_b[h],
                       soff(g, wt ? 1024 : TK));

@@ -84,6 +84,9 @@ struct GemmArgs {
     // int8 weights (WKind::I8) in 16-row tiles: [ceil(N / 16)][K / 64][16][64] bytes, so that a
     // 1 KB block holds one K group of 16 consecutive rows (ldw = K); 0: rows of ldw bytes
     int wtile = 0;
+    // activation codes (qa) in the same 16-row tiles, [ceil(M / 16)][K / 64][16][64] (lda = K):
+    // written so by the whole-linear entries when the wide kernel runs their product
+    int atile = 0;
 };
 
 // Output tile of the wide kernel for an M x N product (a tile code as above): 128 when 256 x 256
@@ -117,6 +120,8 @@ __host__ __device__ inline int group_shift(int act_mode, WKind wk) {
 }
 
 int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream);
+// whether launch_gemm runs these arguments' product on the wide kernel (the one that reads atile)
+bool gemm_runs_wide(const GemmArgs& a, WKind wk, Epi epi);
 
 // M <= 4 rows, GroupScale / RowScale only (mq_gemv.hip).
 int launch_gemv(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream);

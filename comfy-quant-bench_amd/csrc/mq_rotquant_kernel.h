@@ -400,7 +400,10 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
         const float r = recip_row(s);
         if (lane == 0 && wr == 0) scale[row] = s;
 
-        uint8_t* qr = q + row * ldq;
+        // ldq 0 (one code per byte only): codes in 16-row tiles [M / 16][K / 64][16][64], the
+        // operand layout of the wide GEMM's whole-line activation loads
+        const bool tiled = OUT != 2 && ldq == 0;
+        uint8_t* qr = tiled ? q + (row >> 4) * (static_cast<int64_t>(K) << 4) + (row & 15) * 64 : q + row * ldq;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             // quantization is odd-symmetric (rint and the clamp are), so negating the input of an
@@ -442,7 +445,7 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
                 *reinterpret_cast<uint2*>(qr + col / 2) = out;
             } else {
                 const uint4 out = {word[0], word[1], word[2], word[3]};
-                *reinterpret_cast<uint4*>(qr + col) = out;
+                *reinterpret_cast<uint4*>(qr + (tiled ? (col >> 6) * 1024 + (col & 63) : col)) = out;
             }
         }
     }

@@ -280,8 +280,10 @@ int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t 
  *   x       [M, K] (swiglu = 0) or gate | up [M, 2K] (swiglu = 1) of type x_dtype, stride ldx
  *   hblock  Hadamard block (0, 16, 64, 256); act_bits 8 or 4 (per-token int8 / int4 activations)
  *   weights, scales, bias, y as mq_gemm_w4_group / mq_gemm_rowscale
- *   workspace  device memory, 256-byte aligned: the codes [M, K] and scales [M] first (both
- *           required), then the split-K partials when the shape wants them and they fit;
+ *   workspace  device memory, 256-byte aligned: the codes (M rounded up to 16 rows, K bytes
+ *           each, in rows or in the 16-row tiles of MQ_W8_TILE16 wherever the product runs on the
+ *           kernel that reads those) and scales [M] first (both required), then the split-K
+ *           partials when the shape wants them and they fit;
  *           mq_linear_workspace_bytes(M, N, K) gives the size that holds all of it.
  */
 int64_t mq_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);

@@ -89,3 +89,43 @@ def test_rejects_what_the_layout_does_not_cover(gpu_device):
         ops.gemm_rowscale_acc(qa, wt, 40, 8)            # shape of another N
     with pytest.raises(ValueError, match="K >= 192"):
         _lib.call("mq_tile_weight_i8", wt.data_ptr(), 128, 16, 128, wt.data_ptr(), _lib.stream_of(wt))
+
+
+# The whole-linear entries write the activation codes in 16-row tiles wherever the wide kernel runs
+# their product (MQ_W8_TILE16's layout, for A); the same linear in two steps keeps them as rows.
+# Both give the same output bits: W8A8 (rows and tiled weights), W4A8 group scale, W4A4 group scale
+# (int4 x16 codes), including trailing rows (M = 4352, N = 12288) and split-K (M = 256, K = 12288).
+@pytest.mark.parametrize("m,n,k", [(129, 3000, 3072), (300, 2000, 512), (256, 3072, 12288), (4096, 3072, 3072),
+                                   (4352, 12288, 3072)])
+def test_w8a8_linear_matches_two_steps(gpu_device, m, n, k):
+    print(f"[tile16] w8a8 two-step M={m} N={n} K={k}", flush=True)
+    x = synth.to_bf16_tensor(synth.activations(m, k, seed=m), gpu_device)
+    gen = torch.Generator(device=gpu_device).manual_seed(k)
+    w = torch.randint(-127, 128, (n, k), generator=gen, device=gpu_device, dtype=torch.int8)
+    s = torch.rand(n, generator=gen, device=gpu_device) * 2e-4 + 3e-4
+    bias = (torch.randn(n, generator=gen, device=gpu_device) * 0.02).to(torch.bfloat16)
+    qa, sa = ops.rotate_quantize(x, 256, 8, _lib.Q_BYTES)
+    y2 = ops.gemm_rowscale(qa, sa, w, s, bias, n, 8)
+    for wl in (w, ops.tile_int8_weight(w)):
+        y1 = ops.int8_linear(x, wl, s, bias, torch.bfloat16, True, 256)
+        torch.cuda.synchronize()
+        assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 2000, 512), (4096, 3072, 3072), (4352, 12288, 3072)])
+@pytest.mark.parametrize("act_bits", [8, 4])
+def test_w4_group_linear_matches_two_steps(gpu_device, m, n, k, act_bits):
+    print(f"[tile16] w4 group two-step act{act_bits} M={m} N={n} K={k}", flush=True)
+    x = synth.to_bf16_tensor(synth.activations(m, k, seed=m + 5), gpu_device)
+    gen = torch.Generator(device=gpu_device).manual_seed(k + 1)
+    qd = torch.randint(0, 256, (n, k // 2), generator=gen, device=gpu_device, dtype=torch.uint8)
+    s16 = (torch.rand(n, k // 64, generator=gen, device=gpu_device) * 0.004 + 0.004).to(torch.float16)
+    zp = torch.randint(0, 256, (n, (k // 64 + 1) // 2), generator=gen, device=gpu_device, dtype=torch.uint8)
+    bias = (torch.randn(n, generator=gen, device=gpu_device) * 0.02).to(torch.bfloat16)
+    hb = 256 if act_bits == 8 else 64
+    y1 = ops._linear_w4_group(x, False, hb, act_bits, qd, s16, zp, bias, n, k, torch.bfloat16)
+    layout, mode = (_lib.Q_BYTES, _lib.ACT_I8) if act_bits == 8 else (_lib.Q_X16ALT, _lib.ACT_X16ALT)
+    qa, sa = ops.rotate_quantize(x, hb, act_bits, layout)
+    y2 = ops.gemm_w4_group(qa, sa, qd, s16, zp, bias, n, act_mode=mode)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))

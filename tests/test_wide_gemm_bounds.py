@@ -124,10 +124,11 @@ def test_model_catches_an_offset_past_the_range(which, t):
         _check(300, 200, 320, loads=unshifted, T=t)
 
 
-def _loads_i8(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=(256, 256), tiled=True):
+def _loads_i8(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=(256, 256), tiled=True, atiled=False):
     """The int8-weight kinds' DMA loads (A, and B through the same DMA roles): B rows of K bytes or,
     tiled, 16-row tiles [ceil(N / 16)][K / 64][16][64] whose K group of 16 rows is one 1 KB block
-    (mq_gemm_wide.hip, wt). Also checks that each tile's B resource lies inside the tiled array."""
+    (mq_gemm_wide.hip, wt); atiled: the activation codes in the same tiles (at). Also checks that
+    each tile's resources lie inside the tiled arrays."""
     TM, TN = T
     NH = TM // 128
     G = K // TK
@@ -141,6 +142,9 @@ def _loads_i8(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=(256, 256), tiled=T
         g0 = s * kgroups if slices > 1 else 0
         g1 = min(g0 + kgroups, G4) if slices > 1 else G4
         ra = (rows_m - 1) * K + K
+        if atiled:
+            ra = ((rows_m + 15) >> 4) * G * 1024
+            assert (m0 >> 4) * G * 1024 + ra <= -(-M // 16) * G * 1024
         if tiled:
             rb = ((rows_n + 15) >> 4) * G * 1024
             assert (n0 >> 4) * G * 1024 + rb <= -(-N // 16) * G * 1024
@@ -150,22 +154,24 @@ def _loads_i8(M, N, K, ldwz, ldws, kgroups=None, slices=1, T=(256, 256), tiled=T
         for h in range(NH):
             r = 16 * NH * wave + 16 * h + (lane >> 2)
             c = (lane & 3) ^ ((r >> 1) & 3)
-            dma_a.append(np.where(r < rows_m, r * K + c * 16, KOOB))
+            ta = (r >> 4) * G * 1024 + (r & 15) * 64 + c * 16 if atiled else r * K + c * 16
+            dma_a.append(np.where(r < rows_m, ta, KOOB))
             tb = (r >> 4) * G * 1024 + (r & 15) * 64 + c * 16 if tiled else r * K + c * 16
             dma_b.append(np.where(r < rows_n, tb, KOOB))
         for g in range(g0, g1):
             live = g < G
             for h in range(NH):
-                yield "A", ra if live else 0, dma_a[h], g * TK if live else 0, 16
+                yield "A", ra if live else 0, dma_a[h], (g * (1024 if atiled else TK)) if live else 0, 16
                 yield "B8", rb if live else 0, dma_b[h], (g * (1024 if tiled else TK)) if live else 0, 16
 
 
+@pytest.mark.parametrize("atiled", [True, False])
 @pytest.mark.parametrize("tiled", [True, False])
 @pytest.mark.parametrize("t", TILES)
 @pytest.mark.parametrize("m,n,k", [(257, 300, 192), (300, 256, 320), (513, 400, 3136), (5, 3000, 1024),
                                    (64, 17, 448), (1, 16, 192)])
-def test_int8_weight_dma_stays_in_range(m, n, k, t, tiled):
-    _check(m, n, k, T=t, loads=lambda *a, **kw: _loads_i8(*a, **kw, tiled=tiled))
+def test_int8_weight_dma_stays_in_range(m, n, k, t, tiled, atiled):
+    _check(m, n, k, T=t, loads=lambda *a, **kw: _loads_i8(*a, **kw, tiled=tiled, atiled=atiled))
 
 
 def test_int8_tiled_model_catches_a_wrong_band_stride():
