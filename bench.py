@@ -225,13 +225,14 @@ def kernels_child(args) -> int:
     for _ in range(3):
         ck.gemm_w4_group(qa, sa, qd.view(torch.uint8), s16, zp.view(torch.uint8), bias, n)
     if args.with_rowscale:
-        # the W8A8 row-scale GEMM of the same shape (random int8 weights, per-row scales), for
-        # counter runs that compare the two epilogues; the traffic runs leave it out
+        # the W8A8 linear of the same shape (random int8 weights in 16-row tiles, per-row scales),
+        # for profiles and counter runs that compare the two epilogues: its GEMM reads activation
+        # codes and weights in 16-row tiles, as in the config-4 stack; the traffic runs leave it out
         gen = torch.Generator(device=x.device).manual_seed(6)
         q8 = ck.tile_int8_weight(torch.randint(-127, 128, (n, k), generator=gen, device=x.device, dtype=torch.int8))
         ws = torch.rand(n, generator=gen, device=x.device) * 1e-3
-        for _ in range(3):
-            ck.gemm_rowscale(qa, sa, q8, ws, bias, n, 8)
+        for _ in range(args.rowscale_calls):
+            ck.int8_linear(x, q8, ws, bias, torch.bfloat16, True, 256)
         del q8
     x3 = synth.to_bf16_tensor(synth.activations(RQ_M, k, seed=3), x.device)
     for _ in range(3):
@@ -483,7 +484,8 @@ def main() -> int:
                     help="time every configuration's linear shapes instead (one JSON object, not the bench line)")
     ap.add_argument("--kernels-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--with-rowscale", action="store_true",
-                    help="with --kernels-child: also launch the W8A8 row-scale GEMM (counter runs)")
+                    help="with --kernels-child: also run the W8A8 linear of the same shape (profiles, counter runs)")
+    ap.add_argument("--rowscale-calls", type=int, default=3, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
