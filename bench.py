@@ -431,6 +431,8 @@ def sweep() -> dict:
     shapes += [("C2", "w4a4", m, k, n, hb) for hb in (16, 64, 256) for m in (4352, 8192) for k, n in c1_kn]
     shapes += [("C2", "w4a4", 1, 3072, 18432, hb) for hb in (16, 64, 256)]
     shapes += [("C3", "w4a8", 32760, k, n, 256) for k, n in ((3072, 9216), (3072, 14336), (14336, 3072))]
+    # config 4's W8A8 linears (image and text tokens), int8 weights held in 16-row tiles
+    shapes += [("C4", "w8a8", m, k, n, 256) for m in (4096, 256) for k, n in c1_kn]
     out = {"linears": [], "rotquant": []}
     acts: dict = {}
     for cfg, fmt, m, k, n, hb in shapes:
@@ -438,7 +440,11 @@ def sweep() -> dict:
             acts[(m, k)] = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
         x = acts[(m, k)]
         bias = (torch.randn(n, generator=gen, device=dev) * 0.1).to(torch.bfloat16)
-        if fmt == "w4a8":
+        if fmt == "w8a8":
+            q8 = ck.tile_int8_weight(torch.randint(-127, 128, (n, k), generator=gen, device=dev, dtype=torch.int8))
+            rs = torch.rand(n, generator=gen, device=dev) * 2e-4 + 3e-4
+            fn = lambda: ck.int8_linear(x, q8, rs, bias, torch.bfloat16, True, hb)  # noqa: E731
+        elif fmt == "w4a8":
             qd, s16, zp = w4a8_weights(n, k)
             fn = lambda: ck.w4a8_int8_linear(x, qd, s16, None, None, zp, bias, 64, hb, torch.bfloat16)  # noqa: E731
         else:
