@@ -278,7 +278,9 @@ __device__ __forceinline__ void quant16(const float (&v)[16], float sg, float r,
 // half starts K elements into the row) and the activation is swiglu_pair(gate, up).
 // IN: 0 = bf16 input, 1 = fp16 input (either converts exactly to fp32), 2 = fp32 input.
 // NCH: chunks per wave; W: waves per row (NCH * W * 1024 >= K).
-template <int BLK, int OUT, int NCH, int ACT, int W, int IN>
+// TL: codes in 16-row tiles (one code per byte only), chosen at compile time so that the
+// row-major store keeps its exact code
+template <int BLK, int OUT, int NCH, int ACT, int W, int IN, bool TL>
 __global__ void __launch_bounds__(64 * kWaves)
 rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
                 uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale) {
@@ -400,9 +402,9 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
         const float r = recip_row(s);
         if (lane == 0 && wr == 0) scale[row] = s;
 
-        // ldq 0 (one code per byte only): codes in 16-row tiles [M / 16][K / 64][16][64], the
-        // operand layout of the wide GEMM's whole-line activation loads
-        const bool tiled = OUT != 2 && ldq == 0;
+        // TL: codes in 16-row tiles [M / 16][K / 64][16][64], the operand layout of the wide
+        // GEMM's whole-line activation loads
+        constexpr bool tiled = TL && OUT != 2;
         uint8_t* qr = tiled ? q + (row >> 4) * (static_cast<int64_t>(K) << 4) + (row & 15) * 64 : q + row * ldq;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
@@ -467,7 +469,8 @@ int launch_rq(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, void* q, int
         int per_cu = per_cu_cache.load(std::memory_order_relaxed);
         if (per_cu <= 0) {
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &per_cu, reinterpret_cast<const void*>(&rotquant_kernel<BLK, OUT, NCH, ACT, W, IN>), 64 * kWaves,
+                    &per_cu, reinterpret_cast<const void*>(&rotquant_kernel<BLK, OUT, NCH, ACT, W, IN, false>),
+                    64 * kWaves,
                     0) != hipSuccess ||
                 per_cu <= 0)
                 per_cu = 1;
@@ -478,9 +481,15 @@ int launch_rq(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, void* q, int
         wgs = std::min<int64_t>(groups, static_cast<int64_t>(cus > 0 ? cus : 256) * per_cu);
     }
     if (wgs == 0) return 0;
-    hipLaunchKernelGGL((rotquant_kernel<BLK, OUT, NCH, ACT, W, IN>), dim3(static_cast<unsigned>(wgs)),
-                       dim3(64 * kWaves), 0, stream, x, ldx, static_cast<int>(M), static_cast<int>(K),
-                       static_cast<uint8_t*>(q), ldq, scale);
+    // a row stride of 0 asks for the codes in 16-row tiles (one code per byte)
+    if (OUT != 2 && ldq == 0)
+        hipLaunchKernelGGL((rotquant_kernel<BLK, OUT, NCH, ACT, W, IN, OUT != 2>), dim3(static_cast<unsigned>(wgs)),
+                           dim3(64 * kWaves), 0, stream, x, ldx, static_cast<int>(M), static_cast<int>(K),
+                           static_cast<uint8_t*>(q), ldq, scale);
+    else
+        hipLaunchKernelGGL((rotquant_kernel<BLK, OUT, NCH, ACT, W, IN, false>), dim3(static_cast<unsigned>(wgs)),
+                           dim3(64 * kWaves), 0, stream, x, ldx, static_cast<int>(M), static_cast<int>(K),
+                           static_cast<uint8_t*>(q), ldq, scale);
     return launch_status("rotquant");
 }
 
