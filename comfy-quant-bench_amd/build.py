@@ -19,7 +19,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "kitchen_amd", "libmq.so")
 SOURCES = ["mq_abi.hip", "mq_rotquant.hip", "mq_rotquant_f16.hip", "mq_rotquant_f32.hip", "mq_swiglu.hip",
-           "mq_swiglu_f16.hip",
+           "mq_swiglu_f16.hip", "mq_swiglu_eager.hip", "mq_swiglu_eager_f16.hip",
            "mq_codebook.hip", "mq_wquant.hip", "mq_gemv.hip", "mq_gemm.hip", "mq_gemm_wide.hip"]
 ARCH = "gfx950"
 

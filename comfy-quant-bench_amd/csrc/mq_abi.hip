@@ -156,6 +156,17 @@ int check_rotquant(const char* what, const void* x, int x_dtype, bool f32_ok, in
     return MQ_OK;
 }
 
+// The SwiGLU prologue kernels of a mode (MQ_SWIGLU_FUSED / MQ_SWIGLU_EAGER) and input type.
+int launch_swiglu(int mode, int h_dtype, const uint16_t* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
+                  int packed, void* q, int64_t ldq, float* scale, hipStream_t st) {
+    const bool f16 = h_dtype == MQ_DT_F16;
+    if (mode == MQ_SWIGLU_EAGER)
+        return f16 ? launch_swiglu_eager_rotquant_f16(h, M, K, ldh, hblock, bits, packed, q, ldq, scale, st)
+                   : launch_swiglu_eager_rotquant_bf16(h, M, K, ldh, hblock, bits, packed, q, ldq, scale, st);
+    return f16 ? launch_swiglu_rotquant_f16(h, M, K, ldh, hblock, bits, packed, q, ldq, scale, st)
+               : launch_swiglu_rotquant_bf16(h, M, K, ldh, hblock, bits, packed, q, ldq, scale, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -174,16 +185,15 @@ int mq_rotquant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, i
 }
 
 int mq_swiglu_rotquant(const void* h, int h_dtype, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
-                       int packed, void* q, int64_t ldq, float* scale, void* stream) {
+                       int packed, int mode, void* q, int64_t ldq, float* scale, void* stream) {
     clear_error();
+    MQ_REQUIRE(mode == MQ_SWIGLU_FUSED || mode == MQ_SWIGLU_EAGER,
+               "swiglu_rotquant: mode must be MQ_SWIGLU_FUSED (1) or MQ_SWIGLU_EAGER (2), got %d", mode);
     const int rc =
         check_rotquant("swiglu_rotquant", h, h_dtype, false, M, K, 2 * K, ldh, hblock, bits, packed, q, ldq, scale);
     if (rc != MQ_OK || M == 0) return rc;
-    auto* hs = static_cast<const uint16_t*>(h);
-    auto* st = static_cast<hipStream_t>(stream);
-    return h_dtype == MQ_DT_F16
-               ? launch_swiglu_rotquant_f16(hs, M, K, ldh, hblock, bits, packed, q, ldq, scale, st)
-               : launch_swiglu_rotquant_bf16(hs, M, K, ldh, hblock, bits, packed, q, ldq, scale, st);
+    return launch_swiglu(mode, h_dtype, static_cast<const uint16_t*>(h), M, K, ldh, hblock, bits, packed, q, ldq,
+                         scale, static_cast<hipStream_t>(stream));
 }
 
 int mq_decode_w4a8_codebook(const void* qdata, int64_t ldq, const void* s_rel, int64_t lds, const float* s_channel,
@@ -428,7 +438,8 @@ LinearWs linear_ws(int64_t M, int64_t N, int64_t K) {
 int check_linear(const char* what, int act_bits, int swiglu, int64_t M, int64_t N, int64_t K, const void* workspace,
                  int64_t workspace_bytes) {
     MQ_REQUIRE(act_bits == 8 || act_bits == 4, "%s: act_bits must be 8 or 4 (got %d)", what, act_bits);
-    MQ_REQUIRE(swiglu == 0 || swiglu == 1, "%s: swiglu must be 0 or 1 (got %d)", what, swiglu);
+    MQ_REQUIRE(swiglu == MQ_SWIGLU_NONE || swiglu == MQ_SWIGLU_FUSED || swiglu == MQ_SWIGLU_EAGER,
+               "%s: swiglu must be 0 (none), 1 (fused) or 2 (eager), got %d", what, swiglu);
     MQ_REQUIRE(M >= 0 && N >= 0 && K > 0 && K % 64 == 0, "%s: bad shape M=%lld N=%lld K=%lld (K %% 64 == 0)", what,
                (long long)M, (long long)N, (long long)K);
     MQ_REQUIRE(M < (int64_t(1) << 31), "%s: M too large", what);
@@ -449,7 +460,7 @@ int quantize_into(const void* x, int x_dtype, int64_t ldx, int hblock, int act_b
     void* q = ws_base + w.codes;
     float* s = reinterpret_cast<float*>(ws_base + w.scales);
     if (!tiled)
-        return swiglu ? mq_swiglu_rotquant(x, x_dtype, M, K, ldx, hblock, act_bits, layout, q, K, s, stream)
+        return swiglu ? mq_swiglu_rotquant(x, x_dtype, M, K, ldx, hblock, act_bits, layout, swiglu, q, K, s, stream)
                       : mq_rotquant(x, x_dtype, M, K, ldx, hblock, act_bits, layout, q, K, s, stream);
     const int rc = swiglu ? check_rotquant("swiglu_rotquant", x, x_dtype, false, M, K, 2 * K, ldx, hblock, act_bits,
                                            layout, q, K, s)
@@ -458,9 +469,7 @@ int quantize_into(const void* x, int x_dtype, int64_t ldx, int hblock, int act_b
     if (rc != MQ_OK) return rc;
     auto* xs = static_cast<const uint16_t*>(x);
     auto* st = static_cast<hipStream_t>(stream);
-    if (swiglu)
-        return x_dtype == MQ_DT_F16 ? launch_swiglu_rotquant_f16(xs, M, K, ldx, hblock, act_bits, layout, q, 0, s, st)
-                                    : launch_swiglu_rotquant_bf16(xs, M, K, ldx, hblock, act_bits, layout, q, 0, s, st);
+    if (swiglu) return launch_swiglu(swiglu, x_dtype, xs, M, K, ldx, hblock, act_bits, layout, q, 0, s, st);
     if (x_dtype == MQ_DT_F32)
         return launch_rotquant_f32(static_cast<const float*>(x), M, K, ldx, hblock, act_bits, layout, q, 0, s, st);
     return x_dtype == MQ_DT_F16 ? launch_rotquant_f16(xs, M, K, ldx, hblock, act_bits, layout, q, 0, s, st)

@@ -1,17 +1,18 @@
 // Load-time decode of comfy-kitchen's shipped asym_w4a8_int8 weights (4-bit codebook indices,
-// fp8 e4m3fn per-group scales s_rel, per-row s_channel) to an int8 weight with a per-row scale,
-// the form the int8 row-scale GEMM takes (patches/comfy_kitchen_w4a8_dequant_fused.patch:12-15:
-// "Decoded W4A8 is a ConvRot INT8 weight with a per-row scale").
+// fp8 e4m3fn per-group scales s_rel, per-row s_channel) to an int8 weight whose per-row scale is
+// the stored s_channel, the form the int8 row-scale GEMM takes. comfy-kitchen finishes a decoded
+// W4A8 weight as dequantize_int8_convrot_weight_dtype(int8_weight, s_channel, ...)
+// (patches/comfy_kitchen_w4a8_dequant_fused.patch:15-18): the int8 weight's row scale is s_channel
+// unchanged, so level * s_rel is already in int8 units and
 //
 //   t[n,k]  = fp32(level(code[n,k]) * fp8(s_rel[n, k / gs]))   level = codebook[code], or the
 //                                                               signed nibble without a codebook
-//   s[n]    = fp32(max_k |t[n,k]| / 127)
-//   q8[n,k] = clamp(rne(t[n,k] / s[n]), -127, 127)  (IEEE division; 0 for an all-zero row)
-//   row_scale[n] = fp32(s[n] * s_channel[n])
+//   q8[n,k] = clamp(rne(t[n,k]), -127, 127)                     (0 where t is NaN)
+//   row_scale[n] = s_channel[n]
 //
-// One 256-thread workgroup per weight row, two passes over the row (absmax, then codes); each
-// thread takes 8 consecutive k per step (one dword of packed codes in, 8 bytes out). The decode
-// runs once per weight; it is HBM-bound at 1.5 bytes per weight element.
+// One 256-thread workgroup per weight row, one pass; each thread takes 8 consecutive k per step
+// (one dword of packed codes in, 8 bytes out). The decode runs once per weight; it is HBM-bound
+// at 1.5 bytes per weight element.
 #include "mq_device.h"
 #include "mq_internal.h"
 
@@ -37,44 +38,23 @@ decode_kernel(const uint8_t* __restrict__ qdata, int64_t ldq, const uint8_t* __r
               const float* __restrict__ s_channel, const float* __restrict__ codebook, int gs, int K,
               int8_t* __restrict__ q8, int64_t ldq8, float* __restrict__ row_scale) {
     __shared__ float lev[16];
-    __shared__ float red[kThreads / 64];
     const int64_t row = blockIdx.x;
     const int tid = threadIdx.x;
     if (tid < 16) lev[tid] = codebook ? codebook[tid] : static_cast<float>(tid >= 8 ? tid - 16 : tid);
+    if (tid == 0) row_scale[row] = s_channel[row];
     __syncthreads();
     const uint8_t* qr = qdata + row * ldq;
     const uint8_t* sr = s_rel + row * lds;
-
-    auto element = [&](uint32_t w, int k0, int i) {
-        return lev[(w >> (4 * i)) & 0xfu] * fp8_e4m3fn(sr[(k0 + i) / gs]);
-    };
-
-    float am = 0.0f;
-    for (int k0 = tid * 8; k0 < K; k0 += kThreads * 8) {
-        const uint32_t w = *reinterpret_cast<const uint32_t*>(qr + k0 / 2);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) am = __builtin_fmaxf(am, __builtin_fabsf(element(w, k0, i)));
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) am = __builtin_fmaxf(am, __shfl_xor(am, o, 64));
-    if ((tid & 63) == 0) red[tid >> 6] = am;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kThreads / 64; ++i) am = __builtin_fmaxf(am, red[i]);
-
-    const float s = am / 127.0f;
-    if (tid == 0) row_scale[row] = s * s_channel[row];
     int8_t* out = q8 + row * ldq8;
     for (int k0 = tid * 8; k0 < K; k0 += kThreads * 8) {
         const uint32_t w = *reinterpret_cast<const uint32_t*>(qr + k0 / 2);
         uint32_t lo = 0, hi = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            float q = 0.0f;
-            if (s != 0.0f) {
-                q = __builtin_rintf(element(w, k0, i) / s);
-                q = __builtin_fminf(__builtin_fmaxf(q, -127.0f), 127.0f);
-            }
+            const float t = lev[(w >> (4 * i)) & 0xfu] * fp8_e4m3fn(sr[(k0 + i) / gs]);
+            float q = __builtin_rintf(t);
+            q = __builtin_fminf(__builtin_fmaxf(q, -127.0f), 127.0f);
+            if (t != t) q = 0.0f;
             const uint32_t byte = static_cast<uint32_t>(static_cast<int>(q)) & 0xffu;
             if (i < 4) lo |= byte << (8 * i);
             else hi |= byte << (8 * (i - 4));

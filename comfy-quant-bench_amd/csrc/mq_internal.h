@@ -29,11 +29,16 @@ int launch_rotquant_f16(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, in
 int launch_rotquant_f32(const float* x, int64_t M, int64_t K, int64_t ldx, int hblock, int bits,
                         int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
 
-// --- SwiGLU prologue + rotate + quantize (mq_swiglu*.hip); h holds gate | up, K columns each
+// --- SwiGLU prologue + rotate + quantize (mq_swiglu*.hip); h holds gate | up, K columns each.
+// The fused activation T(silu(g) * u) rounds once; the eager one T(T(silu(g)) * u) twice.
 int launch_swiglu_rotquant_bf16(const uint16_t* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
                                 int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
 int launch_swiglu_rotquant_f16(const uint16_t* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
                                int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
+int launch_swiglu_eager_rotquant_bf16(const uint16_t* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
+                                      int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
+int launch_swiglu_eager_rotquant_f16(const uint16_t* h, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
+                                     int packed, void* q, int64_t ldq, float* scale, hipStream_t stream);
 
 // --- load-time decode of the shipped asym_w4a8_int8 codebook weights (mq_codebook.hip)
 int launch_decode_w4a8_codebook(const uint8_t* qdata, int64_t ldq, const uint8_t* s_rel, int64_t lds,

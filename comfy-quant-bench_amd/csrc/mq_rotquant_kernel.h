@@ -80,9 +80,19 @@ __device__ __forceinline__ float silu_f32(uint32_t b, float g, const float* tab)
 }
 
 // Two activations from one dword of gates and one of ups (two bf16 each), as bf16-valued floats.
+// EAGER = false: bf16(silu(g) * u), one rounding (the fused quantizer). EAGER = true: silu(g) is
+// rounded to bf16 first and the product (exact in fp32: two 8-bit significands) then rounded again,
+// bf16(bf16(silu(g)) * u): the eager torch path silu(gate).mul_(up) in bf16.
+template <bool EAGER>
 __device__ __forceinline__ void swiglu_pair(uint32_t wg, uint32_t wu, const float* tab, float& a0, float& a1) {
-    const float p0 = silu_f32(wg & 0xffffu, bf16lo(wg), tab) * bf16lo(wu);
-    const float p1 = silu_f32(wg >> 16, bf16hi(wg), tab) * bf16hi(wu);
+    float s0 = silu_f32(wg & 0xffffu, bf16lo(wg), tab), s1 = silu_f32(wg >> 16, bf16hi(wg), tab);
+    if constexpr (EAGER) {
+        const uint32_t sh = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{s0, s1}, bf16x2));
+        s0 = __uint_as_float(sh << 16);
+        s1 = __uint_as_float(sh & 0xffff0000u);
+    }
+    const float p0 = s0 * bf16lo(wu);
+    const float p1 = s1 * bf16hi(wu);
     const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{p0, p1}, bf16x2));
     a0 = __uint_as_float(h << 16);
     a1 = __uint_as_float(h & 0xffff0000u);
@@ -91,10 +101,18 @@ __device__ __forceinline__ void swiglu_pair(uint32_t wg, uint32_t wu, const floa
 __device__ __forceinline__ float f16lo(uint32_t w) { return f16_bits_to_f32(static_cast<uint16_t>(w & 0xffffu)); }
 __device__ __forceinline__ float f16hi(uint32_t w) { return f16_bits_to_f32(static_cast<uint16_t>(w >> 16)); }
 
-// fp16 inputs: silu of both gates from the global fp16 table, the products rounded to fp16.
+// fp16 inputs: silu of both gates from the global fp16 table, the products rounded to fp16 (EAGER:
+// silu(g) rounded to fp16 first; the product of two 11-bit significands is exact in fp32).
+template <bool EAGER>
 __device__ __forceinline__ void swiglu_pair_f16(uint32_t wg, uint32_t wu, const uint32_t* tab, float& a0, float& a1) {
-    const float p0 = __uint_as_float(tab[wg & 0xffffu]) * f16lo(wu);
-    const float p1 = __uint_as_float(tab[wg >> 16]) * f16hi(wu);
+    float s0 = __uint_as_float(tab[wg & 0xffffu]), s1 = __uint_as_float(tab[wg >> 16]);
+    if constexpr (EAGER) {
+        const uint32_t sh = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{s0, s1}, f16x2));
+        s0 = f16lo(sh);
+        s1 = f16hi(sh);
+    }
+    const float p0 = s0 * f16lo(wu);
+    const float p1 = s1 * f16hi(wu);
     const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{p0, p1}, f16x2));
     a0 = f16lo(h);
     a1 = f16hi(h);
@@ -275,7 +293,8 @@ __device__ __forceinline__ void quant16(const float (&v)[16], float sg, float r,
 //      3 = int4 codes one per byte as 16 * q, negated in odd 64-column groups (the operand layout
 //          the group-scale GEMM takes for int4 activations: exact, and 16x finer in its fp32 step).
 // ACT: 0 = x is the activation itself; 1 = x holds gate | up halves of K columns each (the up
-// half starts K elements into the row) and the activation is swiglu_pair(gate, up).
+// half starts K elements into the row) and the activation is swiglu_pair(gate, up) rounded once;
+// 2 = the same with the eager path's two roundings (swiglu_pair<true>).
 // IN: 0 = bf16 input, 1 = fp16 input (either converts exactly to fp32), 2 = fp32 input.
 // NCH: chunks per wave; W: waves per row (NCH * W * 1024 >= K).
 // TL: codes in 16-row tiles (one code per byte only), chosen at compile time so that the
@@ -303,8 +322,8 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
     }
     [[maybe_unused]] const float* tab = nullptr;
     [[maybe_unused]] const uint32_t* tab16 = nullptr;
-    if constexpr (ACT == 1 && IN == 1) tab16 = SiluF16Table<IN>::get();
-    if constexpr (ACT == 1 && IN == 0) {
+    if constexpr (ACT >= 1 && IN == 1) tab16 = SiluF16Table<IN>::get();
+    if constexpr (ACT >= 1 && IN == 0) {
         __shared__ __attribute__((aligned(16))) uint32_t silu_lds[2 * kSiluEntries];
         for (uint32_t i = threadIdx.x; i < 2 * kSiluEntries / 4; i += 64 * kWaves)
             reinterpret_cast<uint4*>(silu_lds)[i] = reinterpret_cast<const uint4*>(kSiluTable)[i];
@@ -360,14 +379,14 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
             const uint4 a = *reinterpret_cast<const uint4*>(xr + e);
             const uint4 b = *reinterpret_cast<const uint4*>(xr + e + 8);
             const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-            if constexpr (ACT == 1) {
+            if constexpr (ACT >= 1) {
                 const uint4 ua = *reinterpret_cast<const uint4*>(xr + K + e);
                 const uint4 ub = *reinterpret_cast<const uint4*>(xr + K + e + 8);
                 const uint32_t wu[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    if constexpr (IN == 1) swiglu_pair_f16(w[j], wu[j], tab16, v[c][2 * j], v[c][2 * j + 1]);
-                    else swiglu_pair(w[j], wu[j], tab, v[c][2 * j], v[c][2 * j + 1]);
+                    if constexpr (IN == 1) swiglu_pair_f16<ACT == 2>(w[j], wu[j], tab16, v[c][2 * j], v[c][2 * j + 1]);
+                    else swiglu_pair<ACT == 2>(w[j], wu[j], tab, v[c][2 * j], v[c][2 * j + 1]);
                 }
             } else {
 #pragma unroll
@@ -460,7 +479,7 @@ int launch_rq(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, void* q, int
     // plain inputs: one workgroup per row group; SwiGLU: a grid-stride loop over the row groups,
     // so each workgroup stages the LDS table once for many rows
     int64_t wgs = groups;
-    if constexpr (ACT == 1 && IN == 0) {
+    if constexpr (ACT >= 1 && IN == 0) {
         // as many workgroups as are resident at once (the same number on every CU), each
         // striding over the row groups
         // resident workgroups per CU of this instantiation: queried once (every device this

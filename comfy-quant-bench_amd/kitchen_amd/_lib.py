@@ -11,7 +11,7 @@ import os
 
 import torch  # noqa: F401  (must be imported before the library is loaded)
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmq.so")
 
@@ -25,7 +25,8 @@ _SIGNATURES = {
     "mq_abi_version": ([], c_int),
     "mq_last_error": ([], ctypes.c_char_p),
     "mq_rotquant": ([c_vp, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_vp], c_int),
-    "mq_swiglu_rotquant": ([c_vp, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_vp], c_int),
+    "mq_swiglu_rotquant": ([c_vp, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_vp],
+                           c_int),
     "mq_decode_w4a8_codebook": ([c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_int, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp],
                                 c_int),
     "mq_quantize_weight": ([c_vp, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp],
@@ -56,6 +57,7 @@ EXPORTED = tuple(_SIGNATURES)
 
 # code layouts (include/mq.h)
 Q_BYTES, Q_PACKED, Q_X16ALT = 0, 1, 2
+SWIGLU_NONE, SWIGLU_FUSED, SWIGLU_EAGER = 0, 1, 2
 W8_TILE16 = 0x100            # wbits flag: int8 weights in 16-row tiles (include/mq.h)
 ACT_I8, ACT_I4, ACT_X16ALT = 0, 1, 2
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2

@@ -13,6 +13,17 @@ dataclass over comfy-kitchen's `BaseLayoutParams`, `quantize` / `dequantize`,
 (`ops.w4a8_int8_linear` / `ops.convrot_w4a4_linear`); `dequantize` rebuilds the float weight
 (used by ComfyUI for LoRA merges and full-precision fallbacks).
 
+How a linear reaches the kernels. ComfyUI's `quant_ops` imports comfy-kitchen's
+`register_layout_op` (`patches/comfyui_awq_w4a16_format.patch:54`), the hook through which a
+layout supplies its own handler for a torch op on a QuantizedTensor weight; a layout without one
+is dequantized to a float weight and multiplied by a plain matmul. `register()` therefore
+registers an `aten.linear.default` handler for each layout whenever `register_layout_op` is
+present: `handler(func, args, kwargs)` takes (input, weight, bias) and runs the layout's
+`linear` on the GPU (falling back to dequantize + `F.linear` for host tensors). The decorator's
+exact signature is not in the reference tree (comfy-kitchen is absent); the form used is
+`register_layout_op(torch_op, layout_cls)(handler)`. Without `register_layout_op` ComfyUI runs these
+formats through `dequantize`.
+
 comfy and comfy_kitchen are not imported at module load: `register()` imports them (or takes
 stand-ins, as the CPU tests do) when a ComfyUI process calls it.
 """
@@ -193,6 +204,28 @@ def make_layout_classes(quantized_layout, base_params) -> dict:
     return {W4A8_LAYOUT: W4A8AsymG64Layout, W4A4_LAYOUT: W4A4SymG64Layout}
 
 
+def _use_kernels(x: torch.Tensor, qdata: torch.Tensor) -> bool:
+    return x.is_cuda and qdata.is_cuda and x.dtype in ops.FLOAT_TYPES
+
+
+def make_linear_handler(layout_cls):
+    """The aten.linear.default handler of a layout: `handler(func, args, kwargs)` with args
+    (input, QuantizedTensor weight[, bias]); the weight carries `_qdata` and `_params`."""
+
+    def handler(func, args, kwargs):
+        kwargs = kwargs or {}
+        x, w = args[0], args[1]
+        bias = args[2] if len(args) > 2 else kwargs.get("bias")
+        qdata, params = w._qdata, w._params
+        if _use_kernels(x, qdata):
+            return layout_cls.linear(x, qdata, params, bias)
+        wf = layout_cls.dequantize(qdata, params).to(device=x.device, dtype=x.dtype)
+        return torch.nn.functional.linear(x, wf, None if bias is None else bias.to(x.dtype))
+
+    handler.__name__ = f"{layout_cls.__name__}_linear"
+    return handler
+
+
 def register(quant_ops=None, kitchen_base=None) -> dict:
     """Register both layouts and QUANT_ALGOS entries with ComfyUI (idempotent). `quant_ops` is
     `comfy.quant_ops` and `kitchen_base` `comfy_kitchen.tensor.base`; both are imported when not
@@ -205,10 +238,16 @@ def register(quant_ops=None, kitchen_base=None) -> dict:
     if existing is not None:
         return dict(existing)
     classes = make_layout_classes(kitchen_base.QuantizedLayout, kitchen_base.BaseLayoutParams)
+    layout_op = getattr(quant_ops, "register_layout_op", None)
     for name, cls in classes.items():
         quant_ops.register_layout_class(name, cls)
+        if layout_op is not None:
+            layout_op(torch.ops.aten.linear.default, cls)(make_linear_handler(cls))
     for fmt, entry in QUANT_ALGO_ENTRIES.items():
         quant_ops.QUANT_ALGOS[fmt] = dict(entry)
     quant_ops._kitchen_amd_layouts = classes
+    if layout_op is None:
+        logging.warning("kitchen_amd: comfy.quant_ops has no register_layout_op; %s layers will be "
+                        "dequantized and run through a plain matmul", ", ".join(QUANT_ALGO_ENTRIES))
     logging.info("kitchen_amd: registered %s with ComfyUI", ", ".join(QUANT_ALGO_ENTRIES))
     return dict(classes)

@@ -15,8 +15,15 @@ Names, keyword arguments and error messages follow the reference's contract:
       tools/ck_swiglu/swiglu_quant.cu:111-120 (h = gate | up [M, 2K])
 input_act="swiglu" takes x as the [gate | up] pair and folds silu(gate) * up into the activation
 quantizer (patches/comfy_kitchen_swiglu_w4a4_fused.patch:17-33,60-63;
-patches/comfyui_swiglu_triton_env.patch:65-97), for every convrot group size and both activation
-widths; other activations of ComfyUI's INPUT_ACT_EAGER table ("gelu_tanh",
+patches/comfyui_swiglu_triton_env.patch:65-97). The activation is rounded to x's type as the
+reference rounds it: once (the fused quantizer) where comfy-kitchen fuses, i.e. convrot_w4a4_linear
+with linear_dtype="int4", convrot_groupsize=256 and bf16 / fp16 input
+(patches/comfy_kitchen_swiglu_w4a4_fused.patch:25-31), and in int8_linear (ComfyUI folds the
+activation into the INT8 quantizer, patches/comfyui_swiglu_triton_env.patch:24,97-99; that
+kernel's rounding is not in the reference tree); twice (silu(gate).mul_(up) in x's type,
+patches/comfyui_swiglu_triton_env.patch:16-20) everywhere else convrot_w4a4_linear would apply it
+eagerly (patches/comfy_kitchen_swiglu_w4a4_fused.patch:60-64), still inside the quantizer kernel;
+other activations of ComfyUI's INPUT_ACT_EAGER table ("gelu_tanh",
 patches/comfyui_swiglu_triton_env.patch:54-56) are applied eagerly first, as comfy-kitchen's
 fallback `x = _apply_input_act(x, input_act)` does (patches/comfy_kitchen_swiglu_w4a4_fused.patch:60-64).
 Activations are taken in their own type (bf16, fp16 or fp32: the rotation runs in fp32 from the
@@ -81,30 +88,38 @@ def _swiglu_eager(h: torch.Tensor) -> torch.Tensor:
 
 
 def rotate_quantize(x: torch.Tensor, convrot_groupsize: int | None, bits: int, packed: bool | int = False,
-                    swiglu: bool = False):
+                    swiglu: bool | int = False):
     """Rotate x [.., K] by H_cg per block and quantize per token to int8 (bits 8) or int4 (bits 4).
 
     x: bfloat16, float16 or float32 (rotated in fp32 from its exact value).
     packed: False / Q_BYTES one code per byte, True / Q_PACKED packed int4 [M, K/2], Q_X16ALT the
     group GEMM's int4 operand layout (16 * q, negated in odd 64-column groups).
-    swiglu: x is [.., 2K] = gate | up and the quantized activation is silu(gate) * up rounded to x's
-    type (fused for bf16 / fp16; fp32 gate | up pairs are formed eagerly in fp32 first, as the
-    reference's quantizer takes bf16 or fp16 only).
+    swiglu: x is [.., 2K] = gate | up and the quantized activation is silu(gate) * up in x's type,
+    rounded once (True / SWIGLU_FUSED: the fused quantizer) or twice (SWIGLU_EAGER:
+    silu(gate).mul_(up)); bf16 / fp16 pairs are formed inside the kernel, fp32 pairs eagerly in fp32
+    first (the reference's quantizer takes bf16 or fp16 only).
     Returns (q, scale): q int8 [M, K] or [M, K/2], scale float32 [M]."""
     layout = int(packed)
+    mode = int(swiglu)
+    if mode not in (_lib.SWIGLU_NONE, _lib.SWIGLU_FUSED, _lib.SWIGLU_EAGER):
+        raise ValueError(f"swiglu must be False, True / SWIGLU_FUSED or SWIGLU_EAGER, got {swiglu!r}")
     width = x.shape[-1]
-    if swiglu and width % 2:
+    if mode and width % 2:
         raise ValueError("h must hold gate | up halves")
-    if swiglu and x.dtype == torch.float32:
-        x, swiglu, width = _swiglu_eager(x), False, width // 2
-    k = width // 2 if swiglu else width
+    if mode and x.dtype == torch.float32:
+        x, mode, width = _swiglu_eager(x), _lib.SWIGLU_NONE, width // 2
+    k = width // 2 if mode else width
     x2 = _as_2d(x, width)
     m = x2.shape[0]
     q = torch.empty((m, k // 2 if layout == _lib.Q_PACKED else k), dtype=torch.int8, device=x2.device)
     s = torch.empty((m,), dtype=torch.float32, device=x2.device)
-    _lib.call("mq_swiglu_rotquant" if swiglu else "mq_rotquant", x2.data_ptr(), _lib.dtype_code(x2.dtype), m, k,
-              width, int(convrot_groupsize or 0), int(bits), layout, q.data_ptr(), q.stride(0), s.data_ptr(),
-              _lib.stream_of(x2))
+    if mode:
+        _lib.call("mq_swiglu_rotquant", x2.data_ptr(), _lib.dtype_code(x2.dtype), m, k, width,
+                  int(convrot_groupsize or 0), int(bits), layout, mode, q.data_ptr(), q.stride(0), s.data_ptr(),
+                  _lib.stream_of(x2))
+    else:
+        _lib.call("mq_rotquant", x2.data_ptr(), _lib.dtype_code(x2.dtype), m, k, width, int(convrot_groupsize or 0),
+                  int(bits), layout, q.data_ptr(), q.stride(0), s.data_ptr(), _lib.stream_of(x2))
     return q, s
 
 
@@ -112,16 +127,26 @@ INPUT_ACTS = ("swiglu", "gelu_tanh")
 
 
 def _input_act(x: torch.Tensor, input_act: str | None):
-    """(x for the quantizer, fused SwiGLU?): "swiglu" folds into the quantizer; "gelu_tanh" is applied
-    eagerly in x's type (ComfyUI's INPUT_ACT_EAGER entry, patches/comfyui_swiglu_triton_env.patch:54-56)
+    """(x for the quantizer, SwiGLU mode): "swiglu" folds into the quantizer (SWIGLU_FUSED; callers
+    outside the reference's fused domain switch it to SWIGLU_EAGER); "gelu_tanh" is applied eagerly
+    in x's type (ComfyUI's INPUT_ACT_EAGER entry, patches/comfyui_swiglu_triton_env.patch:54-56)
     before quantizing, the way comfy-kitchen falls back for activations it does not fuse."""
     if input_act is None:
-        return x, False
+        return x, _lib.SWIGLU_NONE
     if input_act == "swiglu":
-        return x, True
+        return x, _lib.SWIGLU_FUSED
     if input_act == "gelu_tanh":
-        return torch.nn.functional.gelu(x, approximate="tanh"), False
+        return torch.nn.functional.gelu(x, approximate="tanh"), _lib.SWIGLU_NONE
     raise ValueError(f"unknown input_act {input_act!r}: expected one of {INPUT_ACTS} or None")
+
+
+def _swiglu_fused_domain(x: torch.Tensor, convrot_groupsize, linear_dtype: str) -> bool:
+    """Whether comfy-kitchen's convrot_w4a4_linear fuses input_act="swiglu" into its quantizer
+    (one rounding): int4 activations, convrot group 256, bf16 / fp16 input, K % 256 == 0 and
+    K <= 16384 (patches/comfy_kitchen_swiglu_w4a4_fused.patch:25-31)."""
+    k = x.shape[-1] // 2
+    return (linear_dtype == "int4" and convrot_groupsize == 256 and x.dtype in (torch.bfloat16, torch.float16)
+            and k % 256 == 0 and k <= 16384)
 
 
 def quantize_int4_rowwise_convrot64(x: torch.Tensor, convrot_groupsize: int = 256):
@@ -352,6 +377,8 @@ def convrot_w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.T
         raise ValueError(f"int4 MMA kernel requires quant_group_size {INT4_GROUP_SIZE}")
     x_out = x
     x, swiglu = _input_act(x, input_act)
+    if swiglu and not _swiglu_fused_domain(x, convrot_groupsize, linear_dtype):
+        swiglu = _lib.SWIGLU_EAGER           # comfy-kitchen's eager fallback: two roundings
     k = x.shape[-1] // 2 if swiglu else x.shape[-1]
     if k != qweight.shape[-1] * 2:
         raise ValueError(f"Input K={k} does not match qweight K={qweight.shape[-1] * 2}")
@@ -373,11 +400,11 @@ def convrot_w4a4_linear(x: torch.Tensor, qweight: torch.Tensor, wscales: torch.T
     return _finish(y, x_out, n)
 
 
-def _linear_input(x: torch.Tensor, swiglu: bool, k: int):
-    """(x as [M, width] for the whole-linear entry points, fused SwiGLU?): fp32 gate | up pairs are
-    formed eagerly (the fused prologue takes bf16 / fp16, as the reference's does)."""
+def _linear_input(x: torch.Tensor, swiglu: int, k: int):
+    """(x as [M, width] for the whole-linear entry points, SwiGLU mode): fp32 gate | up pairs are
+    formed eagerly (the SwiGLU prologue takes bf16 / fp16, as the reference's does)."""
     if swiglu and x.dtype == torch.float32:
-        x, swiglu = _swiglu_eager(x), False
+        x, swiglu = _swiglu_eager(x), _lib.SWIGLU_NONE
     x2 = _as_2d(x, 2 * k if swiglu else k)
     return x2, swiglu
 

@@ -52,20 +52,27 @@ MMDIT_LINEARS = (  # (name, K, N) of the 7 linear types of one stream of one dua
 MMDIT_TOKENS = {"image": 4096, "text": 256}
 
 
+def w4a4_count(linears: int, w4a4_frac: float = 0.35) -> int:
+    """W4A4 linears of a stack of `linears`: w4a4_frac of them, rounded half up (294 of 840)."""
+    return int(linears * w4a4_frac + 0.5)
+
+
 def mmdit_linear_stack(blocks: int = 60, w4a4_frac: float = 0.35, seed: int = 4, device="cuda"):
     """The linear stack of BASELINE config 4: `blocks` dual-stream MMDiT blocks (hidden 3072,
     MLP ratio 4), 7 linear types per stream (q, k, v, out, mlp up, mlp down, adaLN modulation at
-    M = 1), image M = 4096 and text M = 256. A seeded Bernoulli draw puts each linear on W4A4
-    (int4 per-token activations after H_64, int4 symmetric group-64 fp16-scale weights) with
-    probability w4a4_frac, the rest on W8A8 (int8 per-row weights, int8 per-token activations
-    after H_256). Weights are random-init directly in the quantized domain (random codes,
+    M = 1), image M = 4096 and text M = 256. Exactly round(w4a4_frac * linears) of the linears
+    (294 of 840 at the defaults) go on W4A4 (int4 per-token activations after H_64, int4
+    symmetric group-64 fp16-scale weights), placed by a seeded permutation; the rest on W8A8
+    (int8 per-row weights, int8 per-token activations after H_256). Weights are random-init directly in the quantized domain (random codes,
     random positive scales), which is what quantizing random-init weights produces.
 
     Returns a list of dicts: {"name", "stream", "M", "K", "N", "fmt", "tensors"}."""
     from . import ops
 
     gen = torch.Generator(device="cpu").manual_seed(seed)
-    pick = torch.rand(blocks * 2 * len(MMDIT_LINEARS), generator=gen) < w4a4_frac
+    total = blocks * 2 * len(MMDIT_LINEARS)
+    pick = torch.zeros(total, dtype=torch.bool)
+    pick[torch.randperm(total, generator=gen)[:w4a4_count(total, w4a4_frac)]] = True
     dgen = torch.Generator(device=device).manual_seed(seed + 1)
     layers = []
     i = 0

@@ -3,9 +3,13 @@
  *
  * Every entry point takes raw device pointers, sizes and a hipStream_t (passed as void*),
  * enqueues its kernels on that stream and returns immediately. The caller allocates every
- * buffer; the library allocates nothing and keeps no mutable global state, so concurrent calls
- * from several threads are safe. Return value: MQ_OK (0) or a negative MQ_E* code; the message
- * of the last failure on the calling thread is returned by mq_last_error().
+ * buffer; no entry point allocates device memory. Global state: a per-device cache of the compute
+ * unit count and of kernel occupancies (filled once, read-only afterwards, guarded for concurrent
+ * first use), the thread-local error message, and the fixed per-device scratch array behind
+ * mq_linear_w4_group_noalloc (with the cached device address of each GPU's copy). Concurrent calls
+ * from several threads are safe, except mq_linear_w4_group_noalloc calls that overlap on one GPU:
+ * they share its scratch array and race. Return value: MQ_OK (0) or a negative MQ_E* code; the
+ * message of the last failure on the calling thread is returned by mq_last_error().
  *
  * Layout conventions (all row-major, strides in elements of the stated type):
  *   floating-point operands whose type the caller chooses (activations, bias, outputs, weights to
@@ -27,7 +31,7 @@
 extern "C" {
 #endif
 
-#define MQ_ABI_VERSION 8
+#define MQ_ABI_VERSION 9
 
 enum {
     MQ_OK = 0,
@@ -48,6 +52,14 @@ enum {
     MQ_Q_X16ALT = 2,   /* int4 codes one per byte as 16 * q, negated in odd 64-column groups (bits 4):
                           the operand layout of the group GEMMs for int4 activations (MQ_ACT_X16ALT) */
 };
+
+/* SwiGLU prologue modes (the `mode` of mq_swiglu_rotquant, the `swiglu` of the whole linears). */
+#define MQ_SWIGLU_NONE 0    /* whole linears: x is the activation itself                            */
+#define MQ_SWIGLU_FUSED 1   /* T(silu(g) * u): fp32 product rounded once to the input type T, as the */
+                            /* fused quantizer (tools/ck_swiglu/swiglu_quant.cu:56-70)               */
+#define MQ_SWIGLU_EAGER 2   /* T(T(silu(g)) * u): silu rounded to T, then the product rounded again, */
+                            /* as the eager silu(gate).mul_(up) in T                                 */
+                            /* (patches/comfyui_swiglu_triton_env.patch:16-20)                      */
 
 /* Layouts of the activation codes qa taken by the group-scale GEMMs (their `act_mode`). */
 enum {
@@ -86,27 +98,33 @@ int mq_rotquant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, i
                 void* q, int64_t ldq, float* scale, void* stream);
 
 /*
- * SwiGLU prologue fused into rotate + quantize: the activation is
- *   a[m,k] = T( silu(h[m,k]) * h[m,K+k] )      (fp32 arithmetic, one rounding to T = h_dtype)
- * formed while loading the gate | up row, then rotated and quantized exactly as mq_rotquant does
- * with x = a. The intermediate never touches memory; like the reference, the product is rounded to
- * the input's own type (bf16 or fp16, tools/ck_swiglu/swiglu_quant.cu:63-70,124-132).
+ * SwiGLU prologue fused into rotate + quantize: the activation is, by mode,
+ *   MQ_SWIGLU_FUSED  a[m,k] = T( silu(h[m,k]) * h[m,K+k] )        (fp32 product, one rounding)
+ *   MQ_SWIGLU_EAGER  a[m,k] = T( T(silu(h[m,k])) * h[m,K+k] )     (two roundings)
+ * with T = h_dtype, formed while loading the gate | up row, then rotated and quantized exactly as
+ * mq_rotquant does with x = a. The intermediate never touches memory.
  *
- * Replaces swiglu_quantize_int4_rowwise_convrot64(h) (tools/ck_swiglu/swiglu_quant.cu:23-97 and
- * :111-120, dispatched by convrot_w4a4_linear(..., input_act="swiglu") at
- * patches/comfy_kitchen_swiglu_w4a4_fused.patch:17-33) and generalises it to every Hadamard block,
- * int8 codes and the group GEMM's code layouts. silu(g) = g / (1 + exp(-g)) is taken correctly
- * rounded to fp32 (the reference uses a hardware exp approximation and an fp32 division): tables of
- * the exact results, for every bf16 gate outside the closed forms |g| < 2^-25 -> g / 2,
- * g >= 128 -> g, g <= -128 -> -0, and for every fp16 gate.
+ * FUSED replaces swiglu_quantize_int4_rowwise_convrot64(h) (tools/ck_swiglu/swiglu_quant.cu:23-97
+ * and :111-120), which rounds the fp32 product once to the input type (:63-70,124-132);
+ * comfy-kitchen takes it for convrot_w4a4_linear(..., input_act="swiglu") only with
+ * linear_dtype="int4", convrot_groupsize=256 and bf16 / fp16 input
+ * (patches/comfy_kitchen_swiglu_w4a4_fused.patch:25-31). Outside that domain it applies the
+ * activation eagerly first (:60-64), silu(gate).mul_(up) in the input's type
+ * (patches/comfyui_swiglu_triton_env.patch:16-20): EAGER reproduces those two roundings. Both modes
+ * take every Hadamard block, int8 codes and the group GEMM's code layouts. silu(g) =
+ * g / (1 + exp(-g)) is taken correctly rounded to fp32 (the reference's kernel uses a hardware exp
+ * approximation and an fp32 division; torch's silu is its own fp32 evaluation): tables of the exact
+ * results, for every bf16 gate outside the closed forms |g| < 2^-25 -> g / 2, g >= 128 -> g,
+ * g <= -128 -> -0, and for every fp16 gate.
  *
  *   h      [M, 2K] of type h_dtype (MQ_DT_BF16 or MQ_DT_F16): gate in columns [0, K), up in
  *          [K, 2K); row stride ldh >= 2K elements (ldh % 8 == 0, 16-byte aligned base)
+ *   mode   MQ_SWIGLU_FUSED or MQ_SWIGLU_EAGER
  *   other arguments as mq_rotquant (K is the width of the activation, half of h's).
  * Requires K % 16 == 0, K <= 16384, K % hblock == 0.
  */
 int mq_swiglu_rotquant(const void* h, int h_dtype, int64_t M, int64_t K, int64_t ldh, int hblock, int bits,
-                       int packed, void* q, int64_t ldq, float* scale, void* stream);
+                       int packed, int mode, void* q, int64_t ldq, float* scale, void* stream);
 
 /* Weight formats written by mq_quantize_weight. */
 #define MQ_WFMT_U4_ASYM_G64 0   /* configs' W4A8: uint4 asymmetric per 64, fp16 scale, uint4 zero   */
@@ -145,14 +163,18 @@ int mq_quantize_weight(const void* w, int dtype, int64_t N, int64_t K, int64_t l
  * Load-time decode of comfy-kitchen's shipped asym_w4a8_int8 weight (tools/_formats.py:79-125:
  * qdata I8 [N, K/2] 4-bit codes, s_rel fp8 e4m3fn stored as U8 [N, K/gs], s_channel F32 [N],
  * codebook F32 [16] or none) to an int8 weight with a per-row scale, which the int8 row-scale GEMM
- * (mq_gemm_rowscale, wbits 8) then takes; comfy-kitchen finishes the same way ("Decoded W4A8 is a
- * ConvRot INT8 weight with a per-row scale", patches/comfy_kitchen_w4a8_dequant_fused.patch:12-15).
- * comfy-kitchen's own decode rule is not in the reference tree; this one is:
+ * (mq_gemm_rowscale, wbits 8) then takes. comfy-kitchen finishes a decoded W4A8 weight the same way,
+ * as dequantize_int8_convrot_weight_dtype(int8_weight, s_channel, ...)
+ * (patches/comfy_kitchen_w4a8_dequant_fused.patch:15-18): the int8 weight's row scale is the stored
+ * s_channel, unchanged, so level * s_rel is in int8 units:
  *   level = codebook[code] (unsigned nibble, low nibble = even k), or the signed nibble if
  *           codebook is NULL
- *   t[n,k] = fp32(level * fp8(s_rel[n, k / group_size])),  s[n] = fp32(max_k |t[n,k]| / 127)
- *   q8[n,k] = clamp(rne(t[n,k] / s[n]), -127, 127)  (0 for an all-zero row)
- *   row_scale[n] = fp32(s[n] * s_channel[n])
+ *   t[n,k]  = fp32(level * fp8(s_rel[n, k / group_size]))
+ *   q8[n,k] = clamp(rne(t[n,k]), -127, 127)   (0 where t is NaN: an fp8 NaN scale byte)
+ *   row_scale[n] = s_channel[n]
+ * q8 * row_scale is then level * s_rel * s_channel to within half an int8 step wherever
+ * |t| <= 127.5. comfy-kitchen's rounding of t is not in the reference tree (round half to even is
+ * this library's choice).
  *
  *   qdata  [N, K/2] bytes, stride ldq (ldq % 4 == 0, 4-byte aligned)
  *   s_rel  [N, K/group_size] fp8 bytes, stride lds
@@ -277,7 +299,8 @@ int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t 
  * replaces int8_linear (tools/verify_w4a4.py:342-370, wbits 8) and convrot_w4a4_linear with the
  * shipped per-row F32 scale (wbits 4).
  *
- *   x       [M, K] (swiglu = 0) or gate | up [M, 2K] (swiglu = 1) of type x_dtype, stride ldx
+ *   x       [M, K] (swiglu = MQ_SWIGLU_NONE) or gate | up [M, 2K] (MQ_SWIGLU_FUSED / MQ_SWIGLU_EAGER,
+ *           the activation of mq_swiglu_rotquant in that mode) of type x_dtype, stride ldx
  *   hblock  Hadamard block (0, 16, 64, 256); act_bits 8 or 4 (per-token int8 / int4 activations)
  *   weights, scales, bias, y as mq_gemm_w4_group / mq_gemm_rowscale
  *   workspace  device memory, 256-byte aligned: the codes (M rounded up to 16 rows, K bytes
@@ -309,9 +332,13 @@ int mq_linear_rowscale(const void* x, int x_dtype, int64_t ldx, int hblock, int 
  * MQ_NOALLOC_SCRATCH_BYTES in device memory that each GPU the library runs on holds until the
  * process ends; a call whose codes and scales (about M * K + 4 * M bytes) do not fit returns
  * MQ_EINVAL, and split-K partials are used only where they fit beside them. Results equal
- * mq_linear_w4_group's. Every call on one GPU shares that GPU's array: calls that overlap on one
- * GPU (several streams or threads) race and must be serialized by the caller. Nothing in the array
- * needs to start at zero: each call writes every byte it reads.
+ * mq_linear_w4_group's bit for bit whenever mq_linear_workspace_bytes(M, N, K) <=
+ * MQ_NOALLOC_SCRATCH_BYTES (both entries then take the same split-K decision); when only the codes
+ * and scales fit, the product runs without split-K: the same codes and int32 group partials, with
+ * the fp32 group sums associated in another order (outputs can differ in the last bits). Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (several streams or threads)
+ * race and must be serialized by the caller. Nothing in the array needs to start at zero: each call
+ * writes every byte it reads.
  */
 int mq_linear_w4_group_noalloc(const void* x, int x_dtype, int64_t ldx, int hblock, int act_bits, int swiglu,
                                const uint8_t* qw, int64_t ldw, const uint16_t* ws, int64_t ldws, const uint8_t* wz,

@@ -9,21 +9,22 @@ Tensors per Linear (`tools/_formats.py:79-125`, `tools/quant_w4a8.py:8-13`, head
     s_rel      U8  [N, K/gs]  fp8 e4m3fn per-group scale stored as raw bytes
     s_channel  F32 [N]        per-row scale
     codebook   F32 [16]       Lloyd-Max levels (absent under --no-codebook)
-comfy-kitchen decodes this to "a ConvRot INT8 weight with a per-row scale"
-(`patches/comfy_kitchen_w4a8_dequant_fused.patch:12-15`); the int8 GEMM then runs against int8
-per-token activations. comfy-kitchen's decode rule itself is not in the reference tree (the package
-is absent and not vendored), so this build states its own, from the tensor meanings above:
+comfy-kitchen finishes a decoded W4A8 weight as
+`dequantize_int8_convrot_weight_dtype(int8_weight, s_channel, ...)`
+(`patches/comfy_kitchen_w4a8_dequant_fused.patch:15-18`): the decoded int8 weight is paired with the
+stored `s_channel` as its per-row scale, unchanged, so `level * s_rel` is already in int8 units:
 
     level[n, k] = codebook[code]            (code = unsigned nibble)      with a codebook
                 = code as signed int4       (v >= 8 -> v - 16)            without
     t[n, k]     = fp32(level * fp8(s_rel[n, k / gs]))
-    a[n]        = max_k |t[n, k]|;  s[n] = fp32(a[n] / 127)
-    q8[n, k]    = clamp(rne(t[n, k] / s[n]), -127, 127)   (IEEE division; 0 where s[n] = 0)
-    row_scale[n] = fp32(s[n] * s_channel[n])
-so q8 * row_scale approximates the rotated weight level * s_rel * s_channel to within half an int8
-step of each row's range. The decode is "parity unpinned" against comfy-kitchen (no vectors
-exist); it is pinned here by the fp8 format definition (checked against torch's float8_e4m3fn on
-all 256 bytes), known answers, and the per-element rounding bound (tests/test_oracle_codebook.py).
+    q8[n, k]    = clamp(rne(t[n, k]), -127, 127)      (0 where t is NaN)
+    row_scale[n] = s_channel[n]
+
+so q8 * row_scale is level * s_rel * s_channel to within half an int8 step (s_channel / 2) wherever
+|t| <= 127.5. The pairing is the reference's; the rounding of t (half to even here) is not in the
+reference tree (comfy-kitchen is absent), so that detail is "parity unpinned". The oracle is pinned
+by the fp8 format definition (torch's float8_e4m3fn on all 256 bytes), hand-built rows with known
+codes, ties and saturation, and the reconstruction bound (tests/test_oracle_codebook.py).
 """
 from __future__ import annotations
 
@@ -67,13 +68,10 @@ def decode_w4a8_codebook(qdata, s_rel_u8, s_channel, codebook, group_size: int):
     if srel.shape != (n, k // group_size):
         raise ValueError("s_rel must be [N, K / group_size]")
     t = (lev * np.repeat(srel, group_size, axis=1)).astype(F32)
-    a = np.abs(t).max(axis=1)
-    s = (a / F32(127)).astype(F32)
-    safe = np.where(s == 0, F32(1), s)
-    q = np.clip(np.rint(t / safe[:, None]), -127, 127)
-    q = np.where((s == 0)[:, None], 0, q).astype(np.int8)
-    row_scale = (s * np.asarray(s_channel, dtype=F32)).astype(F32)
-    return q, row_scale
+    with np.errstate(invalid="ignore"):
+        q = np.clip(np.rint(t), -127, 127)
+    q = np.where(np.isnan(t), 0, q).astype(np.int8)
+    return q, np.asarray(s_channel, dtype=F32).reshape(-1).copy()
 
 
 def dequant_rotated(qdata, s_rel_u8, s_channel, codebook, group_size: int) -> np.ndarray:

@@ -77,11 +77,23 @@ def quant_per_token(xr: np.ndarray, limit: int) -> tuple[np.ndarray, np.ndarray]
     """Per-token symmetric quantizer, tools/activation_balance.py:65-71 (group_size None).
 
     Returns (q int8 [M, K], s float32 [M]).
+
+    Non-finite values (a row whose activation overflowed, e.g. an fp16 SwiGLU product beyond 65504,
+    spreads +-inf and NaN over its Hadamard block): the absmax is taken over the row's non-NaN
+    magnitudes (an inf makes it inf, so s = inf), and a value whose quotient x / s is not finite
+    (inf / inf, NaN) gets code 0; finite values of such a row quantize to 0 under s = inf. The
+    reference computes that scale through finite_absmax_for_int4_scale<InType>
+    (tools/ck_swiglu/swiglu_quant.cu:85), whose source is not in the reference tree: this rule is
+    this path's own ("parity unpinned" for rows with non-finite values).
     """
     xr = np.asarray(xr, dtype=F32)
-    amax = np.abs(xr).max(axis=1) if xr.shape[1] else np.zeros(xr.shape[0], F32)
-    s = np.maximum(amax / F32(limit), EPS_SCALE).astype(F32)
-    q = np.clip(np.rint(xr / s[:, None]), -limit, limit).astype(np.int8)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        mag = np.abs(xr)
+        mag = np.where(np.isnan(mag), F32(0), mag)
+        amax = mag.max(axis=1) if xr.shape[1] else np.zeros(xr.shape[0], F32)
+        s = np.maximum(amax / F32(limit), EPS_SCALE).astype(F32)
+        t = np.rint(xr / s[:, None])
+        q = np.where(np.isfinite(t), np.clip(t, -limit, limit), 0).astype(np.int8)
     return q, s
 
 

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mq_abi_version() == 8
+    assert lib.mq_abi_version() == 9
 
 
 def _err(lib):
@@ -79,18 +79,22 @@ def test_rotquant_validation_rejects_before_launch(lib):
 
 def test_swiglu_rotquant_validation_rejects_before_launch(lib):
     # h holds gate | up: its row stride must cover 2K columns
-    assert lib.mq_swiglu_rotquant(None, 0, 4, 256, 256, 256, 8, 0, None, 256, None, None) == -1
+    assert lib.mq_swiglu_rotquant(None, 0, 4, 256, 256, 256, 8, 0, 1, None, 256, None, None) == -1
     assert "null" in _err(lib)
-    assert lib.mq_swiglu_rotquant(None, 0, 4, 256, 384, 256, 8, 0, None, 256, None, None) == -1
+    assert lib.mq_swiglu_rotquant(None, 0, 4, 256, 384, 256, 8, 0, 1, None, 256, None, None) == -1
     assert "swiglu_rotquant" in _err(lib)
-    assert lib.mq_swiglu_rotquant(None, 0, 4, 320, 640, 256, 8, 0, None, 320, None, None) == -1
+    assert lib.mq_swiglu_rotquant(None, 0, 4, 320, 640, 256, 8, 0, 1, None, 320, None, None) == -1
     assert "not a multiple of the group size" in _err(lib)
-    assert lib.mq_swiglu_rotquant(None, 0, 4, 32768, 65536, 256, 8, 0, None, 32768, None, None) == -2
-    assert lib.mq_swiglu_rotquant(None, 0, 0, 256, 512, 256, 4, 1, None, 128, None, None) == 0
+    assert lib.mq_swiglu_rotquant(None, 0, 4, 32768, 65536, 256, 8, 0, 1, None, 32768, None, None) == -2
+    assert lib.mq_swiglu_rotquant(None, 0, 0, 256, 512, 256, 4, 1, 1, None, 128, None, None) == 0
     # the SwiGLU prologue takes bf16 or fp16 (as the reference's fused quantizer does)
-    assert lib.mq_swiglu_rotquant(None, 2, 4, 256, 512, 256, 8, 0, None, 256, None, None) == -1
+    assert lib.mq_swiglu_rotquant(None, 2, 4, 256, 512, 256, 8, 0, 1, None, 256, None, None) == -1
     assert "input type" in _err(lib)
-    assert lib.mq_swiglu_rotquant(None, 1, 0, 256, 512, 256, 8, 0, None, 256, None, None) == 0
+    assert lib.mq_swiglu_rotquant(None, 1, 0, 256, 512, 256, 8, 0, 1, None, 256, None, None) == 0
+    # the mode is the fused quantizer's single rounding (1) or the eager path's two (2)
+    assert lib.mq_swiglu_rotquant(None, 0, 0, 256, 512, 256, 8, 0, 2, None, 256, None, None) == 0
+    assert lib.mq_swiglu_rotquant(None, 0, 4, 256, 512, 256, 8, 0, 0, None, 256, None, None) == -1
+    assert "mode" in _err(lib)
 
 
 def test_decode_codebook_validation_rejects_before_launch(lib):
@@ -203,7 +207,7 @@ def test_linear_validation_rejects_before_launch(lib):
         return lib.mq_linear_w4_group(*[v[n] for n in names])
 
     assert call(act_bits=6) == -1 and "act_bits" in _err(lib)
-    assert call(swiglu=2) == -1 and "swiglu" in _err(lib)
+    assert call(swiglu=3) == -1 and "swiglu" in _err(lib)
     assert call(K=3000) == -1 and "K % 64" in _err(lib)
     assert call(workspace=None) == -1 and "workspace" in _err(lib)
     assert call(workspace=a + 16) == -1 and "256-byte" in _err(lib)

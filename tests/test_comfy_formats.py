@@ -28,13 +28,54 @@ class FakeQuantizedLayout:
     pass
 
 
-def _fake_comfy():
+def _fake_comfy(with_layout_op=True):
     registered = {}
     quant_ops = types.SimpleNamespace(QUANT_ALGOS={"int8_tensorwise": {}},
                                       register_layout_class=lambda name, cls: registered.__setitem__(name, cls),
                                       get_layout_class=lambda name: registered[name])
+    if with_layout_op:
+        quant_ops.LAYOUT_OPS = {}
+
+        def register_layout_op(torch_op, layout_cls):
+            def deco(handler):
+                quant_ops.LAYOUT_OPS[(torch_op, layout_cls)] = handler
+                return handler
+            return deco
+
+        quant_ops.register_layout_op = register_layout_op
     base = types.SimpleNamespace(QuantizedLayout=FakeQuantizedLayout, BaseLayoutParams=FakeBaseParams)
     return quant_ops, base, registered
+
+
+class StandInQuantizedTensor(torch.Tensor):
+    """A weight as ComfyUI holds it (QuantizedTensor: _qdata, _params, its layout class). F.linear on
+    it looks up the layout's aten.linear.default handler in the layout-op registry, as a layout
+    dispatch does, and dequantizes when the layout has none."""
+
+    @staticmethod
+    def __new__(cls, qdata, layout_cls, params, registry):
+        return torch.Tensor._make_wrapper_subclass(cls, params.orig_shape, dtype=params.orig_dtype,
+                                                   device=qdata.device)
+
+    def __init__(self, qdata, layout_cls, params, registry):
+        self._qdata, self._layout_cls, self._params, self._registry = qdata, layout_cls, params, registry
+
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        if func is torch.nn.functional.linear:
+            w = args[1]
+            handler = w._registry.get((torch.ops.aten.linear.default, w._layout_cls))
+            if handler is not None:
+                return handler(torch.ops.aten.linear.default, args, kwargs)
+            wf = w._layout_cls.dequantize(w._qdata, w._params)
+            return torch.nn.functional.linear(args[0], wf, *args[2:], **kwargs)
+        with torch._C.DisableTorchFunctionSubclass():
+            return func(*args, **kwargs)
+
+    @classmethod
+    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+        raise NotImplementedError(f"stand-in weight: {func} is not modelled")
 
 
 def test_register_adds_quant_algos_and_layouts():
@@ -50,6 +91,47 @@ def test_register_adds_quant_algos_and_layouts():
     # idempotent: a second call registers nothing new
     assert CF.register(quant_ops, base) == classes
     assert "int8_tensorwise" in quant_ops.QUANT_ALGOS
+    # each layout has its aten.linear handler in the layout-op registry
+    assert set(quant_ops.LAYOUT_OPS) == {(torch.ops.aten.linear.default, classes[CF.W4A8_LAYOUT]),
+                                         (torch.ops.aten.linear.default, classes[CF.W4A4_LAYOUT])}
+
+
+def test_linear_dispatch_reaches_the_layout_handler(monkeypatch):
+    """F.linear on a QuantizedTensor weight goes through the registered aten.linear handler: on the
+    GPU to the layout's quantized op (recorded here), on the host to dequantize + F.linear."""
+    quant_ops, base, _ = _fake_comfy()
+    classes = CF.register(quant_ops, base)
+    torch.manual_seed(0)
+    w = torch.randn(32, 256)
+    x = torch.randn(5, 256)
+    b = torch.randn(32)
+    for layout, q in ((CF.W4A8_LAYOUT, classes[CF.W4A8_LAYOUT].quantize(w)),
+                      (CF.W4A4_LAYOUT, classes[CF.W4A4_LAYOUT].quantize(w))):
+        cls = classes[layout]
+        qdata, params = q
+        wq = StandInQuantizedTensor(qdata, cls, params, quant_ops.LAYOUT_OPS)
+        # host tensors: the handler dequantizes (what the kernels approximate within the int codes)
+        y = torch.nn.functional.linear(x, wq, b)
+        ref = x @ cls.dequantize(qdata, params).T + b
+        assert torch.allclose(y, ref, atol=1e-4, rtol=1e-4)
+        # device tensors: the handler calls the layout's quantized op with the weight's parameters
+        calls = []
+        monkeypatch.setattr(CF, "_use_kernels", lambda x_, q_: True)
+        monkeypatch.setattr(ops, "w4a8_int8_linear", lambda *a, **k: calls.append(("w4a8", a, k)) or "w4a8")
+        monkeypatch.setattr(ops, "convrot_w4a4_linear", lambda *a, **k: calls.append(("w4a4", a, k)) or "w4a4")
+        out = torch.nn.functional.linear(x, wq, b)
+        monkeypatch.undo()
+        kind = "w4a8" if layout == CF.W4A8_LAYOUT else "w4a4"
+        assert out == kind and len(calls) == 1 and calls[0][0] == kind
+        a = calls[0][1]
+        assert a[0] is x and a[1] is qdata and a[2] is params.scale
+        if kind == "w4a8":
+            assert a[5] is params.zero and a[6] is b and a[7] == 64 and a[8] == 256
+        else:
+            assert a[3] is b and calls[0][2]["convrot_groupsize"] == params.convrot_groupsize
+    # without register_layout_op the layers still load; linear then dequantizes
+    quant_ops2, base2, _ = _fake_comfy(with_layout_op=False)
+    assert set(CF.register(quant_ops2, base2)) == {CF.W4A8_LAYOUT, CF.W4A4_LAYOUT}
 
 
 def test_reader_hooks_follow_the_converter_output(tmp_path):

@@ -13,10 +13,15 @@ from oracle import gemm, linear
 pytestmark = pytest.mark.gpu
 
 
-def _case(n, k, gs, seed, with_codebook=True):
+def _case(n, k, gs, seed, with_codebook=True, saturate=False):
+    """Random codes; s_rel in int8 units (fp8 32..120 with levels in [-1, 1], 1..15 with signed
+    int4 levels), or up to 448 with saturate (then |level * s_rel| can pass 127)."""
     rng = np.random.default_rng(seed)
     qdata = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
-    s_rel = rng.integers(0x20, 0x7F, (n, k // gs), dtype=np.uint8)      # finite positive fp8
+    lo, hi = (0x60, 0x70) if with_codebook else (0x38, 0x58)
+    if saturate:
+        lo, hi = 0x20, 0x7F                                                 # finite positive fp8
+    s_rel = rng.integers(lo, hi, (n, k // gs), dtype=np.uint8)
     s_ch = rng.uniform(0.001, 0.05, n).astype(np.float32)
     cb = np.sort(rng.uniform(-1, 1, 16)).astype(np.float32) if with_codebook else None
     return qdata, s_rel, s_ch, cb
@@ -29,13 +34,16 @@ def _dev(a, dev, dtype=None):
 
 @pytest.mark.parametrize("gs", [4, 8, 16, 32, 64])
 @pytest.mark.parametrize("with_codebook", [True, False])
-def test_decode_bitexact(gpu_device, gs, with_codebook):
+@pytest.mark.parametrize("saturate", [False, True])
+def test_decode_bitexact(gpu_device, gs, with_codebook, saturate):
     n, k = 96, 3072
-    print(f"[codebook] decode N={n} K={k} gs={gs} codebook={with_codebook}", flush=True)
-    qdata, s_rel, s_ch, cb = _case(n, k, gs, seed=gs + with_codebook)
+    print(f"[codebook] decode N={n} K={k} gs={gs} codebook={with_codebook} saturate={saturate}", flush=True)
+    qdata, s_rel, s_ch, cb = _case(n, k, gs, seed=gs + with_codebook, saturate=saturate)
     qdata[5] = 0                                                       # all-zero row (with levels[0] = 0)
     if cb is not None:
         cb[0] = 0.0
+        cb[1] = 0.5                                                    # ties: 0.5 * odd s_rel
+    s_rel[7, :] = 0x7F                                                 # fp8 NaN scales -> zero codes
     q8, rs = ck.decode_w4a8_codebook_weight(_dev(qdata, gpu_device, torch.int8),
                                             _dev(s_rel, gpu_device).view(torch.float8_e4m3fn),
                                             _dev(s_ch, gpu_device), None if cb is None else _dev(cb, gpu_device), gs)
@@ -55,7 +63,7 @@ def test_decode_large_shape(gpu_device):
     rows = np.r_[0:128, n - 128:n]
     q0, r0 = cbk.decode_w4a8_codebook(qdata[rows], s_rel[rows], s_ch[rows], cb, 16)
     assert np.array_equal(q8.cpu().numpy()[rows], q0) and np.array_equal(rs.cpu().numpy()[rows], r0)
-    assert (q8.abs().amax(dim=1) == 127).all()
+    assert np.array_equal(rs.cpu().numpy().view(np.uint32), s_ch.view(np.uint32))   # s_channel unchanged
 
 
 @pytest.mark.parametrize("m,n,k", [(512, 3072, 3072), (4096, 1024, 3072)])

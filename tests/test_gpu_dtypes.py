@@ -71,17 +71,36 @@ def test_swiglu_f16_every_gate_bitexact(gpu_device):
     g = g[np.isfinite(g)]
     rng = np.random.default_rng(0)
     for up in (1.0, -0.3125, 7.5, None):
-        print(f"[dtypes] swiglu f16 gate sweep up={up}", flush=True)
         u = (rng.standard_normal(g.size) * 4).astype(np.float16) if up is None else np.full(g.size, up, np.float16)
         h = np.zeros((g.size, 32), np.float16)
         h[:, 0], h[:, 16] = g, u
-        q, s = ops.rotate_quantize(_t(h, gpu_device), 0, 8, False, swiglu=True)
-        torch.cuda.synchronize()
-        a = swiglu.swiglu_f16(h[:, :16].astype(F32), h[:, 16:].astype(F32))
-        # rows whose product overflows fp16 have no finite scale; the comparison covers the rest
-        ok = np.isfinite(a).all(axis=1)
-        q0, s0 = quant.quant_per_token(a[ok], 127)
-        _codes_check(q.cpu().numpy()[ok], s.cpu().numpy()[ok], q0, s0, False)
+        for mode in (_lib.SWIGLU_FUSED, _lib.SWIGLU_EAGER):
+            print(f"[dtypes] swiglu f16 gate sweep up={up} mode={mode}", flush=True)
+            q, s = ops.rotate_quantize(_t(h, gpu_device), 0, 8, False, swiglu=mode)
+            torch.cuda.synchronize()
+            act = swiglu.swiglu_f16_eager if mode == _lib.SWIGLU_EAGER else swiglu.swiglu_f16
+            a = act(h[:, :16].astype(F32), h[:, 16:].astype(F32))
+            # rows whose product overflows fp16 (inf) are compared too: scale +inf, codes 0
+            q0, s0 = quant.quant_per_token(a, 127)
+            _codes_check(q.cpu().numpy(), s.cpu().numpy(), q0, s0, False)
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("hblock,bits,packed", [(64, 4, True), (256, 8, False), (16, 4, 2)])
+def test_swiglu_f16_product_overflow_rows(gpu_device, mode, hblock, bits, packed):
+    # rows whose fp16 product silu(g) * u passes 65504 become inf in the input type; the rotation
+    # spreads inf / NaN over that Hadamard block: the row is quantized with scale +inf and codes 0
+    # (oracle.quant.quant_per_token), the other rows as usual
+    print(f"[dtypes] swiglu f16 overflow mode={mode} hblock={hblock} bits={bits} packed={packed}", flush=True)
+    h = _f16_h(64, 3072, seed=9)
+    h[3, 100], h[3, 3072 + 100] = 300.0, 240.0          # 72000 -> inf
+    h[10, 7], h[10, 3072 + 7] = 200.0, -400.0           # -80000 -> -inf
+    q, s = ops.rotate_quantize(_t(h, gpu_device), hblock, bits, packed, swiglu=mode)
+    torch.cuda.synchronize()
+    with np.errstate(invalid="ignore", over="ignore"):
+        q0, s0 = swiglu.swiglu_rotquant(h.astype(F32), hblock, bits, dtype="f16", eager=mode == 2)
+    assert np.isinf(s0[[3, 10]]).all() and np.isfinite(np.delete(s0, [3, 10])).all()
+    _codes_check(q.cpu().numpy(), s.cpu().numpy(), q0, s0, packed)
 
 
 @pytest.mark.parametrize("hblock", [16, 64, 256])
@@ -265,7 +284,7 @@ def test_shipped_w4a8_is_decoded_once(gpu_device):
     print("[dtypes] shipped w4a8 decode once", flush=True)
     rng = np.random.default_rng(4)
     qdata = torch.from_numpy(rng.integers(-128, 128, (n, k // 2)).astype(np.int8)).to(gpu_device)
-    s_rel = torch.from_numpy(rng.integers(0x30, 0x40, (n, k // gs)).astype(np.uint8)).to(gpu_device)
+    s_rel = torch.from_numpy(rng.integers(0x60, 0x70, (n, k // gs)).astype(np.uint8)).to(gpu_device)
     s_ch = torch.from_numpy(rng.uniform(1e-3, 2e-3, n).astype(F32)).to(gpu_device)
     cb = torch.linspace(-1, 1, 16, device=gpu_device)
     x = synth.to_bf16_tensor(synth.activations(64, k, seed=2), gpu_device)

@@ -54,3 +54,29 @@ def test_gpu_conversion_matches_cpu_and_runs(gpu_device, tmp_path):
     q0, s0, z0 = quant.quant_weight_u4_asym(linear.rotate_weight(w, 256), 64)
     ref = linear.w4a8_asym_linear(synth.bf16_bits_to_f32(xb), q0, s0, z0, None, 256, 64)
     assert gemm.rel_l2(ref.y, y.float().cpu().numpy()) < 4e-3
+
+
+def test_layout_op_linear_runs_the_kernels(gpu_device):
+    """F.linear on a QuantizedTensor weight of each registered layout reaches the layout's
+    aten.linear handler and runs the HIP linear: the output equals the op's bit for bit."""
+    from kitchen_amd import comfy_formats as CF
+    from test_comfy_formats import StandInQuantizedTensor, _fake_comfy
+
+    print("[glue] layout-op aten.linear handler on the GPU", flush=True)
+    quant_ops, base, _ = _fake_comfy()
+    classes = CF.register(quant_ops, base)
+    w = torch.from_numpy(synth.weight(1024, 3072, seed=5)).to(gpu_device)
+    x = synth.to_bf16_tensor(synth.activations(192, 3072, seed=6), gpu_device)
+    b = torch.randn(1024, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16).to(gpu_device)
+    for layout in (CF.W4A8_LAYOUT, CF.W4A4_LAYOUT):
+        cls = classes[layout]
+        qdata, params = cls.quantize(w)
+        wq = StandInQuantizedTensor(qdata, cls, params, quant_ops.LAYOUT_OPS)
+        y = torch.nn.functional.linear(x, wq, b)
+        want = cls.linear(x, qdata, params, b)
+        torch.cuda.synchronize()
+        assert y.dtype == torch.bfloat16 and torch.equal(y, want)
+        # and the quantized result is the dequantized weight's product to within the activation
+        # codes' error (on the CPU oracle for these inputs: 0.009 with int8 codes, 0.207 with int4)
+        ref = x.float() @ cls.dequantize(qdata, params).float().T + b.float()
+        assert gemm.rel_l2(ref.cpu().numpy(), y.float().cpu().numpy()) < (2e-2 if layout == CF.W4A8_LAYOUT else 0.3)

@@ -144,3 +144,25 @@ def test_i4_sym_group_and_rowwise():
     assert s2[0] == 1.0 and q2[0].tolist() == [7, -4, 0, 2]
     q3, s3 = quant.quant_weight_i8_rowwise(np.array([[127.0, -63.5, 0.5]], F32))
     assert s3.shape == (1, 1) and s3[0, 0] == 1.0 and q3[0].tolist() == [127, -64, 0]
+
+
+def test_quant_per_token_non_finite_rows():
+    """A row holding +-inf (an overflowed activation) gets scale +inf and code 0 everywhere; NaN
+    entries get code 0 and do not count in the absmax; finite rows are unchanged."""
+    x = np.array([[1.0, -2.0, np.inf, 0.5],
+                  [1.0, np.nan, -4.0, 2.0],
+                  [1.0, -2.0, 3.0, 0.5]], np.float32)
+    q, s = quant.quant_per_token(x, 7)
+    assert np.isinf(s[0]) and (q[0] == 0).all()
+    # s = fp32(4 / 7) lies above 4 / 7, so 2 / s = 3.4999998 rounds to 3
+    assert s[1] == np.float32(4.0) / np.float32(7) and q[1].tolist() == [2, 0, -7, 3]
+    q2, s2 = quant.quant_per_token(x[2:], 7)
+    assert np.array_equal(q[2], q2[0]) and s[2] == s2[0]
+    # an fp16 SwiGLU product that overflows spreads inf / NaN over its Hadamard block
+    from oracle import swiglu
+    g = np.full((1, 64), 300.0, np.float32)
+    u = np.full((1, 64), 1.0, np.float32)
+    u[0, 5] = 240.0                                     # silu(300) * 240 = 72000 > 65504
+    h = np.concatenate([g, u], axis=1)
+    q, s = swiglu.swiglu_rotquant(h, 16, 4, dtype="f16")
+    assert np.isinf(s[0]) and (q == 0).all()

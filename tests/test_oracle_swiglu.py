@@ -209,3 +209,41 @@ def test_generated_f16_device_table_matches_oracle():
     assert np.array_equal(tab[bits.astype(np.int64)], swiglu.silu32(g).view(np.uint32))
     # non-finite gates follow the formula in IEEE arithmetic: +inf -> +inf, -inf and NaN -> NaN
     assert tab[0x7C00] == 0x7F800000 and np.isnan(tab[[0xFC00, 0x7E00]].view(F32)).all()
+
+
+def test_eager_swiglu_rounds_twice_like_torch():
+    """The eager activation is silu(gate).mul_(up) in the input's type: silu rounded to the type,
+    then the product rounded again. Checked against torch's own rounding (silu taken in float64 and
+    converted by torch), and against torch's silu itself on the CPU, which may differ only where
+    its fp32 silu lies next to a rounding boundary."""
+    import torch
+
+    rng = np.random.default_rng(11)
+    g = quant.bf16_bits_to_f32(quant.f32_to_bf16_bits(rng.standard_normal(200_000).astype(F32) * 3))
+    u = quant.bf16_bits_to_f32(quant.f32_to_bf16_bits(rng.standard_normal(200_000).astype(F32) * 2))
+    g64 = g.astype(np.float64)
+    s64 = torch.from_numpy(g64 / (1 + np.exp(-g64)))
+    for dt, ours in ((torch.bfloat16, swiglu.swiglu_bf16_eager), (torch.float16, swiglu.swiglu_f16_eager)):
+        gt, ut = torch.from_numpy(g).to(dt), torch.from_numpy(u).to(dt)
+        want = (s64.float().to(dt).float() * ut.float()).to(dt).float().numpy()
+        got = ours(gt.float().numpy(), ut.float().numpy())
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        eager_torch = torch.nn.functional.silu(gt).mul_(ut).float().numpy()
+        assert (got != eager_torch).mean() < 1e-3
+    # the two roundings differ from the fused single rounding on some inputs, by one unit at most
+    fused = swiglu.swiglu_bf16(g, u)
+    eager = swiglu.swiglu_bf16_eager(g, u)
+    diff = fused != eager
+    assert 0.05 < diff.mean() < 0.5
+    ulp = np.abs(fused.view(np.int32) - eager.view(np.int32)) >> 16
+    assert ulp.max() == 1
+
+
+def test_eager_swiglu_known_answers():
+    # g = 1: silu32 = 0.731058597564697 -> bf16 0.73046875; times u = 1.0078125 (1 + 2^-7):
+    # eager 0.73046875 * 1.0078125 = 0.736175537... -> bf16 0.734375 (1.46875 * 2^-1),
+    # fused 0.731058... * 1.0078125 = 0.7367700... -> bf16 0.73828125
+    g = np.array([1.0], F32)
+    u = np.array([1.0078125], F32)
+    assert swiglu.swiglu_bf16_eager(g, u)[0] == F32(0.734375)
+    assert swiglu.swiglu_bf16(g, u)[0] == F32(0.73828125)

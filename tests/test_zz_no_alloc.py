@@ -1,7 +1,10 @@
 """mq_linear_w4_group_noalloc, the whole W4 group linear that allocates nothing (its codes, scales
 and split-K partials live in the library's fixed per-device scratch array), against the ordinary
 entry point mq_linear_w4_group with a caller workspace: bit-exact on two calls in a row, the
-second with a smaller input, called through the C ABI."""
+second with a smaller input, called through the C ABI; the trailing-rows product with the SwiGLU
+prologue through the scratch; device memory unchanged across a call; and a shape whose split-K
+partials do not fit beside its codes (then the product runs unsplit: same codes and int32
+partials, fp32 group sums associated differently)."""
 import numpy as np
 import pytest
 import torch
@@ -16,22 +19,30 @@ def _noalloc():
     return _lib.load().mq_linear_w4_group_noalloc
 
 
-def _args(x, qd, s16, zp, bias, y, act_bits):
+def _args(x, qd, s16, zp, bias, y, act_bits, swiglu=0):
     m, k = x.shape
+    k = k // 2 if swiglu else k
     n = qd.shape[0]
-    return [x.data_ptr(), _lib.dtype_code(x.dtype), x.stride(0), 256, act_bits, 0, qd.data_ptr(), qd.stride(0),
+    return [x.data_ptr(), _lib.dtype_code(x.dtype), x.stride(0), 256, act_bits, swiglu, qd.data_ptr(), qd.stride(0),
             s16.data_ptr(), s16.stride(0), _lib.ptr(zp), 0 if zp is None else zp.stride(0), _lib.ptr(bias),
             _lib.DT_BF16 if bias is None else _lib.dtype_code(bias.dtype), y.data_ptr(), _lib.dtype_code(y.dtype),
             y.stride(0), m, n, k]
 
 
-def _reference(x, qd, s16, zp, bias, y, act_bits):
+def _reference(x, qd, s16, zp, bias, y, act_bits, swiglu=0):
     m, k = x.shape
+    k = k // 2 if swiglu else k
     n = qd.shape[0]
     work = torch.empty(_lib.load().mq_linear_workspace_bytes(m, n, k), dtype=torch.uint8, device=x.device)
-    _lib.call("mq_linear_w4_group", *_args(x, qd, s16, zp, bias, y, act_bits), work.data_ptr(), work.numel(),
-              _lib.stream_of(x))
+    _lib.call("mq_linear_w4_group", *_args(x, qd, s16, zp, bias, y, act_bits, swiglu), work.data_ptr(),
+              work.numel(), _lib.stream_of(x))
     return work
+
+
+def _w4a8_weight(n, k, dev, seed=1):
+    w = torch.from_numpy(synth.weight(n, k, seed=seed)).to(dev)
+    qd, s16, zp = ck.quantize_w4a8_asym_weight(w, 64, 256)
+    return qd.view(torch.uint8), s16, zp.view(torch.uint8)
 
 
 @pytest.mark.gpu
@@ -60,6 +71,56 @@ def test_noalloc_equals_workspace_entry_point(gpu_device, act_bits):
         torch.cuda.synchronize()
         assert torch.equal(y0, y1)
         del work
+
+
+@pytest.mark.gpu
+def test_noalloc_trailing_rows_with_swiglu_prologue(gpu_device):
+    # M = 4352 against N = 12288: the last 256 rows run as their own product (trailing rows) on the
+    # 16-row code tiles, and the activation is the SwiGLU prologue of a [gate | up] input
+    m, n, k = 4352, 12288, 3072
+    print(f"[noalloc] trailing rows + swiglu M={m} N={n} K={k}", flush=True)
+    qd, s16, zp = _w4a8_weight(n, k, gpu_device)
+    g = torch.Generator(device=gpu_device).manual_seed(3)
+    h = (torch.randn(m, 2 * k, generator=g, device=gpu_device) * 2).to(torch.bfloat16)
+    bias = torch.randn(n, generator=g, device=gpu_device).to(torch.bfloat16)
+    y0 = torch.empty((m, n), dtype=torch.bfloat16, device=gpu_device)
+    y1 = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+    work = _reference(h, qd, s16, zp, bias, y0, 8, swiglu=_lib.SWIGLU_FUSED)
+    rc = _noalloc()(*_args(h, qd, s16, zp, bias, y1, 8, swiglu=_lib.SWIGLU_FUSED), _lib.stream_of(h))
+    assert rc == 0, _lib.load().mq_last_error().decode()
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
+    # the call itself takes no device memory: free memory is unchanged across a repeat call
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info(gpu_device)[0]
+    rc = _noalloc()(*_args(h, qd, s16, zp, bias, y1, 8, swiglu=_lib.SWIGLU_FUSED), _lib.stream_of(h))
+    torch.cuda.synchronize()
+    assert rc == 0 and torch.cuda.mem_get_info(gpu_device)[0] == free0
+    assert torch.equal(y0, y1)
+    del work
+
+
+@pytest.mark.gpu
+def test_noalloc_when_partials_do_not_fit(gpu_device):
+    # codes and scales (57.4 MB) fit the scratch; whether the split-K partials fit beside them
+    # decides whether the result is the workspace entry's bit for bit
+    m, n, k = 3500, 512, 16384
+    need = _lib.load().mq_linear_workspace_bytes(m, n, k)
+    print(f"[noalloc] M={m} N={n} K={k}: workspace {need} bytes, scratch {SCRATCH_BYTES}", flush=True)
+    qd, s16, zp = _w4a8_weight(n, k, gpu_device, seed=4)
+    x = synth.to_bf16_tensor(synth.activations(m, k, seed=5), gpu_device)
+    y0 = torch.empty((m, n), dtype=torch.bfloat16, device=gpu_device)
+    y1 = torch.empty((m, n), dtype=torch.bfloat16, device=gpu_device)
+    work = _reference(x, qd, s16, zp, None, y0, 8)
+    rc = _noalloc()(*_args(x, qd, s16, zp, None, y1, 8), _lib.stream_of(x))
+    assert rc == 0, _lib.load().mq_last_error().decode()
+    torch.cuda.synchronize()
+    if need <= SCRATCH_BYTES:
+        assert torch.equal(y0, y1)
+    else:
+        a, b = y0.float(), y1.float()
+        assert (torch.linalg.vector_norm(a - b) / torch.linalg.vector_norm(a)).item() < 1e-3
+    del work
 
 
 def test_noalloc_rejects_inputs_beyond_the_scratch():
