@@ -335,7 +335,8 @@ int mq_linear_rowscale(const void* x, int x_dtype, int64_t ldx, int hblock, int 
  * mq_linear_w4_group's bit for bit whenever mq_linear_workspace_bytes(M, N, K) <=
  * MQ_NOALLOC_SCRATCH_BYTES (both entries then take the same split-K decision); when only the codes
  * and scales fit, the product runs without split-K: the same codes and int32 group partials, with
- * the fp32 group sums associated in another order (outputs can differ in the last bits). Every call
+ * the fp32 group sums associated in another order (outputs within the linear's tolerance of the
+ * exact result, not bit-identical to the split product's). Every call
  * on one GPU shares that GPU's array: calls that overlap on one GPU (several streams or threads)
  * race and must be serialized by the caller. Nothing in the array needs to start at zero: each call
  * writes every byte it reads.

@@ -40,7 +40,9 @@ def test_w4a4_group_linear_swiglu_equals_two_steps(gpu_device, m, hb):
     rng = np.random.default_rng(m)
     h = torch.from_numpy(rng.standard_normal((m, 2 * k)).astype(np.float32) * 2).to(torch.bfloat16).to(gpu_device)
     y = ck.convrot_w4a4_linear(h, qw, s16, None, convrot_groupsize=hb, input_act="swiglu")
-    qa, sa = ops.rotate_quantize(h, hb, 4, _lib.Q_X16ALT, swiglu=True)
+    # comfy-kitchen fuses (one rounding) under H256 only; H16 / H64 take its eager two roundings
+    mode = _lib.SWIGLU_FUSED if hb == 256 else _lib.SWIGLU_EAGER
+    qa, sa = ops.rotate_quantize(h, hb, 4, _lib.Q_X16ALT, swiglu=mode)
     y2 = ops.gemm_w4_group(qa, sa, qw, s16, None, None, n, act_mode=_lib.ACT_X16ALT)
     torch.cuda.synchronize()
     assert torch.equal(y, y2)
