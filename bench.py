@@ -222,8 +222,9 @@ def kernels_child(args) -> int:
     m, k, n = args.m, args.k, args.n
     _, _, x, qd, s16, zp, bias = make_inputs(m, k, n)
     qa, sa = ck.quantize_int8_rowwise_convrot(x, 256)
+    xw = ck.expand_w4_weight(qd.view(torch.uint8), zp.view(torch.uint8), 0)   # the linear's GEMM operand
     for _ in range(3):
-        ck.gemm_w4_group(qa, sa, qd.view(torch.uint8), s16, zp.view(torch.uint8), bias, n)
+        ck.gemm_w4_group(qa, sa, xw, s16, None, bias, n)
     if args.with_rowscale:
         # the W8A8 linear of the same shape (random int8 weights in 16-row tiles, per-row scales),
         # for profiles and counter runs that compare the two epilogues: its GEMM reads activation
@@ -531,10 +532,15 @@ def main() -> int:
     ops = 2.0 * m * n * k
     tops = ops / (ms_step * 1e-3) / 1e12
 
-    # ---- dominant kernel (GEMM) alone, same stream, inputs resident
+    # ---- dominant kernel (GEMM) alone, same stream, inputs resident: on the int8 expansion of the
+    # packed weights the linear made at its first call (the same bits as on the packed weights), and
+    # for comparison on the packed weights themselves
     qa, sa = ck.quantize_int8_rowwise_convrot(x, 256)
     qdu, zpu = qd.view(torch.uint8), zp.view(torch.uint8)
-    ms_gemm = time_launches(lambda: ck.gemm_w4_group(qa, sa, qdu, s16, zpu, bias, n), 20, settle_ms=args.settle_ms / 2)
+    xw = ck.expand_w4_weight(qdu, zpu, 0)
+    ms_gemm = time_launches(lambda: ck.gemm_w4_group(qa, sa, xw, s16, None, bias, n), 20, settle_ms=args.settle_ms / 2)
+    ms_gemm_packed = time_launches(lambda: ck.gemm_w4_group(qa, sa, qdu, s16, zpu, bias, n), 20,
+                                   settle_ms=args.settle_ms / 4)
     gemm_tops = ops / (ms_gemm * 1e-3) / 1e12
     ms_rq_ns = time_launches(lambda: ck.quantize_int8_rowwise_convrot(x, 256), 20)
 
@@ -573,10 +579,14 @@ def main() -> int:
         "data": "synthetic: seeded N(0,1) bf16 activations with 1% x20 outlier channels, N(0,0.02) weights",
         "config": {"workload": "w4a8_linear (rotate H256 + int8 per-token quant + uint4-asym g64 GEMM + epilogue)",
                    "M": m, "K": k, "N": n, "hadamard_block": 256, "group": 64, "out": "bf16"},
-        "roofline": {"bound": "mfma", "kernel": "gemm_wide_kernel<256,256,U4Asym,GroupScale,0>",
+        "roofline": {"bound": "mfma", "kernel": "gemm_wide_kernel<256,256,U4Asym,GroupScale,0,expanded>",
                      "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
                      "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": gemm_traffic,
-                     "ops_per_launch": ops, "avg_launch_ms": round(ms_gemm, 5)},
+                     "ops_per_launch": ops, "avg_launch_ms": round(ms_gemm, 5),
+                     "weights": "the uint4 codes and zero-points as stored, expanded once per weight to int8 "
+                                "(q - z, negated in odd K groups) in 16-row tiles, which the GEMM reads; "
+                                "the same bits as the packed weights' GEMM",
+                     "packed_weights_avg_launch_ms": round(ms_gemm_packed, 5)},
         "rotquant_roofline": {"bound": "hbm", "kernel": "rotquant_kernel<256,int8,3>", "M": RQ_M, "K": k,
                               "achieved": round(rq_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                               "frac": round(rq_gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": rq_bytes,

@@ -269,6 +269,23 @@ int mq_tile_weight_i8(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t
                                  static_cast<hipStream_t>(stream));
 }
 
+int mq_expand_weight_w4(const uint8_t* qw, int64_t ldw, const uint8_t* wz, int64_t ldwz, int64_t N, int64_t K,
+                        int layout, int8_t* out, void* stream) {
+    clear_error();
+    MQ_REQUIRE(layout == MQ_ACT_I8 || layout == MQ_ACT_X16ALT || layout == MQ_W4X_ROW,
+               "expand_weight_w4: layout must be MQ_ACT_I8 (0), MQ_ACT_X16ALT (2) or MQ_W4X_ROW (3), got %d", layout);
+    MQ_REQUIRE(N >= 0 && K > 0 && K % 64 == 0, "expand_weight_w4: bad shape N=%lld K=%lld (K %% 64 == 0)",
+               (long long)N, (long long)K);
+    MQ_REQUIRE((N + 15) / 16 * 16 * K < (int64_t(1) << 31), "expand_weight_w4: the expanded weight must be under 2 GiB");
+    if (N == 0) return MQ_OK;
+    MQ_REQUIRE(qw && out, "expand_weight_w4: null pointer");
+    MQ_REQUIRE(ldw >= K / 2 && ldw % 8 == 0 && aligned(qw, 8) && aligned(out, 16),
+               "expand_weight_w4: needs ldw >= K/2, ldw %% 8 == 0, an 8-byte aligned qw and a 16-byte aligned out");
+    MQ_REQUIRE(!wz || ldwz >= (K / 64 + 1) / 2, "expand_weight_w4: ldwz < ceil(K/64/2)");
+    return launch_expand_weight_w4(qw, ldw, wz, ldwz, N, K, layout, reinterpret_cast<uint8_t*>(out),
+                                   static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"
 
 namespace {
@@ -279,14 +296,24 @@ int w4_group_args(const int8_t* qa, int64_t lda, const float* sa, const uint8_t*
                   int bias_dtype, void* y, int y_dtype, int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace,
                   int64_t workspace_bytes, GemmArgs* out) {
     MQ_REQUIRE(group == 64, "gemm_w4_group: quant group size must be 64 (got %d)", group);
+    const bool expanded = (act_mode & MQ_W4_EXPANDED) != 0;
+    act_mode &= ~MQ_W4_EXPANDED;
     MQ_REQUIRE(act_mode >= MQ_ACT_I8 && act_mode <= MQ_ACT_X16ALT, "gemm_w4_group: unknown act_mode %d", act_mode);
-    int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, K / 2);
+    if (expanded) {
+        MQ_REQUIRE(act_mode != MQ_ACT_I4, "gemm_w4_group: expanded weights serve MQ_ACT_I8 and MQ_ACT_X16ALT");
+        MQ_REQUIRE(K >= 192 && K % 64 == 0, "gemm_w4_group: expanded weights need K %% 64 == 0 and K >= 192 (got %lld)",
+                   (long long)K);
+        MQ_REQUIRE(N >= 0 && (N + 15) / 16 * 16 * K < (int64_t(1) << 31),
+                   "gemm_w4_group: expanded weights must be under 2 GiB");
+        ldw = K;
+    }
+    int rc = check_gemm_common(qa, lda, qw, ldw, M, N, K, expanded ? K : K / 2);
     if (rc) return rc;
     MQ_REQUIRE(sa && ws, "gemm_w4_group: null pointer");
     rc = check_gemm_out("gemm_w4_group", bias, bias_dtype, y, y_dtype, ldy, N);
     if (rc) return rc;
     MQ_REQUIRE(ldws >= K / group, "gemm_w4_group: ldws < K/group");
-    MQ_REQUIRE(!wz || ldwz >= (K / group + 1) / 2, "gemm_w4_group: ldwz < ceil(K/group/2)");
+    MQ_REQUIRE(expanded || !wz || ldwz >= (K / group + 1) / 2, "gemm_w4_group: ldwz < ceil(K/group/2)");
     MQ_REQUIRE(workspace_bytes >= 0 && (!workspace || aligned(workspace, 16)),
                "gemm_w4_group: workspace must be 16-byte aligned");
     GemmArgs a{};
@@ -295,6 +322,7 @@ int w4_group_args(const int8_t* qa, int64_t lda, const float* sa, const uint8_t*
     a.M = M; a.N = N; a.K = K;
     a.act_mode = act_mode;
     a.work = workspace; a.work_bytes = workspace ? workspace_bytes : 0;
+    a.wtile = expanded;
     *out = a;
     return MQ_OK;
 }
@@ -490,11 +518,13 @@ int mq_linear_w4_group(const void* x, int x_dtype, int64_t ldx, int hblock, int 
                        int64_t ldwz, const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy, int64_t M,
                        int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
     clear_error();
+    const int expanded = act_bits & MQ_W4_EXPANDED;
+    act_bits &= ~MQ_W4_EXPANDED;
     int rc = check_linear("linear_w4_group", act_bits, swiglu, M, N, K, workspace, workspace_bytes);
     if (rc) return rc == kEmpty ? MQ_OK : rc;
     // int4 activations enter the group GEMM in its x16 operand layout
     const int layout = act_bits == 4 ? MQ_Q_X16ALT : MQ_Q_BYTES;
-    const int act_mode = act_bits == 4 ? MQ_ACT_X16ALT : MQ_ACT_I8;
+    const int act_mode = (act_bits == 4 ? MQ_ACT_X16ALT : MQ_ACT_I8) | expanded;
     auto* base = static_cast<uint8_t*>(workspace);
     const LinearWs w = linear_ws(M, N, K);
     GemmArgs a;
@@ -505,6 +535,11 @@ int mq_linear_w4_group(const void* x, int x_dtype, int64_t ldx, int hblock, int 
     const WKind wk = wz ? WKind::U4Asym : WKind::I4Sym;
     a.atile = 1;   // the codes in 16-row tiles wherever the wide kernel reads them
     a.atile = gemm_runs_wide(a, wk, Epi::GroupScale);
+    if (a.wtile && !a.atile) {
+        set_error("linear_w4_group: expanded 4-bit weights are read by the wide kernel only (M > 4, operands under "
+                  "2 GiB); pass the packed weights");
+        return MQ_EUNSUPPORTED;
+    }
     rc = quantize_into(x, x_dtype, ldx, hblock, act_bits, swiglu, layout, a.atile, M, K, base, stream);
     if (rc) return rc;
     return launch_gemm(a, wk, Epi::GroupScale, static_cast<hipStream_t>(stream));

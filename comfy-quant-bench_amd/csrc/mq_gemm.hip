@@ -270,15 +270,17 @@ bool runs_gemv(const GemmArgs& a, WKind wk, Epi epi) {
 bool gemm_runs_wide(const GemmArgs& a, WKind wk, Epi epi) {
     if (runs_gemv(a, wk, epi)) return false;
     // The 256 x 256-tile kernel addresses each operand with 32-bit buffer offsets.
-    const int64_t wbytes = wk == WKind::I8 ? a.K : a.K / 2;
+    // (4-bit weights with wtile set come expanded to int8 tiles, K bytes per row)
+    const int64_t wbytes = wk == WKind::I8 || a.wtile ? a.K : a.K / 2;
     const bool fits32 = a.M * a.lda < (int64_t(1) << 31) && a.N * a.ldw < (int64_t(1) << 31) &&
                         (a.N * a.ldws + a.K / 64) * 2 < (int64_t(1) << 31) && wbytes <= a.ldw &&
-                        (!a.atile || (a.M + 15) / 16 * 16 * a.K < (int64_t(1) << 31));
+                        (!a.atile || (a.M + 15) / 16 * 16 * a.K < (int64_t(1) << 31)) &&
+                        (!a.wtile || (a.N + 15) / 16 * 16 * a.K < (int64_t(1) << 31));
     // (activation layout 1, int4 codes scaled in the kernel, is served by the 128-tile kernel only)
     // the wide kernel loads the zero-points of four groups as one 2-byte word and two groups'
     // scales as one dword per weight row
     const bool zs_aligned =
-        (wk != WKind::U4Asym || (a.ldwz % 2 == 0 && reinterpret_cast<uintptr_t>(a.wz) % 2 == 0)) &&
+        (wk != WKind::U4Asym || a.wtile || (a.ldwz % 2 == 0 && reinterpret_cast<uintptr_t>(a.wz) % 2 == 0)) &&
         (epi != Epi::GroupScale || (a.ldws % 2 == 0 && reinterpret_cast<uintptr_t>(a.ws16) % 4 == 0));
     // (K >= 192: the wide kernel's last-row load correction needs at least three K groups)
     // Weights in 16-row tiles are read by the wide kernel at every M above the GEMV's few rows.
@@ -289,6 +291,11 @@ int launch_gemm(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
     if (a.M == 0 || a.N == 0) return 0;
     if (a.atile && !gemm_runs_wide(a, wk, epi)) {
         set_error("gemm: activation codes in 16-row tiles are read by the wide kernel only");
+        return -2;
+    }
+    if (a.wtile && wk != WKind::I8 && !gemm_runs_wide(a, wk, epi)) {
+        set_error("gemm: expanded 4-bit weights are read by the wide kernel only (M > 4, K >= 192, "
+                  "operands under 2 GiB); pass the packed weights");
         return -2;
     }
     // a few rows: HBM-bound, served by the dot4 kernel (activation rows staged in LDS); its parity

@@ -251,8 +251,11 @@ __device__ __forceinline__ T& lds(uint8_t* smem, int off) {
 
 // One workgroup: a T x T output tile. AM is the activation layout of the group epilogues
 // (0 int8 codes; 2 int4 codes stored as 16 * q and negated in odd groups, signed int4 weights then
-// entering as 16 * v); row epilogues use 0.
-template <int TM_, int TN_, WKind WK, Epi EPI, int AM, bool SPLIT>
+// entering as 16 * v); row epilogues use 0. XP (4-bit kinds, group scales): the weights come
+// expanded to int8 in 16-row tiles (mq_expand_weight_w4: the bytes the unpack would store, zero-point
+// and sign included), so B takes A's DMA path and no zero-points are loaded; the arithmetic, and
+// the scaling by WK and AM, is the packed kernel's.
+template <int TM_, int TN_, WKind WK, Epi EPI, int AM, bool SPLIT, bool XP>
 __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, int tiles_n) {
     using C = Cfg<TM_, TN_>;
     constexpr int TM = C::TM, TN = C::TN, NI = C::NI, NJ = C::NJ, NTL = C::NTL, TILE_BYTES = C::TILE_BYTES;
@@ -262,7 +265,9 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     static_assert(!SPLIT || EPI == Epi::GroupScale || EPI == Epi::RowScale, "split-K outputs partial results");
     static_assert(AM == 0 || AM == 2, "activation layout 1 is served by the 128-tile kernel");
     constexpr bool kGroup = EPI == Epi::GroupScale || EPI == Epi::GroupPartials;
-    constexpr bool kPacked = WK != WKind::I8;
+    static_assert(!XP || (WK != WKind::I8 && EPI == Epi::GroupScale), "expanded 4-bit weights, group scales");
+    constexpr bool kPacked = WK != WKind::I8 && !XP;
+    constexpr bool kHasZ = WK == WKind::U4Asym && !XP;   // zero-points loaded (packed uint4 weights)
     constexpr int kShift = kGroup && AM == 2 ? (WK == WKind::I4Sym ? 8 : 4) : 0;
     constexpr float kSfac = 1.0f / static_cast<float>(1 << kShift);
     __shared__ __attribute__((aligned(16))) uint8_t smem[C::SMEM_BYTES];
@@ -335,7 +340,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     const bool b_ok = brow < rows_n;
     const int b_off = b_ok ? static_cast<int>(brow * a.ldw) + bpart * C::BPT : kOob;
     // zero-points and scales (null for the kinds that have none: the range is then empty)
-    const bool has_z = WK == WKind::U4Asym, has_s = EPI == Epi::GroupScale;
+    const bool has_z = kHasZ, has_s = EPI == Epi::GroupScale;
     const u4v db = sdesc(a.qw + n0 * a.ldw, (rows_n - 1) * a.ldw + kbytes_w);
     const u4v dz = sdesc(has_z ? a.wz + n0 * a.ldwz : a.qw, has_z ? (rows_n - 1) * a.ldwz + (G + 1) / 2 : 0);
     const u4v ds = sdesc(has_s ? static_cast<const void*>(a.ws16 + n0 * a.ldws) : a.qw,
@@ -420,12 +425,12 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // once a block's zero-points and scales have arrived (before their first use): the moved-back
     // loads of the last block bring the wanted bytes down
     auto settle_zs = [&]() {
-        if constexpr (WK == WKind::U4Asym) zq >>= zsh;
+        if constexpr (kHasZ) zq >>= zsh;
         if constexpr (EPI == Epi::GroupScale) sq >>= ssh;
     };
     auto gload_zs = [&](int b4) {
         const bool lb = b4 == last_b4;   // wave-uniform
-        if constexpr (WK == WKind::U4Asym) {
+        if constexpr (kHasZ) {
             zsh = lb ? zsh_last : 0u;
             zq = asm_ld16(b4 < G ? dz : d_none, lb ? z_last : z_off, b4 < G ? b4 >> 1 : 0);
         }
@@ -590,7 +595,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // (packed weights)
     constexpr int kTB = NTL >= 24 ? 8 : 4, kTS = NTL >= 24 ? 10 : 5, kTL = NTL >= 24 ? 12 : 6;
     constexpr int kB = kPacked ? 1 : 0;
-    constexpr int kZS = (WK == WKind::U4Asym) + (EPI == Epi::GroupScale);
+    constexpr int kZS = kHasZ + (EPI == Epi::GroupScale);
     // Before the barrier that ends group g, A(g + 2) (issued at step kTD of group g - 1) must be
     // complete; issued after it: B(g + 3), [zs if (g - 1) % 4 == 1], A(g + 3), B(g + 4),
     // [zs if g % 4 == 1]. (The partials variant also stores to global memory; it waits for all.)
@@ -695,7 +700,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // could reuse such a register for an address and have it overwritten by a late zero.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if constexpr (kPacked) asm volatile("" : "+v"(rb[0]), "+v"(rb[1]));
-    if constexpr (WK == WKind::U4Asym) asm volatile("" : "+v"(zq));
+    if constexpr (kHasZ) asm volatile("" : "+v"(zq));
     if constexpr (EPI == Epi::GroupScale) asm volatile("" : "+v"(sq));
 #undef MQ_WAIT_B
     // drain: the last LAG tiles of the last group run (dead unless G is a multiple of four)
@@ -918,13 +923,13 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a) {
     }
 }
 
-template <int TM, int TN, WKind WK, Epi EPI, int AM>
+template <int TM, int TN, WKind WK, Epi EPI, int AM, bool XP>
 int launch_tile(const GemmArgs& a, hipStream_t stream) {
     const int tiles_m = static_cast<int>((a.M + TM - 1) / TM);
     const int tiles_n = static_cast<int>((a.N + TN - 1) / TN);
     if constexpr (EPI == Epi::GroupScale || EPI == Epi::RowScale) {
         if (a.ksplit > 1) {
-            hipLaunchKernelGGL((gemm_wide_kernel<TM, TN, WK, EPI, AM, true>),
+            hipLaunchKernelGGL((gemm_wide_kernel<TM, TN, WK, EPI, AM, true, XP>),
                                dim3(static_cast<unsigned>(tiles_m * tiles_n * a.ksplit)), dim3(NT), 0, stream, a,
                                tiles_m, tiles_n);
             const int rc = launch_status("gemm_wide");
@@ -935,26 +940,26 @@ int launch_tile(const GemmArgs& a, hipStream_t stream) {
             return launch_status("gemm_splitk_reduce");
         }
     }
-    hipLaunchKernelGGL((gemm_wide_kernel<TM, TN, WK, EPI, AM, false>), dim3(static_cast<unsigned>(tiles_m * tiles_n)),
+    hipLaunchKernelGGL((gemm_wide_kernel<TM, TN, WK, EPI, AM, false, XP>), dim3(static_cast<unsigned>(tiles_m * tiles_n)),
                        dim3(NT), 0, stream, a, tiles_m, tiles_n);
     return launch_status("gemm_wide");
 }
 
-template <WKind WK, Epi EPI, int AM>
+template <WKind WK, Epi EPI, int AM, bool XP = false>
 int launch_one(const GemmArgs& a, hipStream_t stream) {
     const int t = a.tile ? a.tile : choose_tile(a.M, a.N);
-    if (t == 128) return launch_tile<128, 128, WK, EPI, AM>(a, stream);
-    if (t == 192) return launch_tile<256, 192, WK, EPI, AM>(a, stream);
-    if (t == 256) return launch_tile<256, 256, WK, EPI, AM>(a, stream);
+    if (t == 128) return launch_tile<128, 128, WK, EPI, AM, XP>(a, stream);
+    if (t == 192) return launch_tile<256, 192, WK, EPI, AM, XP>(a, stream);
+    if (t == 256) return launch_tile<256, 256, WK, EPI, AM, XP>(a, stream);
     set_error("gemm: tile code %d is not 128, 192 or 256", t);
     return -1;
 }
 
-template <WKind WK, Epi EPI>
+template <WKind WK, Epi EPI, bool XP = false>
 int launch_group(const GemmArgs& a, hipStream_t stream) {
     switch (a.act_mode) {
-        case 0: return launch_one<WK, EPI, 0>(a, stream);
-        case 2: return launch_one<WK, EPI, 2>(a, stream);
+        case 0: return launch_one<WK, EPI, 0, XP>(a, stream);
+        case 2: return launch_one<WK, EPI, 2, XP>(a, stream);
         default: break;
     }
     set_error("gemm: unknown activation layout %d", a.act_mode);
@@ -964,6 +969,11 @@ int launch_group(const GemmArgs& a, hipStream_t stream) {
 template <WKind WK>
 int launch_wk(const GemmArgs& a, Epi epi, hipStream_t stream) {
     if constexpr (WK != WKind::I8) {   // 4-bit weights: per-group scales
+        if (a.wtile) {                  // expanded to int8 tiles
+            if (epi == Epi::GroupScale) return launch_group<WK, Epi::GroupScale, true>(a, stream);
+            set_error("gemm: expanded 4-bit weights serve the group-scale epilogue only");
+            return -2;
+        }
         if (epi == Epi::GroupScale) return launch_group<WK, Epi::GroupScale>(a, stream);
         if (epi == Epi::GroupPartials) return launch_group<WK, Epi::GroupPartials>(a, stream);
     }

@@ -53,6 +53,10 @@ int launch_quantize_weight(const void* w, int dtype, int64_t N, int64_t K, int64
 // int8 weights [N, K] into the 16-row tile layout of GemmArgs::wtile (mq_wquant.hip)
 int launch_tile_weight_i8(const uint8_t* w, int64_t ldw, int64_t N, int64_t K, uint8_t* out, hipStream_t stream);
 
+// packed 4-bit weights into int8 16-row tiles (mq_expand_weight_w4's layouts; mq_wquant.hip)
+int launch_expand_weight_w4(const uint8_t* qw, int64_t ldw, const uint8_t* wz, int64_t ldwz, int64_t N, int64_t K,
+                            int layout, uint8_t* out, hipStream_t stream);
+
 // --- GEMMs (mq_gemm.hip)
 enum class WKind : int { U4Asym = 0, I4Sym = 1, I8 = 2 };
 enum class Epi : int { GroupScale = 0, GroupPartials = 1, RowScale = 2, RowAcc = 3 };
@@ -87,7 +91,9 @@ struct GemmArgs {
     // choose_tile decides
     int tile = 0;
     // int8 weights (WKind::I8) in 16-row tiles: [ceil(N / 16)][K / 64][16][64] bytes, so that a
-    // 1 KB block holds one K group of 16 consecutive rows (ldw = K); 0: rows of ldw bytes
+    // 1 KB block holds one K group of 16 consecutive rows (ldw = K); 0: rows of ldw bytes. With a
+    // 4-bit kind (group scales): the weights expanded to int8 in those tiles (mq_expand_weight_w4),
+    // read by the wide kernel only; wz then only tells uint4 asymmetric (non-null) from signed
     int wtile = 0;
     // activation codes (qa) in the same 16-row tiles, [ceil(M / 16)][K / 64][16][64] (lda = K):
     // written so by the whole-linear entries when the wide kernel runs their product

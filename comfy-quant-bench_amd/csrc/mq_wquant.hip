@@ -203,7 +203,47 @@ __global__ void __launch_bounds__(256) tile16_kernel(const uint8_t* w, int64_t l
     }
 }
 
+// Packed 4-bit weights [N, K/2] (row stride ldw bytes) expanded to int8 in the same 16-row tiles,
+// one thread per 16-byte unit as in tile16_kernel. A unit holds 16 consecutive k of one row and
+// K group g (its 8 packed bytes); value v = q - z (uint4 with zero-point nibble z of group g) or
+// the signed nibble, then by layout: 0 (the group GEMM's int8 activation layout) negated in odd
+// groups, 2 (its x16 int4 layout) 16 * v for signed weights, 3 (row scale) v as it is.
+__global__ void __launch_bounds__(256) expand_w4_kernel(const uint8_t* qw, int64_t ldw, const uint8_t* wz,
+                                                       int64_t ldwz, int64_t N, int64_t K, int layout,
+                                                       uint8_t* out) {
+    const int64_t G = K / 64, units = (N + 15) / 16 * 16 * (K / 16);
+    for (int64_t u = blockIdx.x * int64_t(256) + threadIdx.x; u < units; u += int64_t(gridDim.x) * 256) {
+        const int64_t chunk = u & 3, row = (u >> 2) & 15, g = (u >> 6) % G, band = (u >> 6) / G;
+        const int64_t n = band * 16 + row;
+        uint32_t o[4] = {0u, 0u, 0u, 0u};
+        if (n < N) {
+            const uint2 w = *reinterpret_cast<const uint2*>(qw + n * ldw + g * 32 + chunk * 8);
+            const int z = wz ? (wz[n * ldwz + (g >> 1)] >> (4 * (g & 1))) & 15 : 0;
+            const bool neg = layout == 0 && (g & 1);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t byte = (e < 8 ? w.x >> (8 * (e >> 1)) : w.y >> (8 * ((e - 8) >> 1))) & 0xffu;
+                const int q = (byte >> (4 * (e & 1))) & 15;
+                int v = wz ? q - z : (q >= 8 ? q - 16 : q);
+                if (neg) v = -v;
+                if (layout == 2 && !wz) v *= 16;
+                o[e >> 2] |= (static_cast<uint32_t>(v) & 0xffu) << (8 * (e & 3));
+            }
+        }
+        *reinterpret_cast<uint4*>(out + u * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
 }  // namespace
+
+int launch_expand_weight_w4(const uint8_t* qw, int64_t ldw, const uint8_t* wz, int64_t ldwz, int64_t N, int64_t K,
+                            int layout, uint8_t* out, hipStream_t stream) {
+    const int64_t units = (N + 15) / 16 * 16 * (K / 16);
+    const int64_t blocks = std::min<int64_t>((units + 255) / 256, 65536);
+    hipLaunchKernelGGL(expand_w4_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, qw, ldw, wz, ldwz,
+                       N, K, layout, out);
+    return launch_status("expand_weight_w4");
+}
 
 int launch_tile_weight_i8(const uint8_t* w, int64_t ldw, int64_t N, int64_t K, uint8_t* out, hipStream_t stream) {
     const int64_t units = (N + 15) / 16 * 16 * (K / 16);

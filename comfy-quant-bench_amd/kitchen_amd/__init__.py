@@ -12,9 +12,11 @@ keyword arguments, executed by hand-written HIP kernels in `libmq.so` through it
 from . import weights
 from ._lib import LIB_PATH, MQError, load
 from .ops import (
+    ExpandedW4,
     PreparedW4A8,
     convrot_w4a4_linear,
     decode_w4a8_codebook_weight,
+    expand_w4_weight,
     gemm_rowscale,
     gemm_rowscale_acc,
     gemm_w4_group,
@@ -39,6 +41,7 @@ from .weights import (
 __all__ = [
     "LIB_PATH", "MQError", "load", "weights",
     "convrot_w4a4_linear", "w4a8_int8_linear", "int8_linear", "int8_rowscale_linear", "PreparedW4A8",
+    "ExpandedW4", "expand_w4_weight", "tile_int8_weight", "is_tile16",
     "quantize_int4_rowwise_convrot64", "quantize_int8_rowwise_convrot", "rotate_quantize",
     "swiglu_quantize_int4_rowwise_convrot64", "decode_w4a8_codebook_weight",
     "gemm_w4_group", "gemm_w4_group_partials", "gemm_rowscale", "gemm_rowscale_acc",

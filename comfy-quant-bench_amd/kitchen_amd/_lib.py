@@ -11,7 +11,7 @@ import os
 
 import torch  # noqa: F401  (must be imported before the library is loaded)
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmq.so")
 
@@ -43,6 +43,7 @@ _SIGNATURES = {
     "mq_gemm_rowscale_ws": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_int, c_vp, c_int, c_i64, c_i64,
                              c_i64, c_i64, c_vp, c_i64, c_vp], c_int),
     "mq_tile_weight_i8": ([c_vp, c_i64, c_i64, c_i64, c_vp, c_vp], c_int),
+    "mq_expand_weight_w4": ([c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_int, c_vp, c_vp], c_int),
     "mq_gemm_rowscale_acc": ([c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_vp], c_int),
     "mq_linear_workspace_bytes": ([c_i64, c_i64, c_i64], c_i64),
     "mq_linear_w4_group": ([c_vp, c_int, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp,
@@ -60,6 +61,8 @@ Q_BYTES, Q_PACKED, Q_X16ALT = 0, 1, 2
 SWIGLU_NONE, SWIGLU_FUSED, SWIGLU_EAGER = 0, 1, 2
 W8_TILE16 = 0x100            # wbits flag: int8 weights in 16-row tiles (include/mq.h)
 ACT_I8, ACT_I4, ACT_X16ALT = 0, 1, 2
+W4_EXPANDED = 0x100          # act_mode / act_bits flag: 4-bit weights expanded to int8 tiles
+W4X_ROW = 3                  # mq_expand_weight_w4 layout for the row-scale GEMMs
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 64 << 20   # MQ_NOALLOC_SCRATCH_BYTES
 DTYPE_CODE = {torch.bfloat16: DT_BF16, torch.float16: DT_F16, torch.float32: DT_F32}

@@ -35,6 +35,7 @@ torch on the input's device, and the HIP kernels run asynchronously on the curre
 """
 from __future__ import annotations
 
+import os
 import weakref
 
 import torch
@@ -216,7 +217,7 @@ def _check_w4_group(qa, qweight, wscales, wzeros, n, group_size):
 
 
 def _check_w4_group_weights(qweight, wscales, wzeros, n, k, group_size):
-    if qweight.shape != (n, k // 2) or qweight.element_size() != 1:
+    if qweight is not None and (qweight.shape != (n, k // 2) or qweight.element_size() != 1):
         raise ValueError(f"qweight must be 8-bit [{n}, {k // 2}]")
     groups = k // group_size
     if wscales is not None and (wscales.dtype != torch.float16 or wscales.shape[0] != n
@@ -279,16 +280,26 @@ def gemm_w4_group(qa, sa, qweight, wscales, wzeros, bias, n: int, group_size: in
     in out_dtype (bf16, fp16 or fp32); bias in its own floating-point type or None.
 
     act_mode: ACT_I8 int8 codes, ACT_I4 int4 codes one per byte, ACT_X16ALT the layout written by
-    rotate_quantize(..., packed=Q_X16ALT). Small M splits K over a torch-allocated workspace."""
+    rotate_quantize(..., packed=Q_X16ALT). Small M splits K over a torch-allocated workspace.
+    qweight may be the ExpandedW4 of the weights for act_mode (M > 4 rows; wzeros is then not read)."""
     m, k = qa.shape
-    _check_w4_group(qa, qweight, wscales, wzeros, n, group_size)
     y = torch.empty((m, n), dtype=out_dtype, device=qa.device)
-    ldwz = wzeros.stride(0) if wzeros is not None else 0
     work = _workspace(m, n, k, qa.device)
-    _lib.call("mq_gemm_w4_group_ws", qa.data_ptr(), qa.stride(0), sa.data_ptr(), qweight.data_ptr(),
-              qweight.stride(0), wscales.data_ptr(), wscales.stride(0), _lib.ptr(wzeros), ldwz, int(group_size),
-              int(act_mode), *_bias_args(bias), y.data_ptr(), _lib.dtype_code(out_dtype), y.stride(0), m, n, k,
-              _lib.ptr(work), 0 if work is None else work.numel(), _lib.stream_of(qa))
+    if isinstance(qweight, ExpandedW4):
+        if qweight.layout != act_mode or (qweight.n, qweight.k) != (n, k):
+            raise ValueError(f"expanded weights for layout {qweight.layout} [{qweight.n}, {qweight.k}] "
+                             f"do not serve act_mode {act_mode} [{n}, {k}]")
+        _check_w4_group(qa, None, wscales, None, n, group_size)
+        qptr, ldw, mode = qweight.tiles.data_ptr(), k, int(act_mode) | _lib.W4_EXPANDED
+        zptr, ldwz = (qweight.tiles.data_ptr() if qweight.asym else None), 0   # non-null: uint4 (not read)
+    else:
+        _check_w4_group(qa, qweight, wscales, wzeros, n, group_size)
+        qptr, ldw, mode = qweight.data_ptr(), qweight.stride(0), int(act_mode)
+        zptr, ldwz = _lib.ptr(wzeros), (wzeros.stride(0) if wzeros is not None else 0)
+    _lib.call("mq_gemm_w4_group_ws", qa.data_ptr(), qa.stride(0), sa.data_ptr(), qptr, ldw, wscales.data_ptr(),
+              wscales.stride(0), zptr, ldwz, int(group_size), mode, *_bias_args(bias), y.data_ptr(),
+              _lib.dtype_code(out_dtype), y.stride(0), m, n, k, _lib.ptr(work), 0 if work is None else work.numel(),
+              _lib.stream_of(qa))
     return y
 
 
@@ -325,8 +336,94 @@ def tile_int8_weight(weight: torch.Tensor) -> torch.Tensor:
     return out
 
 
+# --------------------------------------------------------------------------- expanded 4-bit weights
+
+class ExpandedW4:
+    """Packed 4-bit weights expanded once to int8 in 16-row tiles (mq_expand_weight_w4).
+
+    tiles   int8 [ceil(N / 16), K / 64, 16, 64]
+    layout  _lib.ACT_I8 / _lib.ACT_X16ALT: for the group GEMMs with that activation layout (the
+            bytes their in-kernel unpack would store, zero-point and sign included);
+            _lib.W4X_ROW: an int8 weight for the row-scale GEMMs (the signed codes)
+    asym    uint4 weights with zero-points (folded into the bytes) rather than signed int4
+The GEMMs give the packed weights' results bit for bit from it, without the per-use unpack, at
+twice the packed weight's memory."""
+
+    __slots__ = ("tiles", "layout", "asym", "n", "k")
+
+    def __init__(self, tiles: torch.Tensor, layout: int, asym: bool, n: int, k: int):
+        self.tiles, self.layout, self.asym, self.n, self.k = tiles, int(layout), bool(asym), int(n), int(k)
+
+
+def expand_w4_weight(qweight: torch.Tensor, wzeros=None, layout: int = _lib.ACT_I8) -> ExpandedW4:
+    """qweight 8-bit [N, K/2] packed 4-bit codes (uint4 with wzeros packed uint4 [N, ceil(K/128)],
+    or signed int4 when wzeros is None) -> ExpandedW4 for `layout` (see ExpandedW4)."""
+    if qweight.dim() != 2 or qweight.element_size() != 1:
+        raise ValueError(f"qweight must be 8-bit [N, K/2], got {qweight.dtype} {list(qweight.shape)}")
+    if layout not in (_lib.ACT_I8, _lib.ACT_X16ALT, _lib.W4X_ROW):
+        raise ValueError(f"layout must be ACT_I8, ACT_X16ALT or W4X_ROW, got {layout}")
+    n, k = qweight.shape[0], qweight.shape[1] * 2
+    qw = qweight if qweight.stride(1) == 1 and qweight.stride(0) % 8 == 0 else qweight.contiguous()
+    zz = None
+    if wzeros is not None:
+        if wzeros.element_size() != 1 or wzeros.shape[0] != n or wzeros.shape[1] < (k // 64 + 1) // 2:
+            raise ValueError(f"zero-points must be packed uint4 [{n}, {(k // 64 + 1) // 2}]")
+        zz = wzeros if wzeros.stride(1) == 1 else wzeros.contiguous()
+    out = torch.empty(((n + 15) // 16, k // 64, 16, 64), dtype=torch.int8, device=qweight.device)
+    _lib.call("mq_expand_weight_w4", qw.data_ptr(), qw.stride(0), _lib.ptr(zz), 0 if zz is None else zz.stride(0),
+              n, k, int(layout), out.data_ptr(), _lib.stream_of(qw))
+    return ExpandedW4(out, layout, zz is not None, n, k)
+
+
+# The linears run their 4-bit weights from an int8 expansion wherever the packed weights would run
+# on the wide kernel too, so that the results are the same bits either way: group scales above 128
+# rows (fewer rows run on the 128 x 128 few-row kernel, whose group epilogue rounds differently),
+# row scales above the GEMV's 4 rows (exact int32 sums on every kernel). The GEMV reads the packed
+# bytes: it is bound by their HBM traffic. The expansion is made on a weight's first such call and
+# kept until the tensor it was made from (its base tensor, for a view) is freed, for as long as that
+# weight's storage and version are unchanged. KITCHEN_AMD_EXPAND_W4=0 (or EXPAND_W4 = False) keeps
+# every call on the packed weights.
+EXPAND_W4 = os.environ.get("KITCHEN_AMD_EXPAND_W4", "1") != "0"
+GEMV_ROWS = 4
+FEW_ROWS = 128
+_EXPANDED: dict = {}
+
+
+def _expansion(qweight, wzeros, layout: int, m: int, k: int, wscales=None):
+    """The cached ExpandedW4 of qweight for `layout` when a product of m rows reads one (the wide
+    kernel's conditions: K >= 192, K groups in pairs for the group scales' loads, under 2 GiB),
+    else None."""
+    n = qweight.shape[0]
+    if not EXPAND_W4 or m <= (GEMV_ROWS if layout == _lib.W4X_ROW else FEW_ROWS) or k < 192 or k % 64 or (n + 15) // 16 * 16 * k >= 1 << 31 \
+            or (m + 15) // 16 * 16 * k >= 1 << 31:
+        return None
+    if wscales is not None and (wscales.stride(0) % 2 or wscales.data_ptr() % 4):
+        return None
+    root = qweight._base if qweight._base is not None else qweight
+    zroot = None if wzeros is None else (wzeros._base if wzeros._base is not None else wzeros)
+    key = (qweight.data_ptr(), tuple(qweight.shape), tuple(qweight.stride()),
+           0 if wzeros is None else wzeros.data_ptr(), int(layout))
+    sig = (qweight._version, 0 if wzeros is None else wzeros._version, id(zroot))
+    per = _EXPANDED.get(id(root))
+    hit = None if per is None else per.get(key)
+    if hit is not None and hit[0] == sig:
+        return hit[1]
+    if torch.cuda.is_current_stream_capturing():
+        return None   # nothing is allocated under capture: the packed weights, unless expanded before
+    if per is None:
+        per = _EXPANDED[id(root)] = {}
+        weakref.finalize(root, _EXPANDED.pop, id(root), None)
+    ex = expand_w4_weight(qweight, wzeros, layout)
+    per[key] = (sig, ex)
+    return ex
+
+
 def _weight_args(qweight, n: int, k: int, wbits: int):
     """(ldw, wbits) of the row-scale entries for [N, K'] rows or the 16-row tile layout."""
+    if isinstance(qweight, ExpandedW4):
+        if qweight.layout != _lib.W4X_ROW or (qweight.n, qweight.k) != (n, k):
+            raise ValueError("the row-scale GEMMs take the W4X_ROW expansion of an [N, K/2] weight")
+        return k, 8 | _lib.W8_TILE16
     if is_tile16(qweight):
         if wbits != 8 or qweight.element_size() != 1:
             raise ValueError("the 16-row tile layout holds int8 weights (wbits 8)")
@@ -413,18 +510,25 @@ def _linear_w4_group(x, swiglu, cg, act_bits, qweight, wscales, wzeros, bias, n,
     """rotate + quantize + group GEMM in one library call (mq_linear_w4_group)."""
     x2, swiglu = _linear_input(x, swiglu, k)
     m = x2.shape[0]
-    qw = qweight.contiguous()
-    zz = None if wzeros is None else wzeros.contiguous()
-    _check_w4_group_weights(qw, wscales, zz, n, k, INT4_GROUP_SIZE)
+    _check_w4_group_weights(qweight, wscales, wzeros, n, k, INT4_GROUP_SIZE)
     b = _bias(bias, n, x2.device)
     y = torch.empty((m, n), dtype=out_dtype, device=x2.device)
     if m == 0:
         return y
     work = _linear_workspace(m, n, k, x2.device)
-    _lib.call("mq_linear_w4_group", x2.data_ptr(), _lib.dtype_code(x2.dtype), x2.stride(0), int(cg or 0),
-              int(act_bits), int(swiglu), qw.data_ptr(), qw.stride(0), wscales.data_ptr(), wscales.stride(0),
-              _lib.ptr(zz), 0 if zz is None else zz.stride(0), *_bias_args(b), y.data_ptr(),
-              _lib.dtype_code(out_dtype), y.stride(0), m, n, k, work.data_ptr(), work.numel(), _lib.stream_of(x2))
+    xw = _expansion(qweight, wzeros, _lib.ACT_X16ALT if act_bits == 4 else _lib.ACT_I8, m, k, wscales)
+    if xw is not None:
+        qptr, ldw, ab = xw.tiles.data_ptr(), k, int(act_bits) | _lib.W4_EXPANDED
+        zptr, ldwz = (xw.tiles.data_ptr() if xw.asym else None), 0   # non-null: uint4 (not read)
+    else:
+        qw = qweight.contiguous()
+        zz = None if wzeros is None else wzeros.contiguous()
+        qptr, ldw, ab = qw.data_ptr(), qw.stride(0), int(act_bits)
+        zptr, ldwz = _lib.ptr(zz), (0 if zz is None else zz.stride(0))
+    _lib.call("mq_linear_w4_group", x2.data_ptr(), _lib.dtype_code(x2.dtype), x2.stride(0), int(cg or 0), ab,
+              int(swiglu), qptr, ldw, wscales.data_ptr(), wscales.stride(0), zptr, ldwz, *_bias_args(b),
+              y.data_ptr(), _lib.dtype_code(out_dtype), y.stride(0), m, n, k, work.data_ptr(), work.numel(),
+              _lib.stream_of(x2))
     return y
 
 
@@ -436,6 +540,11 @@ def _linear_rowscale(x, swiglu, cg, act_bits, qweight, wbits, wscales, bias, n, 
     wbytes = k // 2 if wbits == 4 else k
     if not is_tile16(qw) and (qw.shape != (n, wbytes) or qw.element_size() != 1):
         raise ValueError(f"weight must be 8-bit [{n}, {wbytes}]")
+    if wbits == 4:
+        # signed int4 rows: their int8 expansion where the wide kernel reads it (same int32 sums)
+        xw = _expansion(qweight, None, _lib.W4X_ROW, m, k)
+        if xw is not None:
+            qw, wbits = xw.tiles, 8
     ldw, wbits = _weight_args(qw, n, k, int(wbits))
     b = _bias(bias, n, x2.device)
     y = torch.empty((m, n), dtype=out_dtype, device=x2.device)

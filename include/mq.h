@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define MQ_ABI_VERSION 9
+#define MQ_ABI_VERSION 10
 
 enum {
     MQ_OK = 0,
@@ -187,6 +187,37 @@ int mq_decode_w4a8_codebook(const void* qdata, int64_t ldq, const void* s_rel, i
                             float* row_scale, void* stream);
 
 /*
+ * Load-time expansion of packed 4-bit weights [N, K/2] (uint4 with zero-points wz, or signed int4
+ * when wz is NULL) to int8 in the 16-row tiles of MQ_W8_TILE16, [ceil(N/16)][K/64][16][64] bytes
+ * (rows past N zero). Byte (n, k) is v = q - z[n, k/64] (uint4) or the signed nibble, then by
+ * layout:
+ *   MQ_ACT_I8      v, negated where (k / 64) is odd: for the group GEMMs with act_mode MQ_ACT_I8
+ *   MQ_ACT_X16ALT  v for uint4, 16 * v for signed int4: for act_mode MQ_ACT_X16ALT
+ *   MQ_W4X_ROW     v: an int8 weight for the row-scale GEMMs (wbits 8 | MQ_W8_TILE16), the
+ *                  shipped ConvRot W4A4 weight with the same int32 sums as its packed form
+ * These are the bytes the group GEMM's in-kernel unpack stores to LDS for that activation layout,
+ * so a GEMM on them gives the packed GEMM's results bit for bit; the GEMM then reads them by the
+ * same DMA as the activation codes and does no unpack (half the weight bytes per K group more,
+ * none of the unpack's VALU work). No counterpart in the reference (whose kernel unpacks per use,
+ * experiments/qwen21-kernel/kernels/g64_gemm6.cu:93-343): it trades twice the packed weight's
+ * memory for that work. Run once per weight.
+ *   qw   packed 4-bit [N, K/2], stride ldw bytes (ldw % 8 == 0, 8-byte aligned)
+ *   wz   packed uint4 zero-points [N, ceil(K/128)], stride ldwz, or NULL (signed int4)
+ *   out  (N + 15) / 16 * 16 * K bytes, 16-byte aligned, under 2 GiB
+ * Requires K % 64 == 0.
+ */
+#define MQ_W4X_ROW 3
+int mq_expand_weight_w4(const uint8_t* qw, int64_t ldw, const uint8_t* wz, int64_t ldwz, int64_t N, int64_t K,
+                        int layout, int8_t* out, void* stream);
+
+/* act_mode flag of the group GEMMs (act_bits flag of the whole group linears): qw holds the
+ * expansion of mq_expand_weight_w4 for that activation layout (ldw ignored). wz is then not read;
+ * non-NULL marks weights that were uint4 asymmetric (their MQ_ACT_X16ALT scaling differs from signed
+ * int4). Read by the wide kernel only: M > 4 rows (fewer rows take the packed weights), K >= 192,
+ * the expanded array under 2 GiB; the group-scale epilogue only (not the partials entry). */
+#define MQ_W4_EXPANDED 0x100
+
+/*
  * Quantized GEMM with per-group weight scales (W4A8 asym / W4A4 sym, configs' scheme):
  *   P[g,m,n] = sum_{k in group g} qa[m,k] * (w[n,k] - z[n,g])            (exact int32)
  *   y[m,n]   = T( sa[m] * sum_g ws[n,g] * P[g,m,n] + bias[n] )      (fp32, one rounding to T)
@@ -198,7 +229,8 @@ int mq_decode_w4a8_codebook(const void* qdata, int64_t ldq, const void* s_rel, i
  *
  *   qa    activation codes [M, K] in layout act_mode (MQ_ACT_*), stride lda bytes (lda % 16 == 0)
  *   sa    fp32 [M]
- *   qw    packed 4-bit weights [N, K/2], stride ldw bytes (ldw % 16 == 0)
+ *   qw    packed 4-bit weights [N, K/2], stride ldw bytes (ldw % 16 == 0), or with
+ *         act_mode | MQ_W4_EXPANDED their int8 expansion (mq_expand_weight_w4)
  *   ws    fp16 [N, K/group], stride ldws elements
  *   wz    packed uint4 zero-points [N, ceil(K/group/2)], stride ldwz bytes; NULL = signed
  *         symmetric int4 weights (no zero-point)
@@ -301,7 +333,8 @@ int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t 
  *
  *   x       [M, K] (swiglu = MQ_SWIGLU_NONE) or gate | up [M, 2K] (MQ_SWIGLU_FUSED / MQ_SWIGLU_EAGER,
  *           the activation of mq_swiglu_rotquant in that mode) of type x_dtype, stride ldx
- *   hblock  Hadamard block (0, 16, 64, 256); act_bits 8 or 4 (per-token int8 / int4 activations)
+ *   hblock  Hadamard block (0, 16, 64, 256); act_bits 8 or 4 (per-token int8 / int4 activations),
+ *           for mq_linear_w4_group | MQ_W4_EXPANDED with expanded weights
  *   weights, scales, bias, y as mq_gemm_w4_group / mq_gemm_rowscale
  *   workspace  device memory, 256-byte aligned: the codes (M rounded up to 16 rows, K bytes
  *           each, in rows or in the 16-row tiles of MQ_W8_TILE16 wherever the product runs on the

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mq_abi_version() == 9
+    assert lib.mq_abi_version() == 10
 
 
 def _err(lib):
@@ -216,3 +216,29 @@ def test_linear_validation_rejects_before_launch(lib):
     assert lib.mq_linear_rowscale(a, 0, 3072, 256, 5, 0, a, 3072, 8, a, None, 0, a, 0, 1024, 64, 1024, 3072, a,
                                   need, None) == -1
     assert "act_bits" in _err(lib)
+
+
+def test_expanded_w4_validation(lib):
+    # 4-bit weights expanded to int8 tiles: layouts 0 (int8 codes), 2 (x16 int4 codes), 3 (row scale)
+    a = 1 << 20
+    assert lib.mq_expand_weight_w4(a, 96, None, 0, 8, 192, 1, a, None) == -1
+    assert "layout" in _err(lib)
+    assert lib.mq_expand_weight_w4(a, 104, None, 0, 8, 200, 0, a, None) == -1
+    assert "K % 64" in _err(lib)
+    assert lib.mq_expand_weight_w4(a, 100, None, 0, 8, 192, 0, a, None) == -1
+    assert "ldw" in _err(lib)
+    assert lib.mq_expand_weight_w4(a, 96, a, 1, 8, 192, 2, a, None) == -1
+    assert "ldwz" in _err(lib)
+    assert lib.mq_expand_weight_w4(None, 96, None, 0, 0, 192, 3, None, None) == 0
+    # the group GEMMs take them for the int8 and x16 int4 activation layouts, K >= 192
+    assert lib.mq_gemm_w4_group(a, 256, a, a, 0, a, 4, None, 0, 64, 1 | 0x100, None, 0, a, 0, 64, 8, 64, 256,
+                                None) == -1
+    assert "MQ_ACT_I8 and MQ_ACT_X16ALT" in _err(lib)
+    assert lib.mq_gemm_w4_group(a, 128, a, a, 0, a, 2, None, 0, 64, 0x100, None, 0, a, 0, 64, 8, 64, 128, None) == -1
+    assert "K >= 192" in _err(lib)
+    assert lib.mq_gemm_w4_group_partials(a, 256, a, 128, None, 0, 64, 0x100, a, 8, 64, 256, None) == -1
+    assert "act_mode" in _err(lib)
+    # a GEMV-sized product (M <= 4) takes the packed weights: refused before anything is launched
+    assert lib.mq_linear_w4_group(a, 0, 256, 256, 8 | 0x100, 0, a, 0, a, 4, a, 2, None, 0, a, 0, 64, 2, 64, 256, a,
+                                  1 << 20, None) == -2
+    assert "wide kernel only" in _err(lib)
