@@ -44,9 +44,11 @@ RQ_M = 32760                 # video-token shape of the rotate+quantize roofline
 COPY_BYTES = 256 << 20       # calibration copy for the traffic counters
 GEMM_KERNEL = "gemm_wide_kernel"
 RQ_KERNEL = "rotquant_kernel"
-GEMV_KERNEL = "gemv_kernel"
+GEMV_KERNEL = "gemv_kernel<(mq::WKind)0"
+GEMV_I8_KERNEL = "gemv_kernel<(mq::WKind)2"
 GEMV_N = 18432               # config 1's adaLN linear at M = 1: K = 3072 -> N = 18432
 GEMV_COPIES = 10             # weight copies cycled over the calls: 305 MB, above the 256 MB MALL
+GEMV_I8_COPIES = 6           # int8 weight copies for the W8A8 GEMV: 340 MB, above the MALL
 COPY_KERNEL = "copyBuffer"
 
 
@@ -203,6 +205,66 @@ def measure_gemv(x, settle_ms: float, launches: int = 40) -> dict:
             "timing": f"HIP graph of {launches} launches over {GEMV_COPIES} weight copies, per launch"}
 
 
+def gemv_i8_inputs(x, k: int):
+    """The M = 1 W8A8 GEMM's operands (config 4's adaLN linear on W8A8): the quantized first
+    activation row and GEMV_I8_COPIES random int8 weight sets [GEMV_N, k] in the 16-row tiles the
+    stack holds them in, with fp32 per-row scales."""
+    import torch
+
+    import kitchen_amd as ck
+
+    dev = x.device
+    gen = torch.Generator(device=dev).manual_seed(7)
+    qa, sa = ck.quantize_int8_rowwise_convrot(x[:1], 256)
+    copies = [(ck.tile_int8_weight(torch.randint(-127, 128, (GEMV_N, k), generator=gen, device=dev, dtype=torch.int8)),
+               torch.rand(GEMV_N, generator=gen, device=dev) * 2e-4 + 3e-4)
+              for _ in range(GEMV_I8_COPIES)]
+    bias = torch.zeros(GEMV_N, dtype=torch.bfloat16, device=dev)
+    return qa, sa, copies, bias
+
+
+def gemv_i8_bytes(k: int) -> int:
+    """Algorithmic bytes of one M = 1 W8A8 call: int8 weights, fp32 row scales, the int8 activation
+    row and its scale, bias and bf16 output."""
+    return GEMV_N * k + 4 * GEMV_N + k + 4 + 2 * GEMV_N + 2 * GEMV_N
+
+
+def measure_gemv_i8(x, settle_ms: float, launches: int = 36) -> dict:
+    """The M = 1 W8A8 GEMM (the int8 row-scale GEMV) at the adaLN shape, timed as measure_gemv:
+    weight copies cycled past the MALL, the calls replayed from one HIP graph."""
+    import torch
+
+    import kitchen_amd as ck
+
+    k = x.shape[1]
+    qa, sa, copies, bias = gemv_i8_inputs(x, k)
+
+    def calls():
+        for i in range(launches):
+            q8, ws = copies[i % GEMV_I8_COPIES]
+            ck.gemm_rowscale(qa, sa, q8, ws, bias, GEMV_N, 8)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        calls()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        calls()
+    ms = time_launches(graph.replay, 5, settle_ms=settle_ms) / launches
+    nbytes = gemv_i8_bytes(k)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    del graph, copies
+    torch.cuda.empty_cache()
+    return {"bound": "hbm", "kernel": "gemv_kernel<I8,RowScale,0,1> (weights in 16-row tiles)", "M": 1, "K": k,
+            "N": GEMV_N, "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": nbytes, "avg_launch_ms": round(ms, 5),
+            "weight_copies": GEMV_I8_COPIES,
+            "timing": f"HIP graph of {launches} launches over {GEMV_I8_COPIES} weight copies, per launch"}
+
+
 def _aux(fn) -> dict:
     """An auxiliary measurement of the bench line: its result, or {"error": ...} if it raised, so
     that the headline figures are still printed (the error names what to look at)."""
@@ -243,6 +305,10 @@ def kernels_child(args) -> int:
     for qdc, s16c, zpc in copies[:3]:
         ck.gemm_w4_group(gqa, gsa, qdc, s16c, zpc, gbias, GEMV_N)
     del copies
+    gqa, gsa, copies, gbias = gemv_i8_inputs(x, k)
+    for q8c, wsc in copies[:3]:
+        ck.gemm_rowscale(gqa, gsa, q8c, wsc, gbias, GEMV_N, 8)
+    del copies
     src = torch.empty(COPY_BYTES // 4, dtype=torch.int32, device=x.device)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -260,7 +326,7 @@ def _counter_means(csv_path: str, counter: str) -> dict:
         if row.get("Counter_Name") != counter:
             continue
         name = row["Kernel_Name"]
-        for key in (GEMM_KERNEL, RQ_KERNEL, GEMV_KERNEL, COPY_KERNEL):
+        for key in (GEMM_KERNEL, RQ_KERNEL, GEMV_KERNEL, GEMV_I8_KERNEL, COPY_KERNEL):
             if key in name:
                 sums.setdefault(key, []).append((int(row.get("Grid_Size") or 0), float(row["Counter_Value"])))
     out = {}
@@ -304,7 +370,7 @@ def measure_traffic(args) -> dict:
     f_fetch = COPY_BYTES / (out["FETCH_SIZE"][COPY_KERNEL] * 1024.0)
     f_write = COPY_BYTES / (out["WRITE_SIZE"][COPY_KERNEL] * 1024.0)
     res = {"fetch_scale": round(f_fetch, 4), "write_scale": round(f_write, 4)}
-    for key in (GEMM_KERNEL, RQ_KERNEL, GEMV_KERNEL):
+    for key in (GEMM_KERNEL, RQ_KERNEL, GEMV_KERNEL, GEMV_I8_KERNEL):
         if key in out["FETCH_SIZE"] and key in out["WRITE_SIZE"]:
             fetch = out["FETCH_SIZE"][key] * 1024.0 * f_fetch
             write = out["WRITE_SIZE"][key] * 1024.0 * f_write
@@ -553,6 +619,7 @@ def main() -> int:
 
     # ---- M = 1 GEMV (config 1's adaLN shape), weights cycled past the MALL
     gemv = _aux(lambda: measure_gemv(x, args.settle_ms / 2))
+    gemv_i8 = _aux(lambda: measure_gemv_i8(x, args.settle_ms / 2))
 
     # ---- the mixed W4A4 / W8A8 MMDiT linear stack (60 blocks x 14 linears)
     stack = None if args.no_stack else _aux(measure_stack)
@@ -562,6 +629,8 @@ def main() -> int:
     rq_traffic = traffic.get(RQ_KERNEL, {}).get("bytes") if traffic else None
     if "error" not in gemv:
         gemv["traffic"] = traffic.get(GEMV_KERNEL, {}).get("bytes") if traffic else None
+    if "error" not in gemv_i8:
+        gemv_i8["traffic"] = traffic.get(GEMV_I8_KERNEL, {}).get("bytes") if traffic else None
 
     result = {
         "metric": METRIC,
@@ -593,6 +662,7 @@ def main() -> int:
                               "traffic": rq_traffic, "avg_launch_ms": round(ms_rq, 5),
                               "north_star_M_launch_ms": round(ms_rq_ns, 5)},
         "gemv_roofline": gemv,
+        "gemv_i8_roofline": gemv_i8,
     }
     if stack is not None:
         result["c4_linear_stack"] = stack
