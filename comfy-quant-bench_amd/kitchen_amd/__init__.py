@@ -26,6 +26,7 @@ from .ops import (
     is_tile16,
     quantize_int4_rowwise_convrot64,
     quantize_int8_rowwise_convrot,
+    release_expanded_weights,
     rotate_quantize,
     swiglu_quantize_int4_rowwise_convrot64,
     tile_int8_weight,
@@ -41,7 +42,7 @@ from .weights import (
 __all__ = [
     "LIB_PATH", "MQError", "load", "weights",
     "convrot_w4a4_linear", "w4a8_int8_linear", "int8_linear", "int8_rowscale_linear", "PreparedW4A8",
-    "ExpandedW4", "expand_w4_weight", "tile_int8_weight", "is_tile16",
+    "ExpandedW4", "expand_w4_weight", "release_expanded_weights", "tile_int8_weight", "is_tile16",
     "quantize_int4_rowwise_convrot64", "quantize_int8_rowwise_convrot", "rotate_quantize",
     "swiglu_quantize_int4_rowwise_convrot64", "decode_w4a8_codebook_weight",
     "gemm_w4_group", "gemm_w4_group_partials", "gemm_rowscale", "gemm_rowscale_acc",

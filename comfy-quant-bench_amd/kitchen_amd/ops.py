@@ -381,8 +381,10 @@ def expand_w4_weight(qweight: torch.Tensor, wzeros=None, layout: int = _lib.ACT_
 # row scales above the GEMV's 4 rows (exact int32 sums on every kernel). The GEMV reads the packed
 # bytes: it is bound by their HBM traffic. The expansion is made on a weight's first such call and
 # kept until the tensor it was made from (its base tensor, for a view) is freed, for as long as that
-# weight's storage and version are unchanged. KITCHEN_AMD_EXPAND_W4=0 (or EXPAND_W4 = False) keeps
-# every call on the packed weights.
+# weight's storage and version are unchanged; it costs 1 byte per weight element beside the packed
+# 0.5 (release_expanded_weights() drops them all). A HIP graph that captured a linear keeps the
+# expansion it captured: re-capture after changing a weight in place. KITCHEN_AMD_EXPAND_W4=0 (or
+# EXPAND_W4 = False) keeps every call on the packed weights.
 EXPAND_W4 = os.environ.get("KITCHEN_AMD_EXPAND_W4", "1") != "0"
 GEMV_ROWS = 4
 FEW_ROWS = 128
@@ -416,6 +418,14 @@ def _expansion(qweight, wzeros, layout: int, m: int, k: int, wscales=None):
     ex = expand_w4_weight(qweight, wzeros, layout)
     per[key] = (sig, ex)
     return ex
+
+
+def release_expanded_weights() -> int:
+    """Drop every cached int8 expansion of 4-bit weights (they are made again on their weights'
+    next large-M calls); returns how many were held."""
+    held = sum(len(per) for per in _EXPANDED.values())
+    _EXPANDED.clear()
+    return held
 
 
 def _weight_args(qweight, n: int, k: int, wbits: int):
