@@ -101,6 +101,31 @@ def test_noalloc_trailing_rows_with_swiglu_prologue(gpu_device):
 
 
 @pytest.mark.gpu
+def test_noalloc_with_expanded_weights(gpu_device):
+    # the weights' int8 expansion (act_bits | MQ_W4_EXPANDED) through the scratch: the workspace
+    # entry's bits, and those of the packed weights (the wide kernel runs both at M = 300)
+    m, n, k = 300, 1536, 3072
+    print(f"[noalloc] expanded weights M={m} N={n} K={k}", flush=True)
+    qd, s16, zp = _w4a8_weight(n, k, gpu_device, seed=4)
+    ex = ck.expand_w4_weight(qd, zp, _lib.ACT_I8)
+    x = synth.to_bf16_tensor(synth.activations(m, k, seed=5), gpu_device)
+    bias = torch.randn(n, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(gpu_device)
+    y0, y1, y2 = (torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=gpu_device) for _ in range(3))
+    work = _reference(x, qd, s16, zp, bias, y0, 8)
+    args = _args(x, qd, s16, zp, bias, y1, 8 | _lib.W4_EXPANDED)
+    args[6], args[7] = ex.tiles.data_ptr(), k
+    rc = _noalloc()(*args, _lib.stream_of(x))
+    assert rc == 0, _lib.load().mq_last_error().decode()
+    args = _args(x, qd, s16, zp, bias, y2, 8 | _lib.W4_EXPANDED)
+    args[6], args[7] = ex.tiles.data_ptr(), k
+    w2 = torch.empty(_lib.load().mq_linear_workspace_bytes(m, n, k), dtype=torch.uint8, device=gpu_device)
+    _lib.call("mq_linear_w4_group", *args, w2.data_ptr(), w2.numel(), _lib.stream_of(x))
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1) and torch.equal(y1, y2)
+    del work, w2
+
+
+@pytest.mark.gpu
 def test_noalloc_when_partials_do_not_fit(gpu_device):
     # codes and scales (57.4 MB) fit the scratch; whether the split-K partials fit beside them
     # decides whether the result is the workspace entry's bit for bit. Unsplit, the same int32
