@@ -65,6 +65,27 @@ constexpr float kTieWindow = 0.5f - 0x1p-15f;
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Large outputs store their codes non-temporally (`global_store ... nt`). On MI355X the kernel's
+// traffic pattern (two 16-byte loads per lane per 1024-column chunk, one code store per chunk)
+// streams at 78 % of 8 TB/s with ordinary stores and 89 % with non-temporal ones, measured on a
+// shift-only copy of the pattern at M = 32760, K = 3072 (non-temporal loads lower it to 70 %, so
+// the loads stay ordinary). Small outputs keep ordinary stores: the GEMM that follows reads its
+// codes sooner from the caches (M = 256, K = 3072: a 21 us W8A8 linear takes 23 us with
+// non-temporal code stores). kNtCodeBytes is the output size from which the stores are
+// non-temporal.
+constexpr int64_t kNtCodeBytes = int64_t{64} << 20;
+
+__device__ __forceinline__ void store_codes(bool nt, uint8_t* p, uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+    if (nt) __builtin_nontemporal_store(u32x4{w0, w1, w2, w3}, reinterpret_cast<u32x4*>(p));
+    else *reinterpret_cast<uint4*>(p) = uint4{w0, w1, w2, w3};
+}
+__device__ __forceinline__ void store_codes(bool nt, uint8_t* p, uint32_t w0, uint32_t w1) {
+    if (nt) __builtin_nontemporal_store(u32x2{w0, w1}, reinterpret_cast<u32x2*>(p));
+    else *reinterpret_cast<uint2*>(p) = uint2{w0, w1};
+}
 
 // fp32 bits of silu(g) for every fp16 bit pattern g; specialized where the table is compiled in.
 template <int IN>
@@ -302,7 +323,7 @@ __device__ __forceinline__ void quant16(const float (&v)[16], float sg, float r,
 template <int BLK, int OUT, int NCH, int ACT, int W, int IN, bool TL>
 __global__ void __launch_bounds__(64 * kWaves)
 rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
-                uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale) {
+                uint8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, bool nt) {
     constexpr int LIMIT = OUT == 0 ? 127 : 7;
     constexpr int RPG = kWaves / W;                      // rows per workgroup step
     // Plain inputs exchange lanes and registers through LDS (rotate_chunk_lds) and leave the
@@ -461,13 +482,10 @@ rotquant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
             }
             const int col = (c * W + wr) * 1024 + seg_st * 16;
             if (col >= K) continue;
-            if constexpr (OUT == 2) {
-                const uint2 out = {word[0] | (word[1] << 16), word[2] | (word[3] << 16)};
-                *reinterpret_cast<uint2*>(qr + col / 2) = out;
-            } else {
-                const uint4 out = {word[0], word[1], word[2], word[3]};
-                *reinterpret_cast<uint4*>(qr + (tiled ? (col >> 6) * 1024 + (col & 63) : col)) = out;
-            }
+            if constexpr (OUT == 2)
+                store_codes(nt, qr + col / 2, word[0] | (word[1] << 16), word[2] | (word[3] << 16));
+            else
+                store_codes(nt, qr + (tiled ? (col >> 6) * 1024 + (col & 63) : col), word[0], word[1], word[2], word[3]);
         }
     }
 }
@@ -500,15 +518,16 @@ int launch_rq(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, void* q, int
         wgs = std::min<int64_t>(groups, static_cast<int64_t>(cus > 0 ? cus : 256) * per_cu);
     }
     if (wgs == 0) return 0;
+    const bool nt = (OUT == 2 ? M * K / 2 : M * K) >= kNtCodeBytes;
     // a row stride of 0 asks for the codes in 16-row tiles (one code per byte)
     if (OUT != 2 && ldq == 0)
         hipLaunchKernelGGL((rotquant_kernel<BLK, OUT, NCH, ACT, W, IN, OUT != 2>), dim3(static_cast<unsigned>(wgs)),
                            dim3(64 * kWaves), 0, stream, x, ldx, static_cast<int>(M), static_cast<int>(K),
-                           static_cast<uint8_t*>(q), ldq, scale);
+                           static_cast<uint8_t*>(q), ldq, scale, nt);
     else
         hipLaunchKernelGGL((rotquant_kernel<BLK, OUT, NCH, ACT, W, IN, false>), dim3(static_cast<unsigned>(wgs)),
                            dim3(64 * kWaves), 0, stream, x, ldx, static_cast<int>(M), static_cast<int>(K),
-                           static_cast<uint8_t*>(q), ldq, scale);
+                           static_cast<uint8_t*>(q), ldq, scale, nt);
     return launch_status("rotquant");
 }
 

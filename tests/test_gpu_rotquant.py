@@ -162,6 +162,35 @@ def test_config3_video_tokens_subset(gpu_device):
     assert np.array_equal(q[rows], q0) and np.array_equal(s[rows], s0)
 
 
+@pytest.fixture(scope="module")
+def large_x():
+    # [9600, 14336] (C3's MLP-down width): generated once for the cases below (about 17 s)
+    return synth.activations(9600, 14336, seed=4)
+
+
+@pytest.mark.parametrize("bits,packed", [(8, False), (4, True), (4, _lib.Q_X16ALT)])
+def test_large_output_rows_subset(gpu_device, large_x, bits, packed):
+    # outputs of 64 MiB and more take the non-temporal code stores: [9600, 14336] gives 137.6 MB
+    # of one-byte codes or 68.8 MB packed (four waves per row); a subset of rows against the
+    # oracle, and the code range on all rows
+    xb = large_x
+    m, k = xb.shape
+    print(f"[rotquant] large output M={m} K={k} bits={bits} packed={packed}", flush=True)
+    q, s = _run(xb, 256, bits, packed, gpu_device)
+    rows = np.r_[0:128, m - 128:m, np.random.default_rng(1).choice(np.arange(128, m - 128), 128, replace=False)]
+    q0, s0 = _oracle(xb[rows], 256, bits)
+    assert np.array_equal(s[rows].view(np.uint32), s0.view(np.uint32)), "scales differ"
+    if packed == _lib.Q_X16ALT:
+        sign = np.where((np.arange(k) // 64) % 2 == 1, -1, 1).astype(np.int16)
+        assert np.array_equal(q[rows].astype(np.int16), 16 * q0.astype(np.int16) * sign[None, :])
+        assert (q.view(np.int8) % 16 == 0).all()
+    elif packed:
+        assert np.array_equal(q[rows], quant.pack_i4(q0)), "packed codes differ"
+    else:
+        assert np.array_equal(q[rows], q0), "codes differ"
+        assert np.abs(q.astype(np.int16)).max(axis=1).min() == 127
+
+
 def test_deterministic(gpu_device):
     xb = synth.activations(512, 3072, seed=5)
     a = _run(xb, 256, 8, False, gpu_device)
