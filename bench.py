@@ -284,7 +284,7 @@ def kernels_child(args) -> int:
     m, k, n = args.m, args.k, args.n
     _, _, x, qd, s16, zp, bias = make_inputs(m, k, n)
     qa, sa = ck.quantize_int8_rowwise_convrot(x, 256)
-    xw = ck.expand_w4_weight(qd.view(torch.uint8), zp.view(torch.uint8), 0)   # the linear's GEMM operand
+    xw = ck.expand_w4_weight(qd.view(torch.uint8), zp.view(torch.uint8), 0, s16)   # the linear's GEMM operand
     for _ in range(3):
         ck.gemm_w4_group(qa, sa, xw, s16, None, bias, n)
     if args.with_rowscale:
@@ -603,7 +603,7 @@ def main() -> int:
     # for comparison on the packed weights themselves
     qa, sa = ck.quantize_int8_rowwise_convrot(x, 256)
     qdu, zpu = qd.view(torch.uint8), zp.view(torch.uint8)
-    xw = ck.expand_w4_weight(qdu, zpu, 0)
+    xw = ck.expand_w4_weight(qdu, zpu, 0, s16)
     ms_gemm = time_launches(lambda: ck.gemm_w4_group(qa, sa, xw, s16, None, bias, n), 20, settle_ms=args.settle_ms / 2)
     ms_gemm_packed = time_launches(lambda: ck.gemm_w4_group(qa, sa, qdu, s16, zpu, bias, n), 20,
                                    settle_ms=args.settle_ms / 4)

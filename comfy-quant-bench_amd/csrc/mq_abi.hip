@@ -269,21 +269,35 @@ int mq_tile_weight_i8(const int8_t* w, int64_t ldw, int64_t N, int64_t K, int8_t
                                  static_cast<hipStream_t>(stream));
 }
 
-int mq_expand_weight_w4(const uint8_t* qw, int64_t ldw, const uint8_t* wz, int64_t ldwz, int64_t N, int64_t K,
-                        int layout, int8_t* out, void* stream) {
+int mq_expand_weight_w4(const uint8_t* qw, int64_t ldw, const uint8_t* wz, int64_t ldwz, const uint16_t* ws,
+                        int64_t ldws, int64_t N, int64_t K, int layout, int8_t* out, void* stream) {
     clear_error();
     MQ_REQUIRE(layout == MQ_ACT_I8 || layout == MQ_ACT_X16ALT || layout == MQ_W4X_ROW,
                "expand_weight_w4: layout must be MQ_ACT_I8 (0), MQ_ACT_X16ALT (2) or MQ_W4X_ROW (3), got %d", layout);
     MQ_REQUIRE(N >= 0 && K > 0 && K % 64 == 0, "expand_weight_w4: bad shape N=%lld K=%lld (K %% 64 == 0)",
                (long long)N, (long long)K);
-    MQ_REQUIRE((N + 15) / 16 * 16 * K < (int64_t(1) << 31), "expand_weight_w4: the expanded weight must be under 2 GiB");
+    MQ_REQUIRE(mq_expanded_w4_bytes(N, K, layout) < (int64_t(1) << 31),
+               "expand_weight_w4: the expanded weight must be under 2 GiB");
     if (N == 0) return MQ_OK;
     MQ_REQUIRE(qw && out, "expand_weight_w4: null pointer");
     MQ_REQUIRE(ldw >= K / 2 && ldw % 8 == 0 && aligned(qw, 8) && aligned(out, 16),
                "expand_weight_w4: needs ldw >= K/2, ldw %% 8 == 0, an 8-byte aligned qw and a 16-byte aligned out");
     MQ_REQUIRE(!wz || ldwz >= (K / 64 + 1) / 2, "expand_weight_w4: ldwz < ceil(K/64/2)");
-    return launch_expand_weight_w4(qw, ldw, wz, ldwz, N, K, layout, reinterpret_cast<uint8_t*>(out),
-                                   static_cast<hipStream_t>(stream));
+    const bool scaled = layout != MQ_W4X_ROW;
+    MQ_REQUIRE(!scaled || (ws && ldws >= K / 64), "expand_weight_w4: the group layouts need the fp16 scales (ldws >= K/64)");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int rc = launch_expand_weight_w4(qw, ldw, wz, ldwz, N, K, layout, reinterpret_cast<uint8_t*>(out), st);
+    if (rc || !scaled) return rc;
+    return launch_expand_scales_w4(ws, ldws, N, K,
+                                   reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(out) + (N + 15) / 16 * 16 * K),
+                                   st);
+}
+
+int64_t mq_expanded_w4_bytes(int64_t N, int64_t K, int layout) {
+    if (N < 0 || K <= 0) return 0;
+    const int64_t tiles = (N + 15) / 16 * 16 * K;
+    if (layout == MQ_W4X_ROW) return tiles;
+    return tiles + (K / 64 + 3) / 4 * 4 * 16 * MQ_SCALE_PAIR_LD(N) * 4;
 }
 
 }  // extern "C"
@@ -303,7 +317,7 @@ int w4_group_args(const int8_t* qa, int64_t lda, const float* sa, const uint8_t*
         MQ_REQUIRE(act_mode != MQ_ACT_I4, "gemm_w4_group: expanded weights serve MQ_ACT_I8 and MQ_ACT_X16ALT");
         MQ_REQUIRE(K >= 192 && K % 64 == 0, "gemm_w4_group: expanded weights need K %% 64 == 0 and K >= 192 (got %lld)",
                    (long long)K);
-        MQ_REQUIRE(N >= 0 && (N + 15) / 16 * 16 * K < (int64_t(1) << 31),
+        MQ_REQUIRE(N >= 0 && mq_expanded_w4_bytes(N, K, act_mode) < (int64_t(1) << 31),
                    "gemm_w4_group: expanded weights must be under 2 GiB");
         ldw = K;
     }

@@ -58,6 +58,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float f2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 constexpr int TK = 64;
 constexpr int LAG = 3;                    // tile t's fmas run LAG MFMAs after it
@@ -168,6 +169,16 @@ __device__ __forceinline__ void map_tile(int pid, int tiles_m, int tiles_n, int&
     tn = (pid % in_group) / gsize;
 }
 
+// acc = fma(d, (neg ? -1 : 1) * fp16 half `hi` of s, acc) in one v_fma_mix_f32 with the accumulator
+// as destination (the compiler's own form leaves the destination free, and the loop's four unrolled
+// groups then end with the accumulators in other registers, restored by ~100 moves per iteration).
+__device__ __forceinline__ void fma_mix(float& acc, float d, uint32_t s, int hi, int neg) {
+    if (hi == 0 && neg == 0) asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[0,1,0]" : "+v"(acc) : "v"(d), "v"(s));
+    else if (hi == 0) asm("v_fma_mix_f32 %0, %1, -%2, %0 op_sel_hi:[0,1,0]" : "+v"(acc) : "v"(d), "v"(s));
+    else if (neg == 0) asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(acc) : "v"(d), "v"(s));
+    else asm("v_fma_mix_f32 %0, %1, -%2, %0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(acc) : "v"(d), "v"(s));
+}
+
 // Buffer resource over [base, base + bytes): loads whose vector offset lies outside the range
 // return 0 (the scalar offset is added to the address but is not part of that check, so it must
 // keep every in-range access inside the buffer). Invalid rows are given the vector offset kOob.
@@ -203,6 +214,12 @@ typedef uint32_t u2v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u2v asm_ld64(u4v d, int voff, int soff) {
     u2v v;
     asm volatile("s_nop 4\n\tbuffer_load_dwordx2 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
+    return v;
+}
+typedef uint32_t u3v __attribute__((ext_vector_type(3)));
+__device__ __forceinline__ u3v asm_ld96(u4v d, int voff, int soff) {
+    u3v v;
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx3 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff) : "memory");
     return v;
 }
 __device__ __forceinline__ uint32_t asm_ld32(u4v d, int voff, int soff) {
@@ -270,6 +287,17 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     constexpr bool kHasZ = WK == WKind::U4Asym && !XP;   // zero-points loaded (packed uint4 weights)
     constexpr int kShift = kGroup && AM == 2 ? (WK == WKind::I4Sym ? 8 : 4) : 0;
     constexpr float kSfac = 1.0f / static_cast<float>(1 << kShift);
+    // kXS (expanded weights on 256-row tiles): the expanded weights carry their group scales as fp16
+    // column pairs after the int8 tiles (mq_expand_weight_w4: dword [g][c][u] = the scales of group
+    // g of columns 32 u + c and 32 u + 16 + c, zero past N and past G, scale_pair_ld(N) dwords per
+    // [g][c] row). Each lane loads its NJ columns' scales of a group with one load straight into
+    // registers (no LDS stores or reads, no LDS wait before the group's barrier), one group ahead,
+    // and the fp32 step multiplies by the fp16 scale itself (v_fma_mix). The step then runs unscaled
+    // by kSfac, a power of two moved to the row scales of the epilogue: every product and sum is
+    // 2^kShift times the scaled one, the same bits after it. The 128 x 128 tile keeps its scales in
+    // LDS (its eight-MFMA groups leave a load one group ahead too little time: 25 % slower).
+    constexpr bool kXS = XP && TM_ == 256;
+    constexpr float kSfacA = kXS ? kSfac : 1.0f;   // applied to the activation scales
     __shared__ __attribute__((aligned(16))) uint8_t smem[C::SMEM_BYTES];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -298,7 +326,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     float ep_a = 0.0f, ep_b = 0.0f;
     if constexpr (kFinal) {
         if (tid < TM) {
-            if (tid < rows_m) ep_a = a.sa[m0 + tid];
+            if (tid < rows_m) ep_a = a.sa[m0 + tid] * kSfacA;   // exact
         } else if (tid - TM < rows_n) {
             const int64_t col = n0 + (tid - TM);
             if (a.bias) ep_a = load_as_f32(a.bias, a.bias_dtype, col);
@@ -347,6 +375,12 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
                          has_s ? ((rows_n - 1) * a.ldws + G) * 2 : 0);
     const int z_off = has_z && b_ok ? static_cast<int>(brow * a.ldwz) : kOob;
     const int s_off = has_s && b_ok && bpart < 2 ? static_cast<int>(brow * a.ldws * 2) + 4 * bhalf : kOob;
+    // kXS: the scale pairs after the expanded weight's tiles, G4 groups (every access below lies
+    // inside them)
+    const int sp_ld = static_cast<int>(scale_pair_ld(N));                 // dwords per [g][c] row
+    const int sp_stride = 16 * sp_ld * 4;                                  // bytes per group
+    const auto rsp = rsrc(a.qw + (N + 15) / 16 * 16 * a.K, kXS ? static_cast<int64_t>(G4) * sp_stride : 0);
+    const auto rsp_none = rsrc(a.qw, 0);
     const int b_st00 = B_LDS + lds_off(brow, TPR == 2 ? 2 * bpart : bpart);
     const int b_st10 = B_LDS + lds_off(brow, TPR == 2 ? 2 * bpart + 1 : bpart);
     // scales stored transposed, [wn][column % 16][column tile], so a lane's NJ scales are adjacent
@@ -355,6 +389,9 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // fragment reads: lane l reads chunk l / 16 of row l % 16 of a 16-row block (swizzle depends
     // only on the row within the block, so one per-lane offset serves every block)
     const int fr = lane & 15, fk = ((lane >> 4) ^ ((fr >> 1) & 3)) << 4;
+    // kXS: this lane's scales, columns n0 + wn WC + 16 j + fr, j = 0 .. NJ - 1, in NJ / 2 adjacent
+    // dwords (n0 + wn WC is a multiple of 32)
+    const int sc_off = static_cast<int>((fr * sp_ld + ((n0 + wn * WC) >> 5)) * 4);
     const int a_rd0 = A_LDS + (wm * WR + fr) * TK + fk;   // + i * 16 * TK
     const int b_rd0 = B_LDS + (wn * WC + fr) * TK + fk;   // + j * 16 * TK
     const int s_rd0 = S_LDS + 4 * ((wn * 16 + fr) * NJ);        // + 4 * j
@@ -439,6 +476,33 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             sq = asm_ld32(b4 < G ? ds : d_none, lb ? s_last : s_off, soff(b4, 2));
         }
     };
+    // kXS: group g's scales of this lane's NJ columns into register slot `slot` (= g % 2); groups
+    // past the scale pairs (the loop's last loads) read zeros through an empty range
+    uint32_t sc[2][NJ / 2];
+#pragma unroll
+    for (int h = 0; h < NJ / 2; ++h) sc[0][h] = sc[1][h] = 0u;
+    auto gload_sc = [&](int g, int slot) {
+        if constexpr (kXS) {
+            const auto r = g < G4 ? rsp : rsp_none;
+            const int so = g < G4 ? g * sp_stride : 0;
+            if constexpr (NJ == 8) {
+                const v4i v = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, sc_off, so, 0));
+                sc[slot][0] = v.x; sc[slot][1] = v.y; sc[slot][2] = v.z; sc[slot][3] = v.w;
+            } else if constexpr (NJ == 6) {
+                const u3v v = __builtin_amdgcn_raw_buffer_load_b96(r, sc_off, so, 0);
+                sc[slot][0] = v.x; sc[slot][1] = v.y; sc[slot][2] = v.z;
+            } else {
+                static_assert(NJ == 4, "tiles of 4, 6 or 8 column blocks per wave");
+                const u2v v = __builtin_amdgcn_raw_buffer_load_b64(r, sc_off, so, 0);
+                sc[slot][0] = v.x; sc[slot][1] = v.y;
+            }
+        }
+    };
+    // kXS: a wait for at most N outstanding VMEM operations before the barrier (the compiler also
+    // waits for each scale load itself before its first use; these loads are visible to it)
+    auto wait_sc = [&](auto Nc, auto) {
+        if constexpr (kXS) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(decltype(Nc)::value) : "memory");
+    };
     // Wait until at most N VMEM operations are outstanding; register set SET counts as written by
     // the wait, so no use of it moves above it.
 #define MQ_WAIT_B(N, SET) \
@@ -475,9 +539,9 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             constexpr bool neg = decltype(PARc)::value == 1;
             constexpr int u = decltype(Uc)::value;
             if (bpart == (u >> 1) && (TN == TM || brow < TN)) {
-                float sv = f16_bits_to_f32(static_cast<uint16_t>(sq >> (16 * (u & 1)))) * kSfac;   // exact
+                float sv = f16_bits_to_f32(static_cast<uint16_t>(sq >> (16 * (u & 1)))) * (kXS ? 1.0f : kSfac);   // exact
                 sv = g >= g0 && g < gend ? (neg ? -sv : sv) : 0.0f;
-                ds_write4<TN * 4>(s_st, st * TN * 4, sv);
+                if constexpr (!kXS) ds_write4<TN * 4>(s_st, st * TN * 4, sv);
                 cs += sv;
             }
         }
@@ -514,7 +578,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     auto read_b = [&](int st, int col, int slot) { fb[slot] = lds<v4i>(smem, b_rd + st * TILE_BYTES + col * 16 * TK); };
     // the 4 scales of columns 4 h .. 4 h + 3 (adjacent in the transposed scale layout) into quad q
     auto read_s = [&](int st, int h, int q) {
-        if constexpr (EPI == Epi::GroupScale) fs[q] = lds<f4>(smem, s_rd + st * TN * 4 + 16 * h);
+        if constexpr (EPI == Epi::GroupScale && !kXS) fs[q] = lds<f4>(smem, s_rd + st * TN * 4 + 16 * h);
     };
     // Partials of tile tp (held in d[tp & 3]) of group gp.
     auto write_partials = [&](int tp, int gp, bool odd) {
@@ -528,9 +592,16 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
             if (row < M && col < N) part[row * N + col] = odd ? -pv : pv;
         }
     };
-    // fmas of tile tp of a group of parity par: acc += float(seed + X) * (+-s)
+    // fmas of tile tp of a group of parity par: acc += float(seed + X) * (+-s); kXS: s is the tile
+    // column's fp16 scale in slot par, taken as fp16 by the fma itself (v_fma_mix_f32)
     auto fma_tile = [&](int tp, int par) {
         const int ip = tp % NI, jp = tp / NI;
+        if constexpr (kXS) {
+            const uint32_t sp = sc[par][jp >> 1];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) fma_mix(acc[ip][jp][r], __int_as_float(d[tp & 3][r]), sp, jp & 1, par);
+            return;
+        }
         const float sv = NJ >= 6 ? fs[jp >> 2][jp & 3] : fs[par][jp & 3];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -545,6 +616,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // register set g % 2 holds (or is loading) B(g + 2), set (g + 1) % 2 B(g + 3).
     // The VMEM issue order leaves B(2), A(2), B(3) in flight, as in the steady state; A(0), A(1) are
     // complete once the compiler has waited for B(1)'s registers.
+    gload_sc(g0, 0);   // kXS: the first group's scales (each group loads the next one's)
     dma_group(g0, 0);
     dma_group(g0 + 1, 1);
     gload_zs(g0);
@@ -552,6 +624,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     gload_b(g0 + 1, 1);
     MQ_WAIT_B(0, 0);
     MQ_WAIT_B(0, 1);
+    wait_sc(I0{}, std::integral_constant<int, 0>{});
     settle_zs();
     store_b(0, 0, I0{}, I0{}, 0);
     store_b(0, 0, I0{}, I0{}, 1);
@@ -588,8 +661,12 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // operations issued after the one awaited. With int8 weights the group's DMA is all its VMEM
     // work; issued eight MFMAs into the group rather than at its first, it takes 1.5-2 % off the
     // 256 x 256 row-scale product (measured, same bits).
+    // kXS: group g + 1's scales load at step LAG of group g (once group g - 1's last fmas, steps
+    // 0 .. LAG - 1, have read that slot), ahead of the group's DMA; the wait before the barrier that
+    // ends group g takes them (kTD > LAG).
     constexpr int kDmaOps = NH * (kPacked ? 1 : 2);
-    constexpr int kTD = kPacked ? 0 : 8 % NTL;
+    constexpr int kTD = kPacked ? 0 : kXS && 8 % NTL <= LAG ? LAG + 1 : 8 % NTL;
+    static_assert(!kXS || kTD > LAG, "the scales load before the group's DMA");
     // steps of the B unpack (kTB: wait for the registers, store; kTB + 1: second half for T = 256),
     // of the scale store (kTS) and of the next packed B load (kTL); kTB > 0 follows the DMA of step 0
     // (packed weights)
@@ -599,17 +676,24 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // Before the barrier that ends group g, A(g + 2) (issued at step kTD of group g - 1) must be
     // complete; issued after it: B(g + 3), [zs if (g - 1) % 4 == 1], A(g + 3), B(g + 4),
     // [zs if g % 4 == 1]. (The partials variant also stores to global memory; it waits for all.)
+    // kXS: group g + 1's scales (issued at step LAG of group g, before its DMA and zs) must be complete
+    // too, which leaves only the group's DMA and zs outstanding.
     constexpr int kVmAfter[4] = {
-        EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB, EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB + kZS,
-        EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB + kZS, EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB};
+        EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB,
+        EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB + kZS,
+        EPI == Epi::GroupPartials ? 0 : kXS ? kDmaOps : kDmaOps + 2 * kB + kZS,
+        EPI == Epi::GroupPartials ? 0 : kDmaOps + 2 * kB};
     // At step kTB of group g, register set g % 2 (B(g + 2), loaded at step kTL of group g - 2) must
     // have arrived, and in groups with g % 4 == 2 the block of zero-points and scales loaded at the
     // end of group g - 1. Issued after B(g + 2): [zs if g % 4 == 3], A(g + 2), B(g + 3),
     // [zs if g % 4 == 2], A(g + 3).
+    // kXS has no B registers: only the block's scales (g % 4 == 2) are awaited, with the group's scale
+    // load and DMA issued after them.
     constexpr int kWaitB[4] = {
-        EPI == Epi::GroupPartials ? 0 : 2 * kDmaOps + kB, EPI == Epi::GroupPartials ? 0 : 2 * kDmaOps + kB,
-        EPI == Epi::GroupPartials ? 0 : (kZS > 0 ? kDmaOps : 2 * kDmaOps + kB),
-        EPI == Epi::GroupPartials ? 0 : 2 * kDmaOps + kB + kZS};
+        EPI == Epi::GroupPartials ? 0 : kXS ? 63 : 2 * kDmaOps + kB,
+        EPI == Epi::GroupPartials ? 0 : kXS ? 63 : 2 * kDmaOps + kB,
+        EPI == Epi::GroupPartials ? 0 : kXS ? 1 + kDmaOps : (kZS > 0 ? kDmaOps : 2 * kDmaOps + kB),
+        EPI == Epi::GroupPartials ? 0 : kXS ? 63 : 2 * kDmaOps + kB + kZS};
 
     // K group g with A stage, B stage and register set fixed by U = g % 4 (compile-time). Step t = NI j + i.
     auto group = [&](int g, auto Uc) {
@@ -635,6 +719,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
                 const int gp = t < LAG ? g - 1 : g;
                 if (gp >= 0 && gp < G) write_partials(tp, gp, t < LAG ? PAR == 0 : PAR == 1);
             }
+            if constexpr (kXS)
+                if (t == LAG) gload_sc(g + 1, PAR ^ 1);
             if (t == kTD) dma_group(g + 3, ST3);
             // B fragments three columns ahead (the next group's first columns from stage ST1,
             // complete since the barrier that ended group g - 1)
@@ -677,8 +763,11 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
         // wave waits until at most the LDS operations issued after its last store are outstanding
         // (the next group's fragment and scale reads, which stay in flight across the barrier).
         // Group g's own stages were last read by MFMAs that have issued.
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kVmAfter[U]) : "memory");
-        if constexpr (NJ != 8) {
+        // (kXS: group g + 1's scales, slot PAR ^ 1, arrive with the same wait. kXS stores nothing to LDS
+        // in the loop, so no LDS wait is needed.)
+        if constexpr (kXS) wait_sc(std::integral_constant<int, kVmAfter[U]>{}, std::integral_constant<int, PAR ^ 1>{});
+        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kVmAfter[U]) : "memory");
+        if constexpr (NJ != 8 && !kXS) {
             constexpr int kLdsAfter = lds_ops_after(NI, NJ, kTS, EPI == Epi::GroupScale);
             static_assert(kLdsAfter < 16, "lgkmcnt holds 0-15");
             asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(kLdsAfter) : "memory");
@@ -702,6 +791,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     if constexpr (kPacked) asm volatile("" : "+v"(rb[0]), "+v"(rb[1]));
     if constexpr (kHasZ) asm volatile("" : "+v"(zq));
     if constexpr (EPI == Epi::GroupScale) asm volatile("" : "+v"(sq));
+    wait_sc(I0{}, I0{});
+    wait_sc(I0{}, I1{});
 #undef MQ_WAIT_B
     // drain: the last LAG tiles of the last group run (dead unless G is a multiple of four)
 #pragma unroll
@@ -756,7 +847,7 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
                     const int64_t row = m0 + wm * WR + i * 16 + 4 * (lane >> 4) + r;
                     if (row >= M) continue;
                     if constexpr (EPI == Epi::GroupScale)
-                        static_cast<float*>(a.work)[slice_off + row * N + col] = acc[i][j][r] - cv;
+                        static_cast<float*>(a.work)[slice_off + row * N + col] = (acc[i][j][r] - cv) * kSfacA;
                     else
                         static_cast<int32_t*>(a.work)[slice_off + row * N + col] = acci[i][j][r];
                 }

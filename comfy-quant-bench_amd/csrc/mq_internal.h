@@ -54,6 +54,10 @@ int launch_quantize_weight(const void* w, int dtype, int64_t N, int64_t K, int64
 int launch_tile_weight_i8(const uint8_t* w, int64_t ldw, int64_t N, int64_t K, uint8_t* out, hipStream_t stream);
 
 // packed 4-bit weights into int8 16-row tiles (mq_expand_weight_w4's layouts; mq_wquant.hip)
+// dwords per [g][c] row of the scale pairs that expanded 4-bit weights carry (MQ_SCALE_PAIR_LD)
+__host__ __device__ inline int64_t scale_pair_ld(int64_t N) { return ((N + 15) / 16 + 17) / 2; }
+int launch_expand_scales_w4(const uint16_t* ws, int64_t ldws, int64_t N, int64_t K, uint32_t* out,
+                            hipStream_t stream);
 int launch_expand_weight_w4(const uint8_t* qw, int64_t ldw, const uint8_t* wz, int64_t ldwz, int64_t N, int64_t K,
                             int layout, uint8_t* out, hipStream_t stream);
 

@@ -234,7 +234,34 @@ __global__ void __launch_bounds__(256) expand_w4_kernel(const uint8_t* qw, int64
     }
 }
 
+// fp16 group scales [N, G] (row stride ldws) as the expanded-weight group GEMM's lanes load them:
+// dword [g][c][u] (u fastest, ld dwords per [g][c]) = ws[32 u + c, g] | ws[32 u + 16 + c, g] << 16,
+// zero for columns past N and groups past G; G4 groups in all (G rounded up to four).
+__global__ void __launch_bounds__(256) expand_scales_kernel(const uint16_t* ws, int64_t ldws, int64_t N, int64_t G,
+                                                           int64_t G4, int64_t ld, uint32_t* out) {
+    const int64_t total = G4 * 16 * ld;
+    for (int64_t i = blockIdx.x * int64_t(256) + threadIdx.x; i < total; i += int64_t(gridDim.x) * 256) {
+        const int64_t u = i % ld, c = (i / ld) % 16, g = i / (16 * ld);
+        const int64_t n0 = 32 * u + c, n1 = n0 + 16;
+        uint32_t v = 0u;
+        if (g < G) {
+            if (n0 < N) v = ws[n0 * ldws + g];
+            if (n1 < N) v |= static_cast<uint32_t>(ws[n1 * ldws + g]) << 16;
+        }
+        out[i] = v;
+    }
+}
+
 }  // namespace
+
+int launch_expand_scales_w4(const uint16_t* ws, int64_t ldws, int64_t N, int64_t K, uint32_t* out,
+                            hipStream_t stream) {
+    const int64_t G = K / 64, G4 = (G + 3) / 4 * 4, ld = scale_pair_ld(N);
+    const int64_t blocks = std::min<int64_t>((G4 * 16 * ld + 255) / 256, 65536);
+    hipLaunchKernelGGL(expand_scales_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, ws, ldws, N, G,
+                       G4, ld, out);
+    return launch_status("expand_scales_w4");
+}
 
 int launch_expand_weight_w4(const uint8_t* qw, int64_t ldw, const uint8_t* wz, int64_t ldwz, int64_t N, int64_t K,
                             int layout, uint8_t* out, hipStream_t stream) {

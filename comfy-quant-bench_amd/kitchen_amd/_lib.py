@@ -11,7 +11,7 @@ import os
 
 import torch  # noqa: F401  (must be imported before the library is loaded)
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmq.so")
 
@@ -43,7 +43,8 @@ _SIGNATURES = {
     "mq_gemm_rowscale_ws": ([c_vp, c_i64, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_int, c_vp, c_int, c_i64, c_i64,
                              c_i64, c_i64, c_vp, c_i64, c_vp], c_int),
     "mq_tile_weight_i8": ([c_vp, c_i64, c_i64, c_i64, c_vp, c_vp], c_int),
-    "mq_expand_weight_w4": ([c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_int, c_vp, c_vp], c_int),
+    "mq_expand_weight_w4": ([c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_int, c_vp, c_vp], c_int),
+    "mq_expanded_w4_bytes": ([c_i64, c_i64, c_int], c_i64),
     "mq_gemm_rowscale_acc": ([c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_vp], c_int),
     "mq_linear_workspace_bytes": ([c_i64, c_i64, c_i64], c_i64),
     "mq_linear_w4_group": ([c_vp, c_int, c_i64, c_int, c_int, c_int, c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp,

@@ -290,6 +290,8 @@ def gemm_w4_group(qa, sa, qweight, wscales, wzeros, bias, n: int, group_size: in
             raise ValueError(f"expanded weights for layout {qweight.layout} [{qweight.n}, {qweight.k}] "
                              f"do not serve act_mode {act_mode} [{n}, {k}]")
         _check_w4_group(qa, None, wscales, None, n, group_size)
+        if qweight.scales != _scales_id(wscales):
+            raise ValueError("expanded weights carry the group scales they were made with: pass the same wscales")
         qptr, ldw, mode = qweight.tiles.data_ptr(), k, int(act_mode) | _lib.W4_EXPANDED
         zptr, ldwz = (qweight.tiles.data_ptr() if qweight.asym else None), 0   # non-null: uint4 (not read)
     else:
@@ -341,23 +343,33 @@ def tile_int8_weight(weight: torch.Tensor) -> torch.Tensor:
 class ExpandedW4:
     """Packed 4-bit weights expanded once to int8 in 16-row tiles (mq_expand_weight_w4).
 
-    tiles   int8 [ceil(N / 16), K / 64, 16, 64]
+    tiles   int8 [ceil(N / 16), K / 64, 16, 64], the front of the expansion's buffer
     layout  _lib.ACT_I8 / _lib.ACT_X16ALT: for the group GEMMs with that activation layout (the
-            bytes their in-kernel unpack would store, zero-point and sign included);
+            bytes their in-kernel unpack would store, zero-point and sign included), with the
+            weight's fp16 group scales carried after the tiles in the layout the GEMM's lanes read;
             _lib.W4X_ROW: an int8 weight for the row-scale GEMMs (the signed codes)
     asym    uint4 weights with zero-points (folded into the bytes) rather than signed int4
+    scales  (data_ptr, shape, stride) of the group scales the expansion carries (None for W4X_ROW):
+            the group GEMMs take the same tensor as wscales, for their epilogue's correction term
 The GEMMs give the packed weights' results bit for bit from it, without the per-use unpack, at
 twice the packed weight's memory."""
 
-    __slots__ = ("tiles", "layout", "asym", "n", "k")
+    __slots__ = ("tiles", "buf", "layout", "asym", "n", "k", "scales")
 
-    def __init__(self, tiles: torch.Tensor, layout: int, asym: bool, n: int, k: int):
-        self.tiles, self.layout, self.asym, self.n, self.k = tiles, int(layout), bool(asym), int(n), int(k)
+    def __init__(self, buf: torch.Tensor, layout: int, asym: bool, n: int, k: int, scales=None):
+        self.buf = buf
+        self.tiles = buf[: (n + 15) // 16 * 16 * k].view(torch.int8).view((n + 15) // 16, k // 64, 16, 64)
+        self.layout, self.asym, self.n, self.k, self.scales = int(layout), bool(asym), int(n), int(k), scales
 
 
-def expand_w4_weight(qweight: torch.Tensor, wzeros=None, layout: int = _lib.ACT_I8) -> ExpandedW4:
+def _scales_id(wscales):
+    return (wscales.data_ptr(), tuple(wscales.shape), tuple(wscales.stride()))
+
+
+def expand_w4_weight(qweight: torch.Tensor, wzeros=None, layout: int = _lib.ACT_I8, wscales=None) -> ExpandedW4:
     """qweight 8-bit [N, K/2] packed 4-bit codes (uint4 with wzeros packed uint4 [N, ceil(K/128)],
-    or signed int4 when wzeros is None) -> ExpandedW4 for `layout` (see ExpandedW4)."""
+    or signed int4 when wzeros is None) -> ExpandedW4 for `layout` (see ExpandedW4); the group
+    layouts take the weight's fp16 group scales wscales [N, K/64]."""
     if qweight.dim() != 2 or qweight.element_size() != 1:
         raise ValueError(f"qweight must be 8-bit [N, K/2], got {qweight.dtype} {list(qweight.shape)}")
     if layout not in (_lib.ACT_I8, _lib.ACT_X16ALT, _lib.W4X_ROW):
@@ -369,10 +381,17 @@ def expand_w4_weight(qweight: torch.Tensor, wzeros=None, layout: int = _lib.ACT_
         if wzeros.element_size() != 1 or wzeros.shape[0] != n or wzeros.shape[1] < (k // 64 + 1) // 2:
             raise ValueError(f"zero-points must be packed uint4 [{n}, {(k // 64 + 1) // 2}]")
         zz = wzeros if wzeros.stride(1) == 1 else wzeros.contiguous()
-    out = torch.empty(((n + 15) // 16, k // 64, 16, 64), dtype=torch.int8, device=qweight.device)
+    ws = None
+    if layout != _lib.W4X_ROW:
+        if wscales is None or wscales.dtype != torch.float16 or wscales.dim() != 2 or wscales.shape[0] != n \
+                or wscales.shape[1] < k // 64 or wscales.stride(1) != 1:
+            raise ValueError(f"the group layouts need the fp16 group scales [{n}, {k // 64}] (unit column stride)")
+        ws = wscales
+    nbytes = _lib.load().mq_expanded_w4_bytes(n, k, int(layout))
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=qweight.device)
     _lib.call("mq_expand_weight_w4", qw.data_ptr(), qw.stride(0), _lib.ptr(zz), 0 if zz is None else zz.stride(0),
-              n, k, int(layout), out.data_ptr(), _lib.stream_of(qw))
-    return ExpandedW4(out, layout, zz is not None, n, k)
+              _lib.ptr(ws), 0 if ws is None else ws.stride(0), n, k, int(layout), buf.data_ptr(), _lib.stream_of(qw))
+    return ExpandedW4(buf, layout, zz is not None, n, k, None if ws is None else _scales_id(ws))
 
 
 # The linears run their 4-bit weights from an int8 expansion wherever the packed weights would run
@@ -393,19 +412,24 @@ _EXPANDED: dict = {}
 
 def _expansion(qweight, wzeros, layout: int, m: int, k: int, wscales=None):
     """The cached ExpandedW4 of qweight for `layout` when a product of m rows reads one (the wide
-    kernel's conditions: K >= 192, K groups in pairs for the group scales' loads, under 2 GiB),
-    else None."""
+    kernel's conditions: K >= 192, K groups in pairs for the group scales' loads, under 2 GiB;
+    the group layouts also carry wscales, fp16 with unit column stride), else None."""
     n = qweight.shape[0]
-    if not EXPAND_W4 or m <= (GEMV_ROWS if layout == _lib.W4X_ROW else FEW_ROWS) or k < 192 or k % 64 or (n + 15) // 16 * 16 * k >= 1 << 31 \
-            or (m + 15) // 16 * 16 * k >= 1 << 31:
+    if not EXPAND_W4 or m <= (GEMV_ROWS if layout == _lib.W4X_ROW else FEW_ROWS) or k < 192 or k % 64 \
+            or _lib.load().mq_expanded_w4_bytes(n, k, int(layout)) >= 1 << 31 or (m + 15) // 16 * 16 * k >= 1 << 31:
         return None
-    if wscales is not None and (wscales.stride(0) % 2 or wscales.data_ptr() % 4):
+    if wscales is not None and (wscales.stride(0) % 2 or wscales.data_ptr() % 4 or wscales.stride(1) != 1
+                                or wscales.dtype != torch.float16):
         return None
     root = qweight._base if qweight._base is not None else qweight
     zroot = None if wzeros is None else (wzeros._base if wzeros._base is not None else wzeros)
+    if layout != _lib.W4X_ROW and wscales is None:
+        return None
     key = (qweight.data_ptr(), tuple(qweight.shape), tuple(qweight.stride()),
-           0 if wzeros is None else wzeros.data_ptr(), int(layout))
-    sig = (qweight._version, 0 if wzeros is None else wzeros._version, id(zroot))
+           0 if wzeros is None else wzeros.data_ptr(), int(layout),
+           None if layout == _lib.W4X_ROW else _scales_id(wscales))
+    sig = (qweight._version, 0 if wzeros is None else wzeros._version, id(zroot),
+           0 if layout == _lib.W4X_ROW else wscales._version)
     per = _EXPANDED.get(id(root))
     hit = None if per is None else per.get(key)
     if hit is not None and hit[0] == sig:
@@ -415,7 +439,7 @@ def _expansion(qweight, wzeros, layout: int, m: int, k: int, wscales=None):
     if per is None:
         per = _EXPANDED[id(root)] = {}
         weakref.finalize(root, _EXPANDED.pop, id(root), None)
-    ex = expand_w4_weight(qweight, wzeros, layout)
+    ex = expand_w4_weight(qweight, wzeros, layout, None if layout == _lib.W4X_ROW else wscales)
     per[key] = (sig, ex)
     return ex
 

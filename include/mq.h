@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define MQ_ABI_VERSION 10
+#define MQ_ABI_VERSION 11
 
 enum {
     MQ_OK = 0,
@@ -201,17 +201,27 @@ int mq_decode_w4a8_codebook(const void* qdata, int64_t ldq, const void* s_rel, i
  * none of the unpack's VALU work). No counterpart in the reference (whose kernel unpacks per use,
  * experiments/qwen21-kernel/kernels/g64_gemm6.cu:93-343): it trades twice the packed weight's
  * memory for that work. Run once per weight.
+ * The group-GEMM layouts (MQ_ACT_I8, MQ_ACT_X16ALT) also carry the weight's fp16 group scales, after
+ * the tiles, as the GEMM's lanes read them straight into registers: uint32 [G4][16][ld] with
+ * G4 = 4 * ceil(K/256) and ld = MQ_SCALE_PAIR_LD(N), dword [g][c][u] = ws[32u + c, g] |
+ * ws[32u + 16 + c, g] << 16, zero where the column is >= N or g >= K/64. MQ_W4X_ROW carries none.
  *   qw   packed 4-bit [N, K/2], stride ldw bytes (ldw % 8 == 0, 8-byte aligned)
  *   wz   packed uint4 zero-points [N, ceil(K/128)], stride ldwz, or NULL (signed int4)
- *   out  (N + 15) / 16 * 16 * K bytes, 16-byte aligned, under 2 GiB
+ *   ws   fp16 group scales [N, K/64], stride ldws elements (MQ_ACT_I8 / MQ_ACT_X16ALT; NULL for
+ *        MQ_W4X_ROW)
+ *   out  mq_expanded_w4_bytes(N, K, layout) bytes, 16-byte aligned, under 2 GiB
  * Requires K % 64 == 0.
  */
 #define MQ_W4X_ROW 3
-int mq_expand_weight_w4(const uint8_t* qw, int64_t ldw, const uint8_t* wz, int64_t ldwz, int64_t N, int64_t K,
-                        int layout, int8_t* out, void* stream);
+#define MQ_SCALE_PAIR_LD(N) ((((N) + 15) / 16 + 17) / 2)
+int mq_expand_weight_w4(const uint8_t* qw, int64_t ldw, const uint8_t* wz, int64_t ldwz, const uint16_t* ws,
+                        int64_t ldws, int64_t N, int64_t K, int layout, int8_t* out, void* stream);
+int64_t mq_expanded_w4_bytes(int64_t N, int64_t K, int layout);
 
 /* act_mode flag of the group GEMMs (act_bits flag of the whole group linears): qw holds the
- * expansion of mq_expand_weight_w4 for that activation layout (ldw ignored). wz is then not read;
+ * expansion of mq_expand_weight_w4 for that activation layout (ldw ignored; the GEMM reads the
+ * scales the expansion carries, and ws / ldws for the correction term of its epilogue, so they must
+ * be the scales it was made with). wz is then not read;
  * non-NULL marks weights that were uint4 asymmetric (their MQ_ACT_X16ALT scaling differs from signed
  * int4). Read by the wide kernel only: M > 4 rows (fewer rows take the packed weights), K >= 192,
  * the expanded array under 2 GiB; the group-scale epilogue only (not the partials entry). */

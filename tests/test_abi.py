@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mq_abi_version() == 10
+    assert lib.mq_abi_version() == 11
 
 
 def _err(lib):
@@ -221,15 +221,27 @@ def test_linear_validation_rejects_before_launch(lib):
 def test_expanded_w4_validation(lib):
     # 4-bit weights expanded to int8 tiles: layouts 0 (int8 codes), 2 (x16 int4 codes), 3 (row scale)
     a = 1 << 20
-    assert lib.mq_expand_weight_w4(a, 96, None, 0, 8, 192, 1, a, None) == -1
+    assert lib.mq_expand_weight_w4(a, 96, None, 0, a, 3, 8, 192, 1, a, None) == -1
     assert "layout" in _err(lib)
-    assert lib.mq_expand_weight_w4(a, 104, None, 0, 8, 200, 0, a, None) == -1
+    assert lib.mq_expand_weight_w4(a, 104, None, 0, a, 4, 8, 200, 0, a, None) == -1
     assert "K % 64" in _err(lib)
-    assert lib.mq_expand_weight_w4(a, 100, None, 0, 8, 192, 0, a, None) == -1
+    assert lib.mq_expand_weight_w4(a, 100, None, 0, a, 3, 8, 192, 0, a, None) == -1
     assert "ldw" in _err(lib)
-    assert lib.mq_expand_weight_w4(a, 96, a, 1, 8, 192, 2, a, None) == -1
+    assert lib.mq_expand_weight_w4(a, 96, a, 1, a, 3, 8, 192, 2, a, None) == -1
     assert "ldwz" in _err(lib)
-    assert lib.mq_expand_weight_w4(None, 96, None, 0, 0, 192, 3, None, None) == 0
+    # the group layouts carry the fp16 group scales (K/64 per row at least)
+    assert lib.mq_expand_weight_w4(a, 96, None, 0, None, 3, 8, 192, 0, a, None) == -1
+    assert "scales" in _err(lib)
+    assert lib.mq_expand_weight_w4(a, 96, None, 0, a, 2, 8, 192, 2, a, None) == -1
+    assert "scales" in _err(lib)
+    assert lib.mq_expand_weight_w4(None, 96, None, 0, None, 0, 0, 192, 3, None, None) == 0
+    # sizes: the int8 tiles, then (group layouts) 4 * ceil(K/256) groups x 16 x MQ_SCALE_PAIR_LD(N) dwords
+    for n, k in ((8, 192), (16, 3072), (100, 1024), (12288, 3072)):
+        tiles = (n + 15) // 16 * 16 * k
+        ld = ((n + 15) // 16 + 17) // 2
+        assert lib.mq_expanded_w4_bytes(n, k, 3) == tiles
+        for layout in (0, 2):
+            assert lib.mq_expanded_w4_bytes(n, k, layout) == tiles + (k // 64 + 3) // 4 * 4 * 16 * ld * 4
     # the group GEMMs take them for the int8 and x16 int4 activation layouts, K >= 192
     assert lib.mq_gemm_w4_group(a, 256, a, a, 0, a, 4, None, 0, 64, 1 | 0x100, None, 0, a, 0, 64, 8, 64, 256,
                                 None) == -1

@@ -35,6 +35,17 @@ def _expand_np(qw: np.ndarray, wz, n: int, k: int, layout: int) -> np.ndarray:
     return out.reshape(nb, 16, k // 64, 64).transpose(0, 2, 1, 3)
 
 
+def _scale_pairs_np(s16, n, k):
+    """The group scales as the expansion carries them: uint32 [4 ceil(K/256)][16][ld], dword
+    [g][c][u] = s[32u + c, g] | s[32u + 16 + c, g] << 16, zero past N and K/64."""
+    g = k // 64
+    g4, ld = (g + 3) // 4 * 4, ((n + 15) // 16 + 17) // 2
+    bits = np.zeros((2 * ld * 16, g4), dtype=np.uint32)        # [column, group], columns padded
+    bits[:n, :g] = s16.view(np.uint16)[:, :g]
+    cols = bits.reshape(ld, 2, 16, g4)                           # [u][half][c][g]
+    return (cols[:, 0] | (cols[:, 1] << 16)).transpose(2, 1, 0)  # [g][c][u]
+
+
 @pytest.mark.parametrize("layout", [_lib.ACT_I8, _lib.ACT_X16ALT, _lib.W4X_ROW])
 @pytest.mark.parametrize("asym", [True, False])
 @pytest.mark.parametrize("n,k", [(16, 192), (40, 320), (1, 128), (77, 3072)])
@@ -43,11 +54,23 @@ def test_expansion_bytes(gpu_device, layout, asym, n, k):
     rng = np.random.default_rng(n * 7 + k)
     qw = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
     wz = rng.integers(0, 256, (n, (k // 64 + 1) // 2), dtype=np.uint8) if asym else None
+    # fp16 scales from random bits (finite: exponent field below 31), a padded row stride
+    s16 = rng.integers(0, 1 << 16, (n, k // 64 + 3), dtype=np.uint16)
+    s16 = np.where((s16 & 0x7c00) == 0x7c00, s16 & 0x3fff, s16).view(np.float16)
+    s16_t = torch.from_numpy(s16).to(gpu_device)[:, : k // 64]
     ex = ck.expand_w4_weight(torch.from_numpy(qw).to(gpu_device),
-                             None if wz is None else torch.from_numpy(wz).to(gpu_device), layout)
+                             None if wz is None else torch.from_numpy(wz).to(gpu_device), layout,
+                             None if layout == _lib.W4X_ROW else s16_t)
     torch.cuda.synchronize()
     assert ex.tiles.shape == ((n + 15) // 16, k // 64, 16, 64) and ex.asym == asym
     assert np.array_equal(ex.tiles.cpu().numpy(), _expand_np(qw, wz, n, k, layout))
+    tiles = (n + 15) // 16 * 16 * k
+    if layout == _lib.W4X_ROW:
+        assert ex.buf.numel() == tiles
+    else:
+        pairs = ex.buf[tiles:].cpu().numpy().view(np.uint32)
+        want = _scale_pairs_np(np.ascontiguousarray(s16[:, : k // 64]), n, k)
+        assert pairs.size == want.size and np.array_equal(pairs, want.reshape(-1))
 
 
 def _group_weights(n, k, asym, dev, seed):
@@ -76,7 +99,7 @@ def test_group_gemm_expanded_equals_packed(gpu_device, m, n, k, act_mode, asym):
         qa, sa = ops.rotate_quantize(x, 64, 4, _lib.Q_X16ALT)
     bias = (torch.randn(n, generator=torch.Generator().manual_seed(n)) * 0.1).to(torch.bfloat16).to(gpu_device)
     out = torch.float32 if m == 700 else torch.bfloat16
-    ex = ck.expand_w4_weight(qw.view(torch.uint8), None if zp is None else zp.view(torch.uint8), act_mode)
+    ex = ck.expand_w4_weight(qw.view(torch.uint8), None if zp is None else zp.view(torch.uint8), act_mode, s16)
     y = ops.gemm_w4_group(qa, sa, ex, s16, None, bias, n, act_mode=act_mode, out_dtype=out)
     y0 = ops.gemm_w4_group(qa, sa, qw.view(torch.uint8), s16, None if zp is None else zp.view(torch.uint8), bias, n,
                            act_mode=act_mode, out_dtype=out)
@@ -93,14 +116,14 @@ def test_group_gemm_expanded_equals_packed(gpu_device, m, n, k, act_mode, asym):
 def test_expanded_weights_refused_where_the_wide_kernel_does_not_run(gpu_device):
     w = torch.from_numpy(synth.weight(256, 192, seed=1)).to(gpu_device)
     qw, s16, zp = ck.quantize_w4a8_asym_weight(w, 64, 64)
-    ex = ck.expand_w4_weight(qw.view(torch.uint8), zp.view(torch.uint8), _lib.ACT_I8)
+    ex = ck.expand_w4_weight(qw.view(torch.uint8), zp.view(torch.uint8), _lib.ACT_I8, s16)
     x = synth.to_bf16_tensor(synth.activations(64, 192, seed=2), gpu_device)
     qa, sa = ops.rotate_quantize(x, 64, 8)
     # K = 192: three scale columns per row, not the pairs the wide kernel loads
     with pytest.raises(_lib.MQError, match="wide kernel only"):
         ops.gemm_w4_group(qa, sa, ex, s16, None, None, 256)
     qw, s16, zp = _group_weights(256, 256, True, gpu_device, seed=3)
-    ex = ck.expand_w4_weight(qw.view(torch.uint8), zp.view(torch.uint8), _lib.ACT_I8)
+    ex = ck.expand_w4_weight(qw.view(torch.uint8), zp.view(torch.uint8), _lib.ACT_I8, s16)
     x = synth.to_bf16_tensor(synth.activations(3, 256, seed=4), gpu_device)
     qa, sa = ops.rotate_quantize(x, 256, 8)
     with pytest.raises(_lib.MQError, match="wide kernel only"):   # M <= 4: the GEMV reads packed bytes

@@ -107,7 +107,7 @@ def test_noalloc_with_expanded_weights(gpu_device):
     m, n, k = 300, 1536, 3072
     print(f"[noalloc] expanded weights M={m} N={n} K={k}", flush=True)
     qd, s16, zp = _w4a8_weight(n, k, gpu_device, seed=4)
-    ex = ck.expand_w4_weight(qd, zp, _lib.ACT_I8)
+    ex = ck.expand_w4_weight(qd, zp, _lib.ACT_I8, s16)
     x = synth.to_bf16_tensor(synth.activations(m, k, seed=5), gpu_device)
     bias = torch.randn(n, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(gpu_device)
     y0, y1, y2 = (torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=gpu_device) for _ in range(3))
