@@ -113,6 +113,42 @@ def test_group_gemm_expanded_equals_packed(gpu_device, m, n, k, act_mode, asym):
         assert torch.allclose(y.float(), y0.float(), rtol=2 ** -7, atol=2e-2)
 
 
+# K groups not a multiple of four (odd, and 2 mod 4) on the 256-row tiles (256 x 192, 256 x 256,
+# trailing rows), whose lanes read the group scales the expansion carries (zero-padded past G),
+# and on the 128 x 128 tile; the scale and zero-point rows padded to even strides, as the wide
+# kernel loads them (so the packed weights run on it too)
+ODD_G = [(2100, 4000, 320), (2100, 4000, 1472), (4096, 12288, 320), (4096, 12288, 448), (4352, 12288, 1920),
+         (700, 3000, 192)]
+
+
+@pytest.mark.parametrize("m,n,k", ODD_G)
+@pytest.mark.parametrize("act_mode", [_lib.ACT_I8, _lib.ACT_X16ALT])
+@pytest.mark.parametrize("asym", [True, False])
+def test_expanded_equals_packed_uneven_groups(gpu_device, m, n, k, act_mode, asym):
+    print(f"[expand] uneven groups M={m} N={n} K={k} act_mode={act_mode} asym={asym}", flush=True)
+    g = k // 64
+    w = torch.from_numpy(synth.weight(n, k, seed=k)).to(gpu_device)
+    if asym:
+        qw, s16, zp = ck.quantize_w4a8_asym_weight(w, 64, 64)
+        zc = zp.shape[1]
+        zpp = torch.zeros((n, zc + zc % 2), dtype=torch.uint8, device=gpu_device)
+        zpp[:, :zc] = zp.view(torch.uint8)
+        zp = zpp[:, :zc]
+    else:
+        (qw, s16), zp = ck.quantize_w4a4_group_weight(w, 64, 64), None
+    sp = torch.zeros((n, g + g % 2), dtype=torch.float16, device=gpu_device)
+    sp[:, :g] = s16
+    s16 = sp[:, :g]
+    x = synth.to_bf16_tensor(synth.activations(m, k, seed=m), gpu_device)
+    qa, sa = ops.rotate_quantize(x, 64, 8) if act_mode == _lib.ACT_I8 else ops.rotate_quantize(x, 64, 4, _lib.Q_X16ALT)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(n)) * 0.1).to(torch.bfloat16).to(gpu_device)
+    ex = ck.expand_w4_weight(qw.view(torch.uint8), zp, act_mode, s16)
+    y = ops.gemm_w4_group(qa, sa, ex, s16, None, bias, n, act_mode=act_mode)
+    y0 = ops.gemm_w4_group(qa, sa, qw.view(torch.uint8), s16, zp, bias, n, act_mode=act_mode)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all() and torch.equal(y, y0)
+
+
 def test_expanded_weights_refused_where_the_wide_kernel_does_not_run(gpu_device):
     w = torch.from_numpy(synth.weight(256, 192, seed=1)).to(gpu_device)
     qw, s16, zp = ck.quantize_w4a8_asym_weight(w, 64, 64)
