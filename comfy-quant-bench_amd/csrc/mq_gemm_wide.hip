@@ -23,7 +23,9 @@
 // into the stage of group g + 2 mid-group, and one barrier per group closes the ring.
 // Zero-points and scales are loaded once per block of four groups (one 2-byte and one 4-byte load
 // per weight row), not per group: each such load touches one cache line per row, and per-group
-// loads of 1-2 bytes per row were a third of the kernel's L1 -> L2 requests.
+// loads of 1-2 bytes per row were a third of the kernel's L1 -> L2 requests. The scales are stored
+// to LDS for the fragment-ordered reads of the fmas, except with expanded weights on 256-row tiles
+// (kXS below), whose lanes load their columns' scales from the expansion straight into registers.
 //
 // Per-group scale epilogue without an int->float conversion. The MFMA accumulator of group g
 // is seeded with the bit pattern of 1.5 * 2^23, so the int32 result D = seed + X reads as the
@@ -295,7 +297,8 @@ __global__ void __launch_bounds__(NT) gemm_wide_kernel(GemmArgs a, int tiles_m, 
     // and the fp32 step multiplies by the fp16 scale itself (v_fma_mix). The step then runs unscaled
     // by kSfac, a power of two moved to the row scales of the epilogue: every product and sum is
     // 2^kShift times the scaled one, the same bits after it. The 128 x 128 tile keeps its scales in
-    // LDS (its eight-MFMA groups leave a load one group ahead too little time: 25 % slower).
+    // LDS (its eight-MFMA groups leave a load one group ahead too little time: 25 % slower; loads
+    // three groups ahead in four register slots were still 5 % slower than the LDS scales).
     constexpr bool kXS = XP && TM_ == 256;
     constexpr float kSfacA = kXS ? kSfac : 1.0f;   // applied to the activation scales
     __shared__ __attribute__((aligned(16))) uint8_t smem[C::SMEM_BYTES];
