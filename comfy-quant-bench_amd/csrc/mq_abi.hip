@@ -518,6 +518,22 @@ int quantize_into(const void* x, int x_dtype, int64_t ldx, int hblock, int act_b
                                 : launch_rotquant_bf16(xs, M, K, ldx, hblock, act_bits, layout, q, 0, s, st);
 }
 
+// A one-row linear whose product runs on the GEMV (gemv_quantizes_row): the GEMV rotates and
+// quantizes the row in its prologue, one launch, with the rotate+quantize entry's argument checks
+// and its codes and scale (the workspace is then not written).
+int launch_fused_row(GemmArgs& a, WKind wk, Epi epi, const void* x, int x_dtype, int64_t ldx, int hblock,
+                     int act_bits, int layout, uint8_t* ws_base, void* stream) {
+    const LinearWs w = linear_ws(1, 1, a.K);
+    const int rc = check_rotquant("rotquant", x, x_dtype, true, 1, a.K, a.K, ldx, hblock, act_bits, layout,
+                                  ws_base + w.codes, a.K, reinterpret_cast<const float*>(ws_base + w.scales));
+    if (rc != MQ_OK) return rc;
+    a.x = x;
+    a.x_dtype = x_dtype;
+    a.hblock = hblock;
+    a.x_bits = act_bits;
+    return launch_gemm(a, wk, epi, static_cast<hipStream_t>(stream));
+}
+
 }  // namespace
 
 extern "C" {
@@ -554,6 +570,8 @@ int mq_linear_w4_group(const void* x, int x_dtype, int64_t ldx, int hblock, int 
                   "2 GiB); pass the packed weights");
         return MQ_EUNSUPPORTED;
     }
+    if (swiglu == MQ_SWIGLU_NONE && gemv_quantizes_row(a, wk, Epi::GroupScale))
+        return launch_fused_row(a, wk, Epi::GroupScale, x, x_dtype, ldx, hblock, act_bits, layout, base, stream);
     rc = quantize_into(x, x_dtype, ldx, hblock, act_bits, swiglu, layout, a.atile, M, K, base, stream);
     if (rc) return rc;
     return launch_gemm(a, wk, Epi::GroupScale, static_cast<hipStream_t>(stream));
@@ -576,6 +594,8 @@ int mq_linear_rowscale(const void* x, int x_dtype, int64_t ldx, int hblock, int 
     if (rc) return rc == kEmpty ? MQ_OK : rc;
     a.atile = 1;   // the codes in 16-row tiles wherever the wide kernel reads them
     a.atile = gemm_runs_wide(a, wk, Epi::RowScale);
+    if (swiglu == MQ_SWIGLU_NONE && gemv_quantizes_row(a, wk, Epi::RowScale))
+        return launch_fused_row(a, wk, Epi::RowScale, x, x_dtype, ldx, hblock, act_bits, MQ_Q_BYTES, base, stream);
     rc = quantize_into(x, x_dtype, ldx, hblock, act_bits, swiglu, MQ_Q_BYTES, a.atile, M, K, base, stream);
     if (rc) return rc;
     return launch_gemm(a, wk, Epi::RowScale, static_cast<hipStream_t>(stream));

@@ -267,6 +267,10 @@ bool runs_gemv(const GemmArgs& a, WKind wk, Epi epi) {
 
 }  // namespace
 
+bool gemv_quantizes_row(const GemmArgs& a, WKind wk, Epi epi) {
+    return runs_gemv(a, wk, epi) && a.M == 1 && a.K <= 4096 && (epi == Epi::GroupScale || epi == Epi::RowScale);
+}
+
 bool gemm_runs_wide(const GemmArgs& a, WKind wk, Epi epi) {
     if (runs_gemv(a, wk, epi)) return false;
     // The 256 x 256-tile kernel addresses each operand with 32-bit buffer offsets.

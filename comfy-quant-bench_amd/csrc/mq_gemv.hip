@@ -25,8 +25,16 @@
 //   GroupPartials / RowAcc (parity entries) write the exact int32 group partials P[g, m, n] (the
 //                two chunks of a group sit in lanes 2i and 2i + 1 and are added by a DPP exchange;
 //                the x16 / sign factors of the int4 layouts undone by exact shifts) or the full-K sums
+//
+// One-row whole linears (FQ != 0, M = 1, K <= 4096) hand the GEMV the activation row itself: the
+// workgroup's four waves rotate and quantize it as the rotate+quantize kernel does with four waves
+// per row (same load layout, same mq_rotate.h instructions, the same cross-wave maximum), write the
+// codes straight into the LDS staging and keep the row scale in a register. The row's loads are
+// issued before the weight loads, so the quantizer's work overlaps their flight, and the linear is
+// one launch instead of two with the same codes, scale and output bits.
 #include "mq_device.h"
 #include "mq_internal.h"
+#include "mq_rotate.h"
 
 namespace mq {
 namespace {
@@ -52,8 +60,11 @@ __device__ __forceinline__ int row16_sum(int v) {
 
 // One row (the adaLN modulation linear, M = 1) is built for five waves per SIMD: 1280 resident
 // workgroups, so config 1's N = 18432 (1152 workgroups) runs in one wave of workgroups.
-template <WKind WK, Epi EPI, int AM, int MR>
+// FQ: 0 = int8 / int4 codes from qa and sa; else the row from x, rotated and quantized in the
+// prologue to int8 codes (1), int4 codes one per byte (2) or the x16 alternating layout (3).
+template <WKind WK, Epi EPI, int AM, int MR, int FQ = 0>
 __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(GemmArgs a) {
+    static_assert(FQ == 0 || MR == 1, "the fused quantizer serves one row");
     constexpr bool kPacked = WK != WKind::I8;
     constexpr int kChunkK = kPacked ? 32 : 16;          // K values per 16-byte weight chunk
     constexpr int kH = kPacked ? 6 : 12;                // chunks a lane holds in registers at once
@@ -83,33 +94,62 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
     // stored).
     constexpr int kStage = 2;                           // activation blocks per thread loaded up front
     uint4 xs[MR][kStage];
+    // FQ: this lane's 16 input values (the rotate+quantize kernel's layout with four waves per row:
+    // wave w takes columns 1024 w .. 1024 w + 1023, lane L the 16 of segment (L >> 2) + 16 (L & 3));
+    // lanes past K load the row's first columns, whose values are left out and never stored
+    [[maybe_unused]] uint4 xv[4];
+    [[maybe_unused]] const int e0 = wave * 1024 + 16 * ((lane >> 2) + 16 * (lane & 3));
+    if constexpr (FQ != 0) {
+        const int e = e0 < K ? e0 : 0;
+        if (a.x_dtype == kDtF32) {
+            const float* xr = static_cast<const float*>(a.x) + e;
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
-#pragma unroll
-        for (int it = 0; it < kStage; ++it) {
-            const int bl = tid + it * 64 * kWaves;
-            const int64_t mr = m < a.M ? m : a.M - 1;
-            xs[m][it] = *reinterpret_cast<const uint4*>(a.qa + mr * a.lda + 16 * (bl < blocks ? bl : 0));
+            for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const uint4*>(xr + 4 * j);
+        } else {
+            const uint16_t* xr = static_cast<const uint16_t*>(a.x) + e;
+            xv[0] = *reinterpret_cast<const uint4*>(xr);
+            xv[1] = *reinterpret_cast<const uint4*>(xr + 8);   // (xv[2], xv[3]: fp32 rows only)
         }
+    } else {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int it = 0; it < kStage; ++it) {
+                const int bl = tid + it * 64 * kWaves;
+                const int64_t mr = m < a.M ? m : a.M - 1;
+                xs[m][it] = *reinterpret_cast<const uint4*>(a.qa + mr * a.lda + 16 * (bl < blocks ? bl : 0));
+            }
+    }
     __builtin_amdgcn_sched_barrier(0);   // keep the activation loads ahead of the weight loads
 
-    // chunks c0 + 16 h, h < kH, of this lane: weights, zero-point byte, fp16 scale
+    // chunks c0 + 16 h, h0 <= h < h1, of this lane: weights (lw), zero-point byte and fp16 scale (lz)
     uint4 w[kH];
     uint32_t zb[kH], sb[kH];
-    auto load_chunks = [&](int c0) {
+    auto load_chunks = [&](int c0, int h0, int h1, bool lw, bool lz) {
 #pragma unroll
         for (int h = 0; h < kH; ++h) {
+            if (h < h0 || h >= h1) continue;
             const int c = min(c0 + 16 * h, nch - 1);
             const int g = c * kChunkK / 64;
-            w[h] = *reinterpret_cast<const uint4*>(wrow + (wt ? (c >> 2) * 1024 + (c & 3) * 16
-                                                                 : 16 * static_cast<int64_t>(c)));
-            zb[h] = 0u;
-            sb[h] = 0u;
-            if constexpr (WK == WKind::U4Asym) zb[h] = a.wz[nc * a.ldwz + (g >> 1)];
-            if constexpr (EPI == Epi::GroupScale) sb[h] = a.ws16[nc * a.ldws + g];
+            if (lw)
+                w[h] = *reinterpret_cast<const uint4*>(wrow + (wt ? (c >> 2) * 1024 + (c & 3) * 16
+                                                                     : 16 * static_cast<int64_t>(c)));
+            if (lz) {
+                zb[h] = 0u;
+                sb[h] = 0u;
+                if constexpr (WK == WKind::U4Asym) zb[h] = a.wz[nc * a.ldwz + (g >> 1)];
+                if constexpr (EPI == Epi::GroupScale) sb[h] = a.ws16[nc * a.ldws + g];
+            }
         }
     };
-    load_chunks(sub);
+    // FQ: the first kPre weight chunks go out before the row's quantizer runs, the rest of the
+    // round and the zero-points and scales after it, so that the registers of the loads in flight
+    // leave the quantizer the ones it needs (a spill there would first wait for every load)
+    constexpr int kPre = FQ == 0 ? kH : (kPacked ? kH : 8);
+    // chunks whose zero-points and scales go out before it (as many as leave no spill)
+    constexpr int kPreZ = FQ == 0 ? kH : WK == WKind::U4Asym ? 2 : 3;
+    load_chunks(sub, 0, kPreZ, true, true);
+    load_chunks(sub, kPreZ, kPre, true, false);
     __builtin_amdgcn_sched_barrier(0);
 
     // Stage block bl of row m (de-interleaved per 8 values for 4-bit weights): packed weights put
@@ -133,16 +173,76 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
             bsum[m * blocks + bl] = sm;
         }
     };
+    [[maybe_unused]] float s_row = 0.0f;   // FQ: the row's scale
+    if constexpr (FQ != 0) {
+        // rotate_chunk_lds / rotate_chunk of the Hadamard block, the row's absmax over the four
+        // waves, the division-free scale and quant16, in the rotate+quantize kernel's order
+        constexpr int LIMIT = FQ == 1 ? 127 : 7;
+        __shared__ __attribute__((aligned(16))) float tr_lds[kWaves * kTrWave];
+        __shared__ float red_lds[kWaves];
+        float* tb = tr_lds + wave * kTrWave + (lane & 3) * kTrG;
+        const LdsTranspose tr{tb + (lane >> 2), tb + (lane >> 2) * kTrS};
+        float v[16];
+        if (a.x_dtype == kDtF32) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
+            for (int j = 0; j < 4; ++j) {
+                v[4 * j] = __uint_as_float(xv[j].x);
+                v[4 * j + 1] = __uint_as_float(xv[j].y);
+                v[4 * j + 2] = __uint_as_float(xv[j].z);
+                v[4 * j + 3] = __uint_as_float(xv[j].w);
+            }
+        } else {
+            const uint32_t w16[8] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w};
+            const bool f16 = a.x_dtype == kDtF16;
 #pragma unroll
-        for (int it = 0; it < kStage; ++it) {
-            const int bl = tid + it * 64 * kWaves;
-            if (bl < blocks) stage(m, bl, xs[m][it]);
+            for (int j = 0; j < 8; ++j) {
+                v[2 * j] = f16 ? f16lo(w16[j]) : bf16lo(w16[j]);
+                v[2 * j + 1] = f16 ? f16hi(w16[j]) : bf16hi(w16[j]);
+            }
         }
-        // rows longer than kStage * 256 blocks: the rest block by block
-        for (int bl = tid + kStage * 64 * kWaves; bl < blocks; bl += 64 * kWaves)
-            stage(m, bl, *reinterpret_cast<const uint4*>(a.qa + (m < a.M ? m : a.M - 1) * a.lda + 16 * bl));
+        const int hb = a.hblock;
+        if (hb >= 16) {
+            stage_reg<0>(v);          // element stride 1  (c0 c1)
+            stage_reg<2>(v);          // element stride 4  (c2 c3)
+        }
+        if (hb >= 64) {
+            tr(v);                    // registers now hold c4..c7
+            stage_reg<0>(v);          // element stride 16 (c4 c5)
+            if (hb >= 256) stage_reg<2>(v);   // element stride 64 (c6 c7)
+            tr(v);                    // back to the load layout
+        }
+        float amc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) amc = __builtin_fmaxf(amc, __builtin_fabsf(v[j]));
+        float am = __builtin_fmaxf(0.0f, e0 < K ? amc : 0.0f);
+        am = wave_max_nonneg(am);
+        if (lane == 0) red_lds[wave] = am;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) am = __builtin_fmaxf(am, red_lds[i]);
+        const float s = __builtin_fmaxf(div_limit<LIMIT>(am), 1e-10f);
+        const float r = recip_row(s);
+        // the x16 layout negates odd 64-column groups: column bit 6 is lane bit 4 here
+        const float sg = FQ == 3 && ((lane >> 4) & 1) ? -1.0f : 1.0f;
+        uint32_t word[4];
+#pragma unroll
+        for (int hi = 0; hi < 4; ++hi) word[hi] = quant4_word<LIMIT, FQ == 3>(v + 4 * hi, sg, r, s);
+        if (e0 < K) stage(0, e0 >> 4, make_uint4(word[0], word[1], word[2], word[3]));
+        s_row = s;
+        load_chunks(sub, kPre, kH, true, false);
+        load_chunks(sub, kPreZ, kH, false, true);
+    } else {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+#pragma unroll
+            for (int it = 0; it < kStage; ++it) {
+                const int bl = tid + it * 64 * kWaves;
+                if (bl < blocks) stage(m, bl, xs[m][it]);
+            }
+            // rows longer than kStage * 256 blocks: the rest block by block
+            for (int bl = tid + kStage * 64 * kWaves; bl < blocks; bl += 64 * kWaves)
+                stage(m, bl, *reinterpret_cast<const uint4*>(a.qa + (m < a.M ? m : a.M - 1) * a.lda + 16 * bl));
+        }
     }
     __syncthreads();
 
@@ -154,7 +254,7 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
         acci[m] = 0;
     }
     for (int c0 = sub; c0 < nch; c0 += 16 * kH) {
-        if (c0 != sub) load_chunks(c0);
+        if (c0 != sub) load_chunks(c0, 0, kH, true, true);
 #pragma unroll
         for (int h = 0; h < kH; ++h) {
             const int c = c0 + 16 * h;
@@ -220,7 +320,7 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
         float t;
         if constexpr (EPI == Epi::GroupScale) {
             const float v = row16_sum(accf[m]);
-            t = m < a.M ? v * a.sa[m] : 0.0f;
+            t = m < a.M ? v * (FQ != 0 ? s_row : a.sa[m]) : 0.0f;
         } else {
             int v = row16_sum(acci[m]);
             if constexpr (WK == WKind::I4Sym) v >>= 4;   // exact: a multiple of 16
@@ -228,7 +328,7 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
                 if (sub == 0 && m < a.M && col_ok) a.part[m * a.N + n] = v;
                 continue;
             }
-            t = m < a.M && col_ok ? static_cast<float>(v) * a.sa[m] * a.ws32[n] : 0.0f;
+            t = m < a.M && col_ok ? static_cast<float>(v) * (FQ != 0 ? s_row : a.sa[m]) * a.ws32[n] : 0.0f;
         }
         if (sub == 0 && m < a.M && col_ok) {
             if (a.bias) t += load_as_f32(a.bias, a.bias_dtype, n);
@@ -237,14 +337,14 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
     }
 }
 
-template <WKind WK, Epi EPI, int AM>
+template <WKind WK, Epi EPI, int AM, int FQ = 0>
 int launch_rows(const GemmArgs& a, hipStream_t stream) {
     const int64_t cols = kWaves * kCols;
     const dim3 grid(static_cast<unsigned>((a.N + cols - 1) / cols));
 #define MQ_GV(MR)                                                                                       \
     do {                                                                                                \
         const size_t lds = MR * (a.K / 16) * (16 + (WK == WKind::U4Asym ? 4 : 0));                     \
-        auto kern = gemv_kernel<WK, EPI, AM, MR>;                                                       \
+        auto kern = gemv_kernel<WK, EPI, AM, MR, FQ>;                                                   \
         if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),                     \
                                                hipFuncAttributeMaxDynamicSharedMemorySize,              \
                                                static_cast<int>(lds)) != hipSuccess) {                  \
@@ -254,11 +354,15 @@ int launch_rows(const GemmArgs& a, hipStream_t stream) {
         hipLaunchKernelGGL(kern, grid, dim3(64 * kWaves), lds, stream, a);                              \
         return launch_status("gemv");                                                                   \
     } while (0)
-    switch (a.M) {
-        case 1: MQ_GV(1);
-        case 2: MQ_GV(2);
-        case 3: MQ_GV(3);
-        default: MQ_GV(4);
+    if constexpr (FQ != 0) {
+        MQ_GV(1);
+    } else {
+        switch (a.M) {
+            case 1: MQ_GV(1);
+            case 2: MQ_GV(2);
+            case 3: MQ_GV(3);
+            default: MQ_GV(4);
+        }
     }
 #undef MQ_GV
 }
@@ -272,6 +376,28 @@ int launch_am(const GemmArgs& a, hipStream_t stream) {
 }  // namespace
 
 int launch_gemv(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream) {
+    if (a.x) {   // a one-row whole linear: the GEMV quantizes the row itself (gemv_quantizes_row)
+        if (a.M != 1 || a.K > 4096) {
+            set_error("gemv: the fused row quantizer takes one row of K <= 4096");
+            return -2;
+        }
+        if (epi == Epi::GroupScale && a.act_mode == 2) {   // int4 codes, x16 alternating layout
+            if (wk == WKind::U4Asym) return launch_rows<WKind::U4Asym, Epi::GroupScale, 2, 3>(a, stream);
+            if (wk == WKind::I4Sym) return launch_rows<WKind::I4Sym, Epi::GroupScale, 2, 3>(a, stream);
+        } else if (epi == Epi::GroupScale && a.act_mode == 0 && a.x_bits == 8) {
+            if (wk == WKind::U4Asym) return launch_rows<WKind::U4Asym, Epi::GroupScale, 0, 1>(a, stream);
+            if (wk == WKind::I4Sym) return launch_rows<WKind::I4Sym, Epi::GroupScale, 0, 1>(a, stream);
+        } else if (epi == Epi::RowScale) {
+            if (wk == WKind::I8)
+                return a.x_bits == 4 ? launch_rows<WKind::I8, Epi::RowScale, 0, 2>(a, stream)
+                                     : launch_rows<WKind::I8, Epi::RowScale, 0, 1>(a, stream);
+            if (wk == WKind::I4Sym)
+                return a.x_bits == 4 ? launch_rows<WKind::I4Sym, Epi::RowScale, 0, 2>(a, stream)
+                                     : launch_rows<WKind::I4Sym, Epi::RowScale, 0, 1>(a, stream);
+        }
+        set_error("gemv: unsupported fused row quantizer combination");
+        return -2;
+    }
     if (epi == Epi::GroupScale) {
         if (wk == WKind::U4Asym) return launch_am<WKind::U4Asym, Epi::GroupScale>(a, stream);
         if (wk == WKind::I4Sym) return launch_am<WKind::I4Sym, Epi::GroupScale>(a, stream);

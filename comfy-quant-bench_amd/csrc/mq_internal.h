@@ -102,6 +102,12 @@ struct GemmArgs {
     // activation codes (qa) in the same 16-row tiles, [ceil(M / 16)][K / 64][16][64] (lda = K):
     // written so by the whole-linear entries when the wide kernel runs their product
     int atile = 0;
+    // One-row whole linears (gemv_quantizes_row): the GEMV rotates and quantizes the activation
+    // row x (x_dtype, Hadamard block hblock, x_bits-bit codes) itself instead of reading qa / sa
+    const void* x = nullptr;
+    int x_dtype = 0;
+    int hblock = 0;
+    int x_bits = 8;
 };
 
 // Output tile of the wide kernel for an M x N product (a tile code as above): 128 when 256 x 256
@@ -140,6 +146,10 @@ bool gemm_runs_wide(const GemmArgs& a, WKind wk, Epi epi);
 
 // M <= 4 rows, GroupScale / RowScale only (mq_gemv.hip).
 int launch_gemv(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream);
+// Whether a whole linear of these operands can hand its activation row to the GEMV (one row,
+// K <= 4096, a scaled epilogue): the GEMV then rotates and quantizes the row in its prologue with
+// the rotate+quantize kernel's arithmetic, in the same launch.
+bool gemv_quantizes_row(const GemmArgs& a, WKind wk, Epi epi);
 
 // 256 x 256-tile kernel for large M (mq_gemm_wide.hip).
 int launch_gemm_wide(const GemmArgs& a, WKind wk, Epi epi, hipStream_t stream);

@@ -334,6 +334,9 @@ int mq_gemm_rowscale_acc(const int8_t* qa, int64_t lda, const void* qw, int64_t 
  * Whole linears: rotate + quantize x (or the SwiGLU pair h), then the GEMM, in one call. The
  * activation codes and scales live in the caller's workspace; the kernels, arithmetic and results
  * are those of mq_rotquant / mq_swiglu_rotquant followed by mq_gemm_w4_group_ws / mq_gemm_rowscale_ws.
+ * One row (M = 1, K <= 4096, swiglu = MQ_SWIGLU_NONE) runs as one launch: the GEMV rotates and
+ * quantizes the row itself with the same arithmetic (same codes, scale and output bits) and leaves
+ * the workspace unwritten; it is still required and checked.
  *
  * mq_linear_w4_group replaces w4a8_int8_linear (configs' uint4 asymmetric scheme, act_bits 8,
  * tools/test_verify_formats.py:375-383) and convrot_w4a4_linear with per-group fp16 weight scales
