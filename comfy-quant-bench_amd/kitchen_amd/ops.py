@@ -62,6 +62,10 @@ def _bias(bias, n: int, device):
     """The bias on the device in its own floating-point type (bf16, fp16 or fp32), or None."""
     if bias is None:
         return None
+    # already a contiguous [N] device vector of a float type: used as it is (no new tensor per call)
+    if bias.dim() == 1 and bias.shape[0] == n and bias.device == device and bias.dtype in FLOAT_TYPES \
+            and bias.stride(0) == 1:
+        return bias
     if bias.numel() != n:
         raise ValueError(f"bias has {bias.numel()} elements, expected {n}")
     if bias.dtype not in FLOAT_TYPES:
