@@ -197,12 +197,38 @@ def measure_gemv(x, settle_ms: float, launches: int = 40) -> dict:
     ms = time_launches(graph.replay, 5, settle_ms=settle_ms) / launches
     nbytes = gemv_bytes(k)
     gbps = nbytes / (ms * 1e-3) / 1e9
+    del graph
+
+    # the whole one-row linear on the same weights (bf16 row in; the GEMV rotates and quantizes it
+    # in its own prologue, one launch), timed the same way
+    xrow = x[:1]
+
+    def linear_calls():
+        for i in range(launches):
+            qd, s16, zp = copies[i % GEMV_COPIES]
+            ck.w4a8_int8_linear(xrow, qd, s16, None, None, zp, bias)
+
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        linear_calls()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        linear_calls()
+    ms_lin = time_launches(graph.replay, 5, settle_ms=settle_ms) / launches
+    lin_bytes = nbytes - k - 4 + 2 * k                # the bf16 row in place of its codes and scale
     del graph, copies
     torch.cuda.empty_cache()
     return {"bound": "hbm", "kernel": "gemv_kernel<U4Asym,GroupScale,0,1>", "M": 1, "K": k, "N": GEMV_N,
             "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
             "bytes_per_launch": nbytes, "avg_launch_ms": round(ms, 5), "weight_copies": GEMV_COPIES,
-            "timing": f"HIP graph of {launches} launches over {GEMV_COPIES} weight copies, per launch"}
+            "timing": f"HIP graph of {launches} launches over {GEMV_COPIES} weight copies, per launch",
+            "whole_linear": {"kernel": "gemv_kernel<U4Asym,GroupScale,0,1,FQ=1> (the row rotated and quantized "
+                                       "in the GEMV's prologue)",
+                             "avg_launch_ms": round(ms_lin, 5), "bytes_per_launch": lin_bytes,
+                             "achieved": round(lin_bytes / (ms_lin * 1e-3) / 1e9, 1),
+                             "frac": round(lin_bytes / (ms_lin * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}}
 
 
 def gemv_i8_inputs(x, k: int):
