@@ -176,7 +176,8 @@ __global__ void __launch_bounds__(64 * kWaves, MR == 1 ? 5 : 4) gemv_kernel(Gemm
     [[maybe_unused]] float s_row = 0.0f;   // FQ: the row's scale
     if constexpr (FQ != 0) {
         // rotate_chunk_lds / rotate_chunk of the Hadamard block, the row's absmax over the four
-        // waves, the division-free scale and quant16, in the rotate+quantize kernel's order
+        // waves, the division-free scale and quant16's arithmetic (quant4_word, four values at a
+        // time), in the rotate+quantize kernel's order
         constexpr int LIMIT = FQ == 1 ? 127 : 7;
         __shared__ __attribute__((aligned(16))) float tr_lds[kWaves * kTrWave];
         __shared__ float red_lds[kWaves];
