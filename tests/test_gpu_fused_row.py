@@ -110,3 +110,18 @@ def test_public_ops_one_token(gpu_device):
     torch.cuda.synchronize()
     assert y1.shape == (1, 1, n)
     assert torch.equal(y1.reshape(1, n), y2[:1])
+
+
+@pytest.mark.parametrize("bias_kind", ["none", "f32", "f16"])
+def test_row_bias_types(gpu_device, bias_kind):
+    """No bias, and biases of other floating-point types than the output's."""
+    n, k = 777, 3072
+    print(f"[fused-row] bias {bias_kind}", flush=True)
+    qw, s16, zp, bias = _group_weights(n, k, gpu_device, True, seed=21)
+    b = None if bias_kind == "none" else bias.to(torch.float32 if bias_kind == "f32" else torch.float16)
+    x = _row(k, gpu_device, torch.float16, "rand", seed=21)
+    y1 = ops._linear_w4_group(x, 0, 256, 8, qw, s16, zp, b, n, k, torch.bfloat16)
+    qa, sa = ops.rotate_quantize(x, 256, 8)
+    y2 = ops.gemm_w4_group(qa, sa, qw, s16, zp, b, n)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
