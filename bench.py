@@ -40,6 +40,10 @@ for _p in (REPO, os.path.join(REPO, "comfy-quant-bench_amd")):
 METRIC = "int8-MFMA TOPS & % peak for W4A8/W4A4 linear (rot+quant+GEMM), M=4096"
 INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, 5.0 POPS
 HBM_PEAK_GBPS = 8000.0       # MI355X HBM3E, 8 TB/s
+# Measured on MI355X by a standalone gfx950 probe: v_mfma_i32_16x16x64_i8 on random int8 register
+# operands, 8 waves per SIMD, each MFMA followed by the four fp32 fmas of a per-group scale step, no
+# memory traffic (2109 TOPS; 4042 without the fmas). Reported beside the spec peak, not instead of it.
+GROUP_SCALE_CEILING_TOPS = 2109.0
 RQ_M = 32760                 # video-token shape of the rotate+quantize roofline (302 MB, above the MALL)
 COPY_BYTES = 256 << 20       # calibration copy for the traffic counters
 GEMM_KERNEL = "gemm_wide_kernel"
@@ -681,7 +685,11 @@ def main() -> int:
                      "weights": "the uint4 codes and zero-points as stored, expanded once per weight to int8 "
                                 "(q - z, negated in odd K groups) in 16-row tiles, which the GEMM reads; "
                                 "the same bits as the packed weights' GEMM",
-                     "packed_weights_avg_launch_ms": round(ms_gemm_packed, 5)},
+                     "packed_weights_avg_launch_ms": round(ms_gemm_packed, 5),
+                     "measured_ceiling": {"tops": GROUP_SCALE_CEILING_TOPS,
+                                          "frac": round(gemm_tops / GROUP_SCALE_CEILING_TOPS, 4),
+                                          "what": "int8 MFMA + 4 fp32 group-scale fmas per MFMA, random int8 "
+                                                  "operands, no memory traffic (gfx950 probe)"}},
         "rotquant_roofline": {"bound": "hbm", "kernel": "rotquant_kernel<256,int8,3>", "M": RQ_M, "K": k,
                               "achieved": round(rq_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                               "frac": round(rq_gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": rq_bytes,
