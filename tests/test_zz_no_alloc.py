@@ -59,8 +59,9 @@ def test_noalloc_equals_workspace_entry_point(gpu_device, act_bits):
         qd, zp = qd.view(torch.uint8), None
     bias = torch.randn(n, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(gpu_device)
     # M = 256 runs the split-K path through the scratch's partials region; M = 64 (smaller, second)
-    # the 128-tile kernel with only codes and scales in the scratch
-    for m in (256, 64):
+    # the 128-tile kernel with only codes and scales in the scratch; M = 1 the one-launch GEMV that
+    # quantizes its row itself (the scratch is not written)
+    for m in (256, 64, 1):
         print(f"[noalloc] act_bits={act_bits} M={m} N={n} K={k}", flush=True)
         x = synth.to_bf16_tensor(synth.activations(m, k, seed=m), gpu_device)
         y0 = torch.empty((m, n), dtype=torch.bfloat16, device=gpu_device)
