@@ -218,6 +218,29 @@ def test_linear_validation_rejects_before_launch(lib):
     assert "act_bits" in _err(lib)
 
 
+def test_one_row_linear_validation_rejects_before_launch(lib):
+    # M = 1: the GEMV quantizes the row itself, and the rotate+quantize entry's checks still run first
+    a = 1 << 20
+    need = lib.mq_linear_workspace_bytes(1, 1024, 3072)
+    assert need >= 16 * 3072 + 4
+    args = [a, 0, 3072, 256, 8, 0, a, 1536, a, 48, None, 0, None, 0, a, 0, 1024, 1, 1024, 3072, a, need, None]
+    names = ["x", "x_dtype", "ldx", "hblock", "act_bits", "swiglu", "qw", "ldw", "ws", "ldws", "wz", "ldwz",
+             "bias", "bias_dtype", "y", "y_dtype", "ldy", "M", "N", "K", "workspace", "workspace_bytes", "stream"]
+
+    def call(**kw):
+        v = dict(zip(names, args))
+        v.update(kw)
+        return lib.mq_linear_w4_group(*[v[n] for n in names])
+
+    assert call(hblock=128) == -1 and "group size" in _err(lib)
+    assert call(x=a + 2) == -1 and "16-byte" in _err(lib)
+    assert call(x_dtype=7) == -1 and "input type" in _err(lib)
+    assert call(workspace=None) == -1 and "workspace" in _err(lib)
+    assert lib.mq_linear_rowscale(a, 0, 3072, 128, 8, 0, a, 3072, 8, a, None, 0, a, 0, 1024, 1, 1024, 3072, a,
+                                  need, None) == -1
+    assert "group size" in _err(lib)
+
+
 def test_expanded_w4_validation(lib):
     # 4-bit weights expanded to int8 tiles: layouts 0 (int8 codes), 2 (x16 int4 codes), 3 (row scale)
     a = 1 << 20
